@@ -1,0 +1,100 @@
+"""In-tree build of the native libraries (no setuptools, no hipify).
+
+Outputs, all under ``attention_amd/lib``:
+
+* ``libqd_attention.so``        — gfx950 HIP kernels + the C ABI of
+  ``include/qd_attention.h`` (hipcc, device code for gfx950 only).
+* ``libqd_attention_torch.so``  — thin PyTorch-ROCm op registration
+  (host C++ against torch's headers), linked to the library above.
+
+The reference builds one ``CUDAExtension`` (reference ``setup.py:9-27``);
+here hipcc compiles the HIP source directly so nothing is hipified.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "attention_amd")
+CSRC = os.path.join(PKG, "csrc")
+LIB_DIR = os.path.join(PKG, "lib")
+INCLUDE = os.path.join(ROOT, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+HIP_LIB = os.path.join(LIB_DIR, "libqd_attention.so")
+TORCH_LIB = os.path.join(LIB_DIR, "libqd_attention_torch.so")
+
+# Packed-fp32 VALU forms are disabled for every HIP compile.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    path = os.path.join(ROCM, "bin", "hipcc")
+    return path if os.path.exists(path) else (shutil.which("hipcc") or "hipcc")
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(line for line in res.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out, flush=True)
+
+
+def hip_library_cmd() -> list[str]:
+    return [_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
+            os.path.join(CSRC, "gqa_decode.hip"),
+            "-o", HIP_LIB + ".tmp", f"-Wl,-rpath,{ROCM}/lib"]
+
+
+def torch_binding_cmd() -> list[str]:
+    import torch  # noqa: F401  (paths only)
+    from torch.utils.cpp_extension import include_paths, library_paths
+
+    abi = int(getattr(__import__("torch")._C, "_GLIBCXX_USE_CXX11_ABI", True))
+    incs = [f"-I{p}" for p in include_paths()] + [f"-I{INCLUDE}", f"-I{ROCM}/include"]
+    torch_lib = library_paths()[0]
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            *incs, os.path.join(CSRC, "torch_ops.cpp"),
+            "-o", TORCH_LIB + ".tmp",
+            f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-lamdhip64",
+            f"-L{LIB_DIR}", "-l:libqd_attention.so",
+            "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+
+
+def build(verbose: bool = False) -> None:
+    """Compile both libraries (always; no up-to-date check)."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    _run(hip_library_cmd(), verbose)
+    os.replace(HIP_LIB + ".tmp", HIP_LIB)
+    _run(torch_binding_cmd(), verbose)
+    os.replace(TORCH_LIB + ".tmp", TORCH_LIB)
+
+
+def build_parallel(extra: list[list[str]] | None = None, verbose: bool = False) -> None:
+    """Build the libraries and any extra independent commands concurrently."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        futs = [ex.submit(build, verbose)]
+        for cmd in extra or []:
+            futs.append(ex.submit(_run, cmd, verbose))
+        for f in futs:
+            f.result()
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print("built", HIP_LIB, TORCH_LIB)

@@ -1,0 +1,117 @@
+"""ctypes binding of the C ABI in include/qd_attention.h.
+
+For Python callers that want the C entry points without the torch op layer
+(explicit split/chunk plans, kernel choice, caller-owned output and
+workspace), and the same stub a ctypes user of the reference would add.
+``launch`` takes torch device tensors and enqueues on the current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import torch  # noqa: F401  (loads torch's HIP runtime before the library)
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+HEADER = os.path.join(os.path.dirname(PKG), "include", "qd_attention.h")
+LIB_PATH = os.path.join(PKG, "lib", "libqd_attention.so")
+
+DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.int32: 3}
+QD_FLAG_FORCE_GENERIC = 1
+
+
+class TensorDesc(ctypes.Structure):
+    _fields_ = [("defined", ctypes.c_int32), ("is_device", ctypes.c_int32),
+                ("device_index", ctypes.c_int32), ("contiguous", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("sizes", ctypes.c_int64 * 8)]
+
+
+def desc(sizes, dtype=0, is_device=1, device=0, contiguous=1, defined=1) -> TensorDesc:
+    d = TensorDesc()
+    d.defined, d.is_device, d.device_index, d.contiguous, d.dtype = (
+        defined, is_device, device, contiguous, dtype)
+    d.ndim = len(sizes)
+    for i, s in enumerate(list(sizes)[:8]):
+        d.sizes[i] = s
+    return d
+
+
+def header_functions() -> list[str]:
+    text = open(HEADER).read()
+    return re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\*?\s+(qd_[a-z_0-9]+)\(", text, re.M)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.POINTER(TensorDesc)
+        L.qd_abi_version.restype = ctypes.c_int
+        L.qd_error_string.restype = ctypes.c_char_p
+        L.qd_error_string.argtypes = [ctypes.c_int]
+        L.qd_gqa_decode_validate.restype = ctypes.c_int
+        L.qd_gqa_decode_validate.argtypes = [P, P, P, P, P, ctypes.c_double, ctypes.c_int64,
+                                             ctypes.c_char_p, ctypes.c_size_t]
+        L.qd_gqa_decode_validate_workspace.restype = ctypes.c_int
+        L.qd_gqa_decode_validate_workspace.argtypes = [P, P, ctypes.c_int64, ctypes.c_char_p,
+                                                       ctypes.c_size_t]
+        L.qd_gqa_decode_plan.restype = ctypes.c_int
+        L.qd_gqa_decode_plan.argtypes = [ctypes.c_int] * 8 + [ctypes.POINTER(ctypes.c_int)] * 2
+        L.qd_gqa_decode_workspace_bytes.restype = ctypes.c_size_t
+        L.qd_gqa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 4
+        L.qd_gqa_decode_kernel_kind.restype = ctypes.c_int
+        L.qd_gqa_decode_kernel_kind.argtypes = [ctypes.c_int] * 6
+        L.qd_gqa_decode_launch.restype = ctypes.c_int
+        L.qd_gqa_decode_launch.argtypes = (
+            [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
+            + [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+               ctypes.c_void_p])
+        _lib = L
+    return _lib
+
+
+def validate(q, k, v, table, lens, scale=0.125, splits=1):
+    buf = ctypes.create_string_buffer(256)
+    rc = lib().qd_gqa_decode_validate(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v),
+                                      ctypes.byref(table), ctypes.byref(lens), scale, splits,
+                                      buf, 256)
+    return rc, buf.value.decode()
+
+
+def validate_workspace(q, ws, splits):
+    buf = ctypes.create_string_buffer(256)
+    rc = lib().qd_gqa_decode_validate_workspace(ctypes.byref(q), ctypes.byref(ws), splits, buf, 256)
+    return rc, buf.value.decode()
+
+
+def plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype=2, cu_count=256):
+    s, c = ctypes.c_int(), ctypes.c_int()
+    rc = lib().qd_gqa_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype,
+                                  cu_count, ctypes.byref(s), ctypes.byref(c))
+    assert rc == 0, lib().qd_error_string(rc)
+    return s.value, c.value
+
+
+def launch(q, k, v, table, lens, out, *, scale, splits=1, chunk_pages=0, workspace=None,
+           flags=0, stream=None):
+    """Calls qd_gqa_decode_launch on torch device tensors (no validation)."""
+    B, Hq, D = q.shape
+    _, P, Hkv, _ = k.shape
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else 0
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * 4 if workspace is not None else 0
+    rc = lib().qd_gqa_decode_launch(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), lens.data_ptr(),
+        out.data_ptr(), ws_ptr, ws_bytes, B, Hq, Hkv, D, P, table.shape[1], k.shape[0],
+        DTYPE[q.dtype], float(scale), splits, chunk_pages, flags, stream)
+    return rc
+
+
+def error_string(rc: int) -> str:
+    return lib().qd_error_string(rc).decode()

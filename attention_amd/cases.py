@@ -1,0 +1,135 @@
+"""Seeded synthetic decode inputs: the reference's recipe and the benchmark
+configurations.
+
+``make_decode_case`` follows reference ``benchmarks/data.py:8-43``: a CPU
+``torch.Generator`` seeded with ``seed``; fp32 ``randn`` for q, then k, then
+v; a ``randperm`` of the physical blocks so logical and physical page order
+differ; table entries at or beyond ``ceil(len/block_size)`` set to -1; cast
+to dtype/device last.  ``exact_pool=True`` sizes the pool to exactly the
+needed blocks (the benchmark configs), handing each sequence its slice of
+the permutation.  ``k_scale`` multiplies K before the cast (long-context
+config).  ``device_gen=True`` draws the tensors on the GPU instead (same
+shapes, metadata and lengths, different random values), for the multi-GB
+configs where CPU generation would dominate.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+
+def make_decode_case(*, lengths, q_heads=8, kv_heads=2, head_dim=64, block_size=16,
+                     dtype=torch.float32, device="cpu", seed=42, exact_pool=False,
+                     k_scale=1.0, device_gen=False):
+    """Returns ``(q, k_cache, v_cache, block_table, context_lens)``."""
+    assert lengths and all(x >= 0 for x in lengths)
+    assert q_heads % kv_heads == 0
+    bsz = len(lengths)
+    max_pages = max(1, math.ceil(max(lengths) / block_size))
+    used = [math.ceil(x / block_size) for x in lengths]
+    num_blocks = max(1, sum(used)) if exact_pool else bsz * max_pages
+    gen_dev = device if device_gen else "cpu"
+    gen = torch.Generator(device=gen_dev).manual_seed(seed)
+    q = torch.randn(bsz, q_heads, head_dim, generator=gen, dtype=torch.float32, device=gen_dev)
+    k = _randn_cast((num_blocks, block_size, kv_heads, head_dim), gen, gen_dev, dtype, k_scale)
+    v = _randn_cast((num_blocks, block_size, kv_heads, head_dim), gen, gen_dev, dtype, 1.0)
+    cpu_gen = gen if not device_gen else torch.Generator(device="cpu").manual_seed(seed)
+    order = torch.randperm(num_blocks, generator=cpu_gen, dtype=torch.int64)
+    if exact_pool:
+        table = torch.full((bsz, max_pages), -1, dtype=torch.int32)
+        offset = 0
+        for b, n in enumerate(used):
+            table[b, :n] = order[offset:offset + n].to(torch.int32)
+            offset += n
+    else:
+        table = order.view(bsz, max_pages).to(torch.int32)
+        for b, n in enumerate(used):
+            table[b, n:] = -1
+    return (
+        q.to(device=device, dtype=dtype).contiguous(),
+        k.to(device=device).contiguous(),
+        v.to(device=device).contiguous(),
+        table.to(device=device).contiguous(),
+        torch.tensor(lengths, dtype=torch.int32, device=device),
+    )
+
+
+def _randn_cast(shape, gen, gen_dev, dtype, scale):
+    """fp32 randn (times scale) cast to dtype, in slices to bound fp32 memory."""
+    out = torch.empty(shape, dtype=dtype, device=gen_dev)
+    flat = out.view(shape[0], -1)
+    step = max(1, (1 << 26) // max(1, flat.shape[1]))
+    for s in range(0, shape[0], step):
+        e = min(shape[0], s + step)
+        chunk = torch.randn((e - s, flat.shape[1]), generator=gen, dtype=torch.float32, device=gen_dev)
+        if scale != 1.0:
+            chunk.mul_(scale)
+        flat[s:e].copy_(chunk)
+    return out
+
+
+@dataclass(frozen=True)
+class DecodeConfig:
+    name: str
+    batch: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    block_size: int
+    dtype: torch.dtype
+    seed: int
+    len_range: tuple[int, int] | None = None
+    fixed_lengths: tuple[int, ...] | None = None
+    k_scale: float = 1.0
+    force_ones: int = 0
+    description: str = field(default="", compare=False)
+
+    def lengths(self) -> list[int]:
+        if self.fixed_lengths is not None:
+            return list(self.fixed_lengths)
+        lo, hi = self.len_range
+        gen = torch.Generator(device="cpu").manual_seed(10_000 + self.seed)
+        lens = torch.randint(lo, hi + 1, (self.batch,), generator=gen).tolist()
+        for i in range(self.force_ones):
+            lens[(i * self.batch) // max(1, self.force_ones)] = 1
+        return lens
+
+    def make(self, device="cpu", device_gen=False, lengths=None):
+        return make_decode_case(lengths=lengths or self.lengths(), q_heads=self.q_heads,
+                                kv_heads=self.kv_heads, head_dim=self.head_dim,
+                                block_size=self.block_size, dtype=self.dtype, device=device,
+                                seed=self.seed, exact_pool=True, k_scale=self.k_scale,
+                                device_gen=device_gen)
+
+
+CONFIGS: dict[str, DecodeConfig] = {
+    "cfg1": DecodeConfig("cfg1", 4, 8, 2, 64, 16, torch.float16, 42,
+                         fixed_lengths=(17, 100, 255, 512),
+                         description="reference CPU-path config, pool = the 57 needed blocks"),
+    "cfg2": DecodeConfig("cfg2", 32, 32, 8, 128, 16, torch.bfloat16, 1, len_range=(512, 4096),
+                         description="Qwen3-8B-shaped decode"),
+    "cfg3": DecodeConfig("cfg3", 64, 28, 4, 128, 16, torch.bfloat16, 2, len_range=(1, 8192),
+                         force_ones=2, description="Qwen2.5-7B-shaped ragged decode"),
+    "cfg4": DecodeConfig("cfg4", 8, 64, 8, 128, 16, torch.bfloat16, 3,
+                         len_range=(32768, 131072), k_scale=3.0,
+                         description="long-context split-K decode, K x3"),
+    "cfg5": DecodeConfig("cfg5", 256, 40, 8, 128, 32, torch.float16, 4, len_range=(128, 1024),
+                         description="high-batch short-context decode"),
+}
+
+
+def algorithmic_bytes(lengths, batch, q_heads, kv_heads, head_dim, block_size, elem_bytes) -> int:
+    """K+V of valid tokens + q + out + lengths + used table entries.
+
+    Excludes split partials, re-reads and padding slots.
+    """
+    toks = sum(max(0, int(x)) for x in lengths)
+    pages = sum(math.ceil(max(0, int(x)) / block_size) for x in lengths)
+    return (toks * 2 * kv_heads * head_dim * elem_bytes + 2 * batch * q_heads * head_dim * elem_bytes
+            + 4 * batch + 4 * pages)
+
+
+def algorithmic_flops(lengths, q_heads, head_dim) -> int:
+    return 4 * q_heads * head_dim * sum(max(0, int(x)) for x in lengths)

@@ -1,0 +1,902 @@
+// Paged grouped-query decode attention for MI355X (gfx950 / CDNA4).
+//
+// Three kernels and the C ABI declared in include/qd_attention.h:
+//
+//   decode_mfma_kernel     16-bit caches, head_dim 64/128/256, block_size a
+//                          multiple of 16, group size <= 16.  One wave64 per
+//                          (sequence, kv-head, context split).  Each 16-token
+//                          group is two MFMA passes: S^T = K.Q^T with
+//                          v_mfma_f32_16x16x32 (K rows feed the A operand
+//                          straight from 16-byte global loads), then
+//                          O^T += V^T.P^T with v_mfma_f32_16x16x16 (the QK
+//                          accumulator layout is already the B operand; V is
+//                          repacked in registers with v_perm_b32).  Softmax
+//                          state stays per lane in fp32.
+//   decode_generic_kernel  every other shape/dtype the reference accepts
+//                          (fp32, any head_dim in [1,256], any block_size,
+//                          any group size) on the VALU: 16 lanes per token
+//                          row, DPP row reductions.
+//   combine_kernel         log-sum-exp merge of split partials.
+//
+// Reference semantics followed (paths relative to the reference tree):
+//   kv-head map h / (Hq/Hkv)                    csrc/cuda/dense/gqa_decode.cu:31
+//   page/slot addressing, 64-bit offsets        csrc/cuda/dense/gqa_decode.cu:43-47
+//   zero output for empty rows                  csrc/cuda/dense/gqa_decode.cu:64-65
+//   partial layout [B,Hq,S,D+2] = {m, l, acc}   csrc/cuda/dense/gqa_decode.cu:66-69
+//   streaming softmax update / merge            csrc/cuda/common/online_softmax.cuh:10-24
+//   merge kernel output                         csrc/cuda/dense/gqa_decode.cu:74-87
+//
+// Splits cover whole pages (the reference splits the token range
+// [len*z/S, len*(z+1)/S), gqa_decode.cu:40-41); the merged result is the same
+// softmax, and page-aligned splits keep every 16-token group inside one page.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "qd_attention.h"
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ----------------------------------------------------------------------------
+// Element types
+// ----------------------------------------------------------------------------
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<QD_DTYPE_F32> {
+  using S = float;
+  __device__ static float to_f(S x) { return x; }
+  __device__ static S from_f(float x) { return x; }
+};
+template <>
+struct Elem<QD_DTYPE_F16> {
+  using S = _Float16;
+  __device__ static float to_f(S x) { return static_cast<float>(x); }
+  __device__ static S from_f(float x) { return static_cast<_Float16>(x); }  // RNE
+};
+template <>
+struct Elem<QD_DTYPE_BF16> {
+  using S = __bf16;
+  __device__ static float to_f(S x) { return static_cast<float>(x); }
+  __device__ static S from_f(float x) { return static_cast<__bf16>(x); }  // RNE
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+struct DecodeParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* table;
+  const int32_t* lens;
+  void* out;
+  float* ws;
+  int B, Hq, Hkv, D, P, maxP, g;
+  int splits;       // launched splits per (sequence, kv-head)
+  int chunk_pages;  // 0: ceil(npages / splits) per sequence, else fixed
+  int head_chunks;  // generic kernel: ceil(g / kGenericHeads)
+  int64_t num_blocks;
+  float sl2;  // scale * log2(e)
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Token range [tb, te) of split z and the number of non-empty splits of a
+// sequence.  Lengths are clamped to the table capacity max_pages*block_size
+// so that a length beyond the table never reads past the table row.
+struct ChunkInfo {
+  int tb, te, nch;
+};
+
+__device__ __forceinline__ ChunkInfo chunk_info(const DecodeParams& p, int len_raw, int z) {
+  ChunkInfo c{0, 0, 0};
+  const int64_t cap = static_cast<int64_t>(p.maxP) * p.P;
+  const int64_t len = len_raw < cap ? static_cast<int64_t>(len_raw) : cap;
+  if (len <= 0) return c;
+  const int64_t npages = (len + p.P - 1) / p.P;
+  const int64_t cp = p.chunk_pages > 0 ? p.chunk_pages : (npages + p.splits - 1) / p.splits;
+  int64_t nch = (npages + cp - 1) / cp;
+  if (nch > p.splits) nch = p.splits;
+  c.nch = static_cast<int>(nch);
+  const int64_t tb = static_cast<int64_t>(z) * cp * p.P;
+  int64_t te = tb + cp * p.P;
+  if (te > len) te = len;
+  c.tb = static_cast<int>(tb < len ? tb : len);
+  c.te = static_cast<int>(te);
+  return c;
+}
+
+__device__ __forceinline__ int clamp_page(int32_t phys, int64_t num_blocks) {
+  // Out-of-range page ids are caller errors (unchecked by the reference);
+  // clamping keeps every access inside the cache.
+  if (phys < 0) return 0;
+  if (phys >= num_blocks) return static_cast<int>(num_blocks - 1);
+  return phys;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each row of 16 lanes; every lane of the row gets the same bits.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_f<0x141>(x);  // row_half_mirror
+  x += dpp_f<0x140>(x);  // row_mirror
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// ----------------------------------------------------------------------------
+// Portable VALU kernel
+// ----------------------------------------------------------------------------
+
+constexpr int kGenericHeads = 8;
+
+// grid: (splits * head_chunks, Hkv, B), block 64.
+// Lane layout: row = lane/16 is one of 4 token slots, col = lane%16 owns
+// elements [col*EPL, col*EPL + EPL) of head_dim.  Each row keeps its own
+// streaming softmax state over the tokens it visits; rows are merged at the
+// end with the log-sum-exp rule.
+template <int DT, int EPL, bool FULL>
+__global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
+  using E = Elem<DT>;
+  using S = typename E::S;
+  constexpr int GH = kGenericHeads;
+  const int lane = threadIdx.x;
+  const int row = lane >> 4;
+  const int col = lane & 15;
+  const int e0 = col * EPL;
+  const int z = blockIdx.x % p.splits;
+  const int hc = blockIdx.x / p.splits;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int D = p.D;
+
+  const ChunkInfo ci = chunk_info(p, p.lens[b], z);
+  const bool direct = ci.nch <= 1;
+  if (z >= (ci.nch > 1 ? ci.nch : 1)) return;
+
+  const int h0 = kvh * p.g + hc * GH;
+  const int nh = min(GH, p.g - hc * GH);
+  const S* __restrict__ q = static_cast<const S*>(p.q);
+  const S* __restrict__ kc = static_cast<const S*>(p.k);
+  const S* __restrict__ vc = static_cast<const S*>(p.v);
+
+  float qf[GH][EPL];
+#pragma unroll
+  for (int h = 0; h < GH; ++h) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int d = e0 + e;
+      qf[h][e] = (h < nh && (FULL || d < D))
+                     ? E::to_f(q[(static_cast<int64_t>(b) * p.Hq + h0 + h) * D + d])
+                     : 0.f;
+    }
+  }
+
+  float m[GH], l[GH], acc[GH][EPL];
+#pragma unroll
+  for (int h = 0; h < GH; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[h][e] = 0.f;
+  }
+
+  const int64_t rs = static_cast<int64_t>(p.Hkv) * D;
+  const int32_t* __restrict__ trow = p.table + static_cast<int64_t>(b) * p.maxP;
+  for (int t0 = ci.tb; t0 < ci.te; t0 += 4) {
+    const int t = t0 + row;
+    const bool valid = t < ci.te;
+    const int tt = valid ? t : ci.te - 1;
+    const int page = tt / p.P;
+    const int slot = tt - page * p.P;
+    const int phys = clamp_page(trow[page], p.num_blocks);
+    const int64_t base = (static_cast<int64_t>(phys) * p.P + slot) * rs +
+                         static_cast<int64_t>(kvh) * D + e0;
+    float kf[EPL], vf[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const bool ok = FULL || (e0 + e < D);
+      kf[e] = ok ? E::to_f(kc[base + e]) : 0.f;
+      vf[e] = ok ? E::to_f(vc[base + e]) : 0.f;
+    }
+    float s[GH];
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) dot = fmaf(qf[h][e], kf[e], dot);
+      s[h] = row16_sum(dot);
+    }
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      const float x = valid ? s[h] * p.sl2 : -INFINITY;
+      const float mn = fmaxf(m[h], x);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = fast_exp2(m[h] - mref);
+      const float pr = fast_exp2(x - mref);
+      l[h] = fmaf(l[h], alpha, pr);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(acc[h][e], alpha, pr * vf[e]);
+      m[h] = mn;
+    }
+  }
+
+  // Merge the four token rows (xor 16, xor 32).
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      const float mo = __shfl_xor(m[h], off);
+      const float lo = __shfl_xor(l[h], off);
+      const float mn = fmaxf(m[h], mo);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float a = fast_exp2(m[h] - mref);
+      const float bb = fast_exp2(mo - mref);
+      l[h] = l[h] * a + lo * bb;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float ao = __shfl_xor(acc[h][e], off);
+        acc[h][e] = acc[h][e] * a + ao * bb;
+      }
+      m[h] = mn;
+    }
+  }
+
+  if (row != 0) return;
+  if (direct) {
+    S* __restrict__ out = static_cast<S*>(p.out);
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      if (h >= nh) break;
+      const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
+      const int64_t ob = (static_cast<int64_t>(b) * p.Hq + h0 + h) * D;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const int d = e0 + e;
+        if (FULL || d < D) out[ob + d] = E::from_f(l[h] > 0.f ? acc[h][e] * inv : 0.f);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      if (h >= nh) break;
+      float* w = p.ws + ((static_cast<int64_t>(b) * p.Hq + h0 + h) * p.splits + z) * (D + 2);
+      if (col == 0) {
+        w[0] = m[h] * kLn2;
+        w[1] = l[h];
+      }
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const int d = e0 + e;
+        if (FULL || d < D) w[2 + d] = acc[h][e];
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// MFMA kernel
+// ----------------------------------------------------------------------------
+
+template <int DT>
+struct MfmaOps;
+
+template <>
+struct MfmaOps<QD_DTYPE_BF16> {
+  __device__ static f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack2(float x, float y) {
+    const f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  }
+};
+
+template <>
+struct MfmaOps<QD_DTYPE_F16> {
+  __device__ static f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack2(float x, float y) {
+    const f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+};
+
+// V bytes one lane loads from one cache row: head_dim/16 elements.
+template <int D>
+struct VRow {
+  static constexpr int kElems = D / 16;
+  static constexpr int kWords = kElems / 2;  // 32-bit words
+  uint32_t w[kWords];
+};
+
+template <int D>
+__device__ __forceinline__ VRow<D> load_vrow(const char* ptr) {
+  VRow<D> r;
+  if constexpr (VRow<D>::kWords == 2) {
+    const u32x2 x = *reinterpret_cast<const u32x2*>(ptr);
+    r.w[0] = x[0];
+    r.w[1] = x[1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < VRow<D>::kWords / 4; ++i) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(ptr + 16 * i);
+      r.w[4 * i + 0] = x[0];
+      r.w[4 * i + 1] = x[1];
+      r.w[4 * i + 2] = x[2];
+      r.w[4 * i + 3] = x[3];
+    }
+  }
+  return r;
+}
+
+// Registers for one 16-token group in flight.
+template <int D>
+struct GroupBuf {
+  static constexpr int KC = D / 32;
+  u32x4 k[KC];     // K row (lane%16) at elements 32c + 8*(lane/16) .. +8
+  VRow<D> v[4];    // V rows 4*(lane/16)+i, elements (D/16)*(lane%16) ..
+  int tg;          // first token of the group
+};
+
+// grid: (splits, Hkv, B), block 64 (one wave per work item).
+//
+// Lane l, r16 = l % 16, q4 = l / 16:
+//   QK  A = K      lane holds K[token r16][8 elems]     (16x16x32 A layout)
+//       B = Q^T    lane holds Q[head  r16][same elems]
+//       C = S^T    lane holds S[token 4*q4+i][head r16], i = 0..3
+//   PV  A = V^T    lane holds V[token 4*q4+i][d = DV*r16 + j], i = 0..3
+//       B = P^T    lane holds P[head r16][token 4*q4+i]  == C layout of QK
+//       C = O^T    lane holds O[head r16][d = DV*(4*q4+i) + j]
+// so every lane owns one head's softmax state and a contiguous slice of
+// DV*4 output elements of that head.
+template <int D, int DT, int PF>
+__global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
+  using Ops = MfmaOps<DT>;
+  constexpr int KC = D / 32;
+  constexpr int DV = D / 16;
+  constexpr int VB = DV * 2;  // bytes per lane per V row
+  const int lane = threadIdx.x;
+  const int r16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int z = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+
+  const ChunkInfo ci = chunk_info(p, p.lens[b], z);
+  const bool direct = ci.nch <= 1;
+  if (z >= (ci.nch > 1 ? ci.nch : 1)) return;
+
+  const int g = p.g;
+  const int head = kvh * g + r16;
+  const bool head_ok = r16 < g;
+
+  u32x4 qv[KC];
+  {
+    const char* qp = static_cast<const char*>(p.q) +
+                     (static_cast<int64_t>(b) * p.Hq + (head_ok ? head : kvh * g)) * D * 2;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(qp + (32 * c + 8 * q4) * 2);
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      qv[c] = head_ok ? x : zero;
+    }
+  }
+
+  const int64_t row_bytes = static_cast<int64_t>(p.Hkv) * D * 2;
+  const int64_t page_bytes = row_bytes * p.P;
+  const char* kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh) * D * 2;
+  const char* vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh) * D * 2;
+  const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
+  const int32_t* trow = p.table + static_cast<int64_t>(b) * p.maxP;
+
+  const int ng = (ci.te - ci.tb + 15) >> 4;
+  const int page0 = ci.tb / p.P;  // tb is page aligned
+  // Table window: entry (page0 + wbase + lane) in lane, 64 pages at a time.
+  int wbase = 0;
+  int tblv = (lane < p.maxP - page0) ? trow[page0 + lane] : 0;
+
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  f32x4 acc[DV];
+#pragma unroll
+  for (int j = 0; j < DV; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](GroupBuf<D>& buf, int gi) {
+    const int tg = ci.tb + 16 * gi;
+    buf.tg = tg;
+    const int rel = tg - ci.tb;            // token offset from the page-aligned start
+    const int pl = rel / p.P;              // page within the split
+    const int row0 = rel - pl * p.P;       // first row inside the page
+    if (pl - wbase >= 64) {
+      wbase = pl & ~63;
+      tblv = (lane < p.maxP - page0 - wbase) ? trow[page0 + wbase + lane] : 0;
+    }
+    const int phys = clamp_page(__builtin_amdgcn_readlane(tblv, pl - wbase), p.num_blocks);
+    const int64_t off = static_cast<int64_t>(phys) * page_bytes + static_cast<int64_t>(row0) * row_bytes;
+    const char* kp = kbase + off;
+    const char* vp = vbase + off;
+    const int last = ci.te - 1 - tg;  // rows > last are past the end: reuse row `last`
+    const uint32_t rk = static_cast<uint32_t>(min(r16, last));
+    const uint32_t ko = rk * rb32 + 16u * q4;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) buf.k[c] = *reinterpret_cast<const u32x4*>(kp + ko + 64 * c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t rv = static_cast<uint32_t>(min(4 * q4 + i, last));
+      buf.v[i] = load_vrow<D>(vp + rv * rb32 + VB * r16);
+    }
+  };
+
+  auto compute = [&](const GroupBuf<D>& buf) {
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KC; ++c) s = Ops::qk(buf.k[c], qv[c], s);
+    const int last = ci.te - 1 - buf.tg;
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (4 * q4 + i <= last) ? s[i] : -INFINITY;
+    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m_run, mx * p.sl2);
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = fast_exp2(m_run - mref);
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(fmaf(x[i], p.sl2, -mref));
+    l_run = fmaf(l_run, alpha, (pr[0] + pr[1]) + (pr[2] + pr[3]));
+    m_run = mn;
+    if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int j = 0; j < DV; ++j) acc[j] *= alpha;
+    }
+    const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
+#pragma unroll
+    for (int j = 0; j < DV; ++j) {
+      const int w = j >> 1;
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      const u32x2 a = {__builtin_amdgcn_perm(buf.v[1].w[w], buf.v[0].w[w], sel),
+                       __builtin_amdgcn_perm(buf.v[3].w[w], buf.v[2].w[w], sel)};
+      acc[j] = Ops::pv(a, pb, acc[j]);
+    }
+  };
+
+  if (ng > 0) {
+    GroupBuf<D> buf[PF];
+#pragma unroll
+    for (int u = 0; u < PF - 1; ++u)
+      if (u < ng) issue(buf[u], u);
+    for (int gi = 0; gi < ng; gi += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int nxt = gi + u + PF - 1;
+        if (nxt < ng) issue(buf[(u + PF - 1) % PF], nxt);
+        if (gi + u < ng) compute(buf[u]);
+      }
+    }
+  }
+
+  // Per-lane partial sums of l cover this lane's 4 tokens of every group.
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+
+  if (!head_ok) return;
+  if (direct) {
+    using S = typename Elem<DT>::S;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + head) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t wv[DV / 2];
+#pragma unroll
+      for (int j = 0; j < DV; j += 2)
+        wv[j / 2] = Ops::pack2(l_tot > 0.f ? acc[j][i] * inv : 0.f,
+                               l_tot > 0.f ? acc[j + 1][i] * inv : 0.f);
+      char* dst = reinterpret_cast<char*>(o + DV * (4 * q4 + i));
+      if constexpr (DV / 2 == 2) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
+      } else {
+#pragma unroll
+        for (int t = 0; t < DV / 8; ++t)
+          *reinterpret_cast<u32x4*>(dst + 16 * t) =
+              u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+      }
+    }
+  } else {
+    float* w = p.ws + ((static_cast<int64_t>(b) * p.Hq + head) * p.splits + z) * (D + 2);
+    if (q4 == 0) {
+      w[0] = m_run * kLn2;
+      w[1] = l_tot;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float* dst = w + 2 + DV * (4 * q4 + i);
+#pragma unroll
+      for (int j = 0; j < DV; j += 2)
+        *reinterpret_cast<f32x2*>(dst + j) = f32x2{acc[j][i], acc[j + 1][i]};
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Combine kernel: grid (Hq, B), block 64.
+// ----------------------------------------------------------------------------
+
+template <int DT>
+__global__ __launch_bounds__(64) void combine_kernel(DecodeParams p) {
+  using E = Elem<DT>;
+  using S = typename E::S;
+  const int lane = threadIdx.x;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const ChunkInfo ci = chunk_info(p, p.lens[b], 0);
+  const int nch = ci.nch;
+  if (nch <= 1) return;  // written directly by the decode kernel
+  const int D = p.D;
+  const int stride = D + 2;
+  const float* base = p.ws + (static_cast<int64_t>(b) * p.Hq + h) * p.splits * stride;
+
+  // Pass 1: global max over non-empty partials (online_softmax.cuh:18 skips l == 0).
+  float mloc = -INFINITY;
+  for (int s = lane; s < nch; s += 64) {
+    const float ls = base[static_cast<int64_t>(s) * stride + 1];
+    if (ls != 0.f) mloc = fmaxf(mloc, base[static_cast<int64_t>(s) * stride]);
+  }
+  const float M = wave_max(mloc);
+  const float Mref = M == -INFINITY ? 0.f : M;
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+  for (int s0 = 0; s0 < nch; s0 += 64) {
+    const int s = s0 + lane;
+    float wgt = 0.f;
+    if (s < nch) {
+      const float ls = base[static_cast<int64_t>(s) * stride + 1];
+      if (ls != 0.f) {
+        wgt = fast_exp2((base[static_cast<int64_t>(s) * stride] - Mref) * kLog2e);
+        lsum = fmaf(wgt, ls, lsum);
+      }
+    }
+    const int n = min(64, nch - s0);
+    for (int t = 0; t < n; ++t) {
+      const float wt = __shfl(wgt, t);
+      const float* row = base + static_cast<int64_t>(s0 + t) * stride + 2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = lane + 64 * r;
+        if (d < D) acc[r] = fmaf(wt, row[d], acc[r]);
+      }
+    }
+  }
+  const float L = wave_sum(lsum);
+  S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int d = lane + 64 * r;
+    if (d < D) o[d] = E::from_f(L > 0.f ? acc[r] / L : 0.f);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Host side
+// ----------------------------------------------------------------------------
+
+thread_local std::string g_last_error;
+thread_local int g_last_status = 0;
+
+int fail(int status, const std::string& msg) {
+  g_last_status = status;
+  g_last_error = msg;
+  return status;
+}
+
+void copy_msg(char* msg, size_t cap, const char* text) {
+  if (!msg || cap == 0) return;
+  size_t n = strlen(text);
+  if (n >= cap) n = cap - 1;
+  memcpy(msg, text, n);
+  msg[n] = '\0';
+}
+
+int invalid(char* msg, size_t cap, const char* text) {
+  copy_msg(msg, cap, text);
+  return fail(QD_ERR_INVALID_VALUE, text);
+}
+
+bool same_sizes(const qd_tensor_desc* a, const qd_tensor_desc* b) {
+  if (a->ndim != b->ndim) return false;
+  const int n = a->ndim < 8 ? a->ndim : 8;
+  for (int i = 0; i < n; ++i)
+    if (a->sizes[i] != b->sizes[i]) return false;
+  return true;
+}
+
+constexpr int kMfmaHeads = 16;
+
+bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int dtype) {
+  if (dtype != QD_DTYPE_F16 && dtype != QD_DTYPE_BF16) return false;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return false;
+  if (block_size % 16 != 0) return false;
+  if (kv_heads <= 0 || q_heads % kv_heads != 0) return false;
+  return q_heads / kv_heads <= kMfmaHeads;
+}
+
+constexpr int kPrefetch = 3;
+
+using KernelFn = void (*)(DecodeParams);
+
+template <int DT>
+KernelFn pick_mfma(int D) {
+  switch (D) {
+    case 64: return decode_mfma_kernel<64, DT, kPrefetch>;
+    case 128: return decode_mfma_kernel<128, DT, kPrefetch>;
+    default: return decode_mfma_kernel<256, DT, 2>;
+  }
+}
+
+template <int DT>
+KernelFn pick_generic(int D) {
+  const bool v16 = DT != QD_DTYPE_F32;
+  (void)v16;
+  if (D <= 16) return D == 16 ? decode_generic_kernel<DT, 1, true> : decode_generic_kernel<DT, 1, false>;
+  if (D <= 32) return D == 32 ? decode_generic_kernel<DT, 2, true> : decode_generic_kernel<DT, 2, false>;
+  if (D <= 64) return D == 64 ? decode_generic_kernel<DT, 4, true> : decode_generic_kernel<DT, 4, false>;
+  if (D <= 128) return D == 128 ? decode_generic_kernel<DT, 8, true> : decode_generic_kernel<DT, 8, false>;
+  return D == 256 ? decode_generic_kernel<DT, 16, true> : decode_generic_kernel<DT, 16, false>;
+}
+
+KernelFn pick_combine(int dtype) {
+  switch (dtype) {
+    case QD_DTYPE_F32: return combine_kernel<QD_DTYPE_F32>;
+    case QD_DTYPE_F16: return combine_kernel<QD_DTYPE_F16>;
+    default: return combine_kernel<QD_DTYPE_BF16>;
+  }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int qd_abi_version(void) { return QD_ATTENTION_ABI_VERSION; }
+
+const char* qd_error_string(int status) {
+  if (status == QD_OK) return "success";
+  if (status == g_last_status && !g_last_error.empty()) return g_last_error.c_str();
+  return hipGetErrorString(static_cast<hipError_t>(status));
+}
+
+int qd_gqa_decode_validate(const qd_tensor_desc* q, const qd_tensor_desc* k,
+                           const qd_tensor_desc* v, const qd_tensor_desc* table,
+                           const qd_tensor_desc* lens, double scale, int64_t splits, char* msg,
+                           size_t cap) {
+  if (!q || !k || !v || !table || !lens) return invalid(msg, cap, "null tensor descriptor");
+  if (!(splits >= 1 && splits <= 65535)) return invalid(msg, cap, "splits must be in [1, 65535]");
+  const qd_tensor_desc* all[5] = {q, k, v, table, lens};
+  const char* names[5] = {"q", "k_cache", "v_cache", "block_table", "context_lens"};
+  for (int i = 0; i < 5; ++i) {
+    if (!all[i]->defined || !all[i]->is_device) {
+      std::string m = std::string(names[i]) + " must be a CUDA tensor";
+      return invalid(msg, cap, m.c_str());
+    }
+    if (!all[i]->contiguous) {
+      std::string m = std::string(names[i]) + " must be contiguous";
+      return invalid(msg, cap, m.c_str());
+    }
+  }
+  if (q->ndim != 3) return invalid(msg, cap, "q must be [B, Hq, D]");
+  if (k->ndim != 4) return invalid(msg, cap, "k_cache must be [Nblocks, BlockSize, Hkv, D]");
+  if (!same_sizes(v, k)) return invalid(msg, cap, "v_cache shape mismatch");
+  if (table->ndim != 2) return invalid(msg, cap, "block_table must be [B, MaxPages]");
+  if (lens->ndim != 1) return invalid(msg, cap, "context_lens must be [B]");
+  for (int i = 1; i < 5; ++i)
+    if (all[i]->device_index != q->device_index)
+      return invalid(msg, cap, "all tensors must use one CUDA device");
+  if (q->dtype != k->dtype || q->dtype != v->dtype) return invalid(msg, cap, "q/k/v dtype must match");
+  if (q->dtype != QD_DTYPE_F32 && q->dtype != QD_DTYPE_F16 && q->dtype != QD_DTYPE_BF16)
+    return invalid(msg, cap, "q/k/v must be float32/float16/bfloat16");
+  if (table->dtype != QD_DTYPE_I32 || lens->dtype != QD_DTYPE_I32)
+    return invalid(msg, cap, "block_table and context_lens must be int32");
+  if (q->sizes[0] != table->sizes[0] || q->sizes[0] != lens->sizes[0])
+    return invalid(msg, cap, "batch sizes must match");
+  if (q->sizes[2] != k->sizes[3]) return invalid(msg, cap, "q head_dim and cache head_dim must match");
+  if (!(q->sizes[1] > 0 && k->sizes[2] > 0 && q->sizes[1] % k->sizes[2] == 0))
+    return invalid(msg, cap, "Hq must be divisible by Hkv");
+  if (!(q->sizes[2] > 0 && q->sizes[2] <= 256)) return invalid(msg, cap, "supported head_dim is [1, 256]");
+  if (!(k->sizes[0] > 0 && k->sizes[1] > 0))
+    return invalid(msg, cap, "cache must have positive blocks and block_size");
+  if (!(table->sizes[1] > 0)) return invalid(msg, cap, "block_table must have at least one page");
+  if (!(isfinite(scale) && scale > 0.0)) return invalid(msg, cap, "scale must be positive and finite");
+  const int64_t imax = 2147483647;
+  if (!(q->sizes[0] <= imax && q->sizes[1] <= imax && k->sizes[2] <= imax && k->sizes[1] <= imax &&
+        table->sizes[1] <= imax))
+    return invalid(msg, cap, "tensor sizes exceed int32 CUDA launch limits");
+  copy_msg(msg, cap, "");
+  return QD_OK;
+}
+
+int qd_gqa_decode_validate_workspace(const qd_tensor_desc* q, const qd_tensor_desc* ws,
+                                     int64_t splits, char* msg, size_t cap) {
+  if (!q || !ws) return invalid(msg, cap, "null tensor descriptor");
+  if (!(splits > 1)) return invalid(msg, cap, "workspace requires splits > 1");
+  if (!(ws->defined && ws->is_device && ws->device_index == q->device_index && ws->contiguous &&
+        ws->dtype == QD_DTYPE_F32))
+    return invalid(msg, cap, "workspace must be contiguous float32 on q device");
+  if (!(ws->ndim == 4 && ws->sizes[0] == q->sizes[0] && ws->sizes[1] == q->sizes[1] &&
+        ws->sizes[2] == splits && ws->sizes[3] == q->sizes[2] + 2))
+    return invalid(msg, cap, "workspace shape must be [B,Hq,splits,D+2]");
+  copy_msg(msg, cap, "");
+  return QD_OK;
+}
+
+int qd_gqa_decode_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size,
+                       int max_pages, int dtype, int cu_count, int* splits, int* chunk_pages) {
+  (void)q_heads;
+  (void)head_dim;
+  (void)dtype;
+  if (!splits || !chunk_pages) return fail(QD_ERR_INVALID_VALUE, "null plan output");
+  if (batch < 0 || kv_heads <= 0 || block_size <= 0 || max_pages <= 0)
+    return fail(QD_ERR_INVALID_VALUE, "invalid shapes for plan");
+  const int64_t cus = cu_count > 0 ? cu_count : 256;
+  // Work items are (sequence, kv-head) pairs; each split of one item is a
+  // wave.  Aim for ~8 resident waves per CU, and keep every split at least
+  // 256 tokens and at most 64 pages so that split partials stay a small
+  // fraction of the K/V bytes.
+  const int64_t items = static_cast<int64_t>(batch) * kv_heads;
+  const int64_t target_waves = cus * 8;
+  int64_t want = items > 0 ? (target_waves + items - 1) / items : 1;
+  if (want < 1) want = 1;
+  const int64_t min_pages = (256 + block_size - 1) / block_size;
+  int64_t cp = (max_pages + want - 1) / want;
+  if (cp < min_pages) cp = min_pages;
+  if (cp > 64) cp = 64;
+  if (cp > max_pages) cp = max_pages;
+  int64_t s = (max_pages + cp - 1) / cp;
+  if (s > 65535) {
+    s = 65535;
+    cp = (max_pages + s - 1) / s;
+  }
+  *splits = static_cast<int>(s);
+  *chunk_pages = static_cast<int>(cp);
+  return QD_OK;
+}
+
+size_t qd_gqa_decode_workspace_bytes(int batch, int q_heads, int head_dim, int splits) {
+  if (splits <= 1 || batch <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
+  return static_cast<size_t>(batch) * q_heads * splits * (head_dim + 2) * sizeof(float);
+}
+
+int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block_size, int dtype,
+                              int flags) {
+  if (flags & QD_FLAG_FORCE_GENERIC) return 0;
+  return mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) ? 1 : 0;
+}
+
+int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* block_table, const int32_t* context_lens, void* out,
+                         float* workspace, size_t workspace_bytes, int batch, int q_heads,
+                         int kv_heads, int head_dim, int block_size, int max_pages,
+                         int64_t num_blocks, int dtype, float scale, int splits, int chunk_pages,
+                         int flags, void* stream) {
+  if (batch < 0) return fail(QD_ERR_INVALID_VALUE, "batch must be >= 0");
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
+    return fail(QD_ERR_INVALID_VALUE, "Hq must be divisible by Hkv");
+  if (head_dim < 1 || head_dim > 256) return fail(QD_ERR_INVALID_VALUE, "supported head_dim is [1, 256]");
+  if (block_size <= 0 || num_blocks <= 0)
+    return fail(QD_ERR_INVALID_VALUE, "cache must have positive blocks and block_size");
+  if (max_pages <= 0) return fail(QD_ERR_INVALID_VALUE, "block_table must have at least one page");
+  if (dtype != QD_DTYPE_F32 && dtype != QD_DTYPE_F16 && dtype != QD_DTYPE_BF16)
+    return fail(QD_ERR_INVALID_VALUE, "q/k/v must be float32/float16/bfloat16");
+  if (!(isfinite(scale) && scale > 0.f)) return fail(QD_ERR_INVALID_VALUE, "scale must be positive and finite");
+  if (splits < 1 || splits > 65535) return fail(QD_ERR_INVALID_VALUE, "splits must be in [1, 65535]");
+  if (chunk_pages < 0) return fail(QD_ERR_INVALID_VALUE, "chunk_pages must be >= 0");
+  if (chunk_pages > 0 && static_cast<int64_t>(chunk_pages) * splits < max_pages)
+    return fail(QD_ERR_INVALID_VALUE, "splits * chunk_pages must cover max_pages");
+  if (batch > 65535 || kv_heads > 65535)
+    return fail(QD_ERR_INVALID_VALUE, "batch and kv_heads must be <= 65535 (grid limit)");
+  if (batch == 0) return QD_OK;
+  if (!q || !k_cache || !v_cache || !block_table || !context_lens || !out)
+    return fail(QD_ERR_INVALID_VALUE, "null tensor pointer");
+  if (splits > 1) {
+    const size_t need = qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, splits);
+    if (!workspace || workspace_bytes < need)
+      return fail(QD_ERR_INVALID_VALUE, "workspace too small for [B,Hq,splits,D+2] float32");
+  }
+
+  DecodeParams prm;
+  prm.q = q;
+  prm.k = k_cache;
+  prm.v = v_cache;
+  prm.table = block_table;
+  prm.lens = context_lens;
+  prm.out = out;
+  prm.ws = workspace;
+  prm.B = batch;
+  prm.Hq = q_heads;
+  prm.Hkv = kv_heads;
+  prm.D = head_dim;
+  prm.P = block_size;
+  prm.maxP = max_pages;
+  prm.g = q_heads / kv_heads;
+  prm.splits = splits;
+  prm.chunk_pages = chunk_pages;
+  prm.head_chunks = (prm.g + kGenericHeads - 1) / kGenericHeads;
+  prm.num_blocks = num_blocks;
+  prm.sl2 = scale * kLog2e;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool use_mfma = qd_gqa_decode_kernel_kind(q_heads, kv_heads, head_dim, block_size, dtype, flags) &&
+                        aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out);
+  (void)hipGetLastError();  // start from a clean error state
+  if (use_mfma) {
+    const KernelFn fn = dtype == QD_DTYPE_F16 ? pick_mfma<QD_DTYPE_F16>(head_dim)
+                                              : pick_mfma<QD_DTYPE_BF16>(head_dim);
+    hipLaunchKernelGGL(fn, dim3(splits, kv_heads, batch), dim3(64), 0, st, prm);
+  } else {
+    KernelFn fn;
+    switch (dtype) {
+      case QD_DTYPE_F32: fn = pick_generic<QD_DTYPE_F32>(head_dim); break;
+      case QD_DTYPE_F16: fn = pick_generic<QD_DTYPE_F16>(head_dim); break;
+      default: fn = pick_generic<QD_DTYPE_BF16>(head_dim); break;
+    }
+    const int64_t gx = static_cast<int64_t>(splits) * prm.head_chunks;
+    if (gx > 2147483647) return fail(QD_ERR_INVALID_VALUE, "splits * head chunks exceed the grid limit");
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(gx), kv_heads, batch), dim3(64), 0, st, prm);
+  }
+  if (splits > 1) {
+    hipLaunchKernelGGL(pick_combine(dtype), dim3(q_heads, batch), dim3(64), 0, st, prm);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return fail(static_cast<int>(e), std::string("gqa_decode kernel launch failed: ") + hipGetErrorString(e));
+  }
+  return QD_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,269 @@
+"""Paged GQA decode benchmark on one MI355X.
+
+One step = one ``attention_amd.gqa_decode`` call over the whole batch of the
+workload (default cfg2, the Qwen3-8B-shaped config BASELINE.json's target is
+quoted on), with q/K/V/metadata already resident in HBM.  The timed region
+rotates over several K/V pools whose total exceeds the 256 MB Infinity Cache
+so that every call streams its K/V from HBM.  Output allocation is inside
+the timed region, as in the reference's measurement
+(reference ``benchmarks/measure_decode.py:40``).
+
+Prints one JSON line: ``value`` is achieved algorithmic HBM GB/s per call
+(bytes = K+V of valid tokens + q + out + lengths + used table entries),
+``us_per_call`` the latency; ``roofline`` the decode kernel's fraction of
+the 8 TB/s HBM peak; ``cpu_baseline`` the reference CPU path timed on the
+host cores.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
+  python bench.py --mode copy     # HBM copy of known size (counter calibration)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "paged GQA decode µs/call and achieved HBM GB/s (% of peak), 1 MI355X"
+DT_NAME = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="cfg2")
+    ap.add_argument("--pools", type=int, default=0, help="K/V pools to rotate (0: enough for >768 MB)")
+    ap.add_argument("--kernel", choices=["auto", "generic"], default="auto",
+                    help="generic: force the portable VALU kernel through the C ABI")
+    ap.add_argument("--splits", type=int, default=0, help="override the plan (C ABI path)")
+    ap.add_argument("--chunk-pages", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-repeats", type=int, default=5)
+    ap.add_argument("--mode", choices=["decode", "copy"], default="decode")
+    ap.add_argument("--device-gen", action="store_true", help="draw inputs on the GPU")
+    return ap.parse_args()
+
+
+def time_loop(fn, steps: int, warmup: int, stream) -> float:
+    """Milliseconds per step: HIP events on `stream` around exactly `steps` calls."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def copy_mode(args) -> None:
+    n = 1 << 30  # bytes per copy
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_()
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    ms = time_loop(lambda i: dst.copy_(src), args.steps, args.warmup, stream)
+    gbs = 2 * n / (ms * 1e-3) / 1e9
+    print(json.dumps({"mode": "copy", "bytes_read_per_call": n, "bytes_written_per_call": n,
+                      "ms_per_call": ms, "gbs": gbs}), flush=True)
+
+
+def cpu_baseline(case_cpu, cfg, repeats: int) -> dict:
+    """Times the reference CPU path (oracle/cpu_path.py) on the host cores."""
+    from oracle.cpu_path import reference_cpu_path
+    from attention_amd.cases import algorithmic_bytes
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    q, k, v, table, lens = case_cpu
+    # Sample: the first sequences of the same batch, enough for ~1-3 s per call.
+    lens_l = lens.tolist()
+    nb, toks = 0, 0
+    for L in lens_l:
+        nb += 1
+        toks += L
+        if toks >= 40_000:
+            break
+    sample = (q[:nb], k, v, table[:nb], lens[:nb])
+    reference_cpu_path(*sample)  # warmup
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        reference_cpu_path(*sample)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    elem = q.element_size()
+    b_sample = algorithmic_bytes(lens_l[:nb], nb, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                                 cfg.block_size, elem)
+    b_full = algorithmic_bytes(lens_l, len(lens_l), cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                               cfg.block_size, elem)
+    gbs = b_sample / t / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_call_full_batch_est": round(t * b_full / b_sample * 1e6, 1),
+            "sample": (f"oracle/cpu_path.reference_cpu_path (torch CPU ops of reference "
+                       f"attention/reference/gqa.py:21-44) on the first {nb} of {len(lens_l)} "
+                       f"sequences ({toks} tokens) of the same {cfg.name} input, median of "
+                       f"{repeats} after 1 warmup: {t * 1e3:.1f} ms"),
+            "cpu": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the decode path is "
+              "measured on one MI355X and multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    if args.mode == "copy":
+        copy_mode(args)
+        return
+
+    import attention_amd
+    from attention_amd import cabi
+    from attention_amd.cases import CONFIGS, algorithmic_bytes, algorithmic_flops
+
+    if not attention_amd.is_cuda_extension_loaded():
+        raise RuntimeError("HIP op library not loaded; run __graft_entry__.build()")
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    lengths = cfg.lengths()
+    if args.device_gen:
+        case = cfg.make(device=dev, device_gen=True, lengths=lengths)
+        case_cpu = None
+    else:
+        case_cpu = cfg.make(device="cpu", lengths=lengths)
+        case = tuple(x.to(dev) for x in case_cpu)
+    q, k, v, table, lens = case
+    kv_bytes = 2 * k.numel() * k.element_size()
+    pools = args.pools or max(2, math.ceil(768e6 / kv_bytes))
+    ks, vs = [k], [v]
+    for i in range(1, pools):
+        ks.append(k.roll(i, dims=0).contiguous())
+        vs.append(v.roll(i, dims=0).contiguous())
+    torch.cuda.synchronize()
+    log(f"{cfg.name}: {len(lengths)} seqs, sum len {sum(lengths)}, KV pool {kv_bytes / 1e6:.1f} MB "
+        f"x {pools} pools, setup {time.perf_counter() - t0:.1f}s")
+
+    elem = q.element_size()
+    alg_bytes = algorithmic_bytes(lengths, cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                                  cfg.block_size, elem)
+    scale = 1.0 / math.sqrt(cfg.head_dim)
+    stream = torch.cuda.current_stream(dev)
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    splits, chunk = cabi.plan(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size,
+                              table.shape[1], cabi.DTYPE[q.dtype], cu)
+
+    if args.kernel == "auto" and args.splits == 0:
+        path = "torch.ops.qd_attention.gqa_decode (plan)"
+
+        def step(i):
+            attention_amd.gqa_decode(q, ks[i % pools], vs[i % pools], table, lens)
+    else:
+        if args.splits:
+            splits, chunk = args.splits, args.chunk_pages
+        flags = cabi.QD_FLAG_FORCE_GENERIC if args.kernel == "generic" else 0
+        out = torch.empty_like(q)
+        ws = torch.empty(max(1, cfg.batch * cfg.q_heads * splits * (cfg.head_dim + 2)), device=dev)
+        path = f"C ABI qd_gqa_decode_launch kernel={args.kernel}"
+
+        def step(i):
+            rc = cabi.launch(q, ks[i % pools], vs[i % pools], table, lens, out, scale=scale,
+                             splits=splits, chunk_pages=chunk, workspace=ws, flags=flags,
+                             stream=stream.cuda_stream)
+            if rc:
+                raise RuntimeError(cabi.error_string(rc))
+    kind = cabi.lib().qd_gqa_decode_kernel_kind(cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                                                cfg.block_size, cabi.DTYPE[q.dtype],
+                                                cabi.QD_FLAG_FORCE_GENERIC if args.kernel == "generic" else 0)
+    kname = "decode_mfma_kernel" if kind == 1 else "decode_generic_kernel"
+    log(f"path: {path}; kernel {kname}; splits={splits} chunk_pages={chunk}; "
+        f"warmup {args.warmup}, steps {args.steps}")
+    ms = time_loop(step, args.steps, args.warmup, stream)
+    us = ms * 1e3
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    log(f"{us:.2f} us/call, {gbs:.1f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of peak)")
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "us_per_call": round(us, 3),
+        "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DT_NAME[q.dtype],
+        "data": ("synthetic: seeded reference recipe (benchmarks/data.py:8-43), "
+                 f"{'GPU' if args.device_gen else 'CPU'}-drawn N(0,1) q/K/V, shuffled exact pool"),
+        "config": {
+            "workload": f"{cfg.name}: {cfg.description}",
+            "batch": cfg.batch, "q_heads": cfg.q_heads, "kv_heads": cfg.kv_heads,
+            "head_dim": cfg.head_dim, "block_size": cfg.block_size,
+            "context_lens": (list(cfg.fixed_lengths) if cfg.fixed_lengths else
+                             f"U{list(cfg.len_range)} seed {10_000 + cfg.seed}: sum {sum(lengths)}, "
+                             f"min {min(lengths)}, max {max(lengths)}"),
+            "kv_pools_rotated": pools, "splits": splits, "chunk_pages": chunk, "path": path,
+            "algorithmic_bytes_per_call": alg_bytes,
+            "flops_per_call": algorithmic_flops(lengths, cfg.q_heads, cfg.head_dim),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": kname + ("+combine_kernel" if splits > 1 else ""),
+            "achieved": round(gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "duration_us": round(us, 3),
+            "note": ("achieved = algorithmic bytes per call / HIP-event time per call on the "
+                     "launch stream (decode + combine launches)"),
+        },
+    }
+    if not args.no_cpu_baseline:
+        if case_cpu is None:
+            case_cpu = tuple(x.cpu() for x in case)
+        log("timing the reference CPU path ...")
+        result["cpu_baseline"] = cpu_baseline(case_cpu, cfg, args.cpu_repeats)
+        log(f"cpu baseline {result['cpu_baseline']['value']} GB/s on "
+            f"{result['cpu_baseline']['cores']} threads")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

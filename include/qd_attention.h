@@ -1,0 +1,136 @@
+/*
+ * qd_attention.h — C ABI of the MI355X (gfx950) paged grouped-query decode
+ * attention library `libqd_attention.so`.
+ *
+ * Everything here is plain C: pointers, sizes and integer codes.  No torch,
+ * no C++ and no HIP types cross this boundary (a HIP stream is passed as an
+ * opaque `void*`, NULL meaning the null stream).  The torch binding
+ * (`attention_amd/csrc/torch_ops.cpp`) is one caller; a ctypes/cffi/cgo
+ * binding is another.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   qd_gqa_decode_validate            csrc/cuda/dense/gqa_decode.cu:103-138
+ *   qd_gqa_decode_validate_workspace  csrc/cuda/dense/gqa_decode.cu:148-152
+ *   qd_gqa_decode_plan                attention/core.py:80-96 (gqa_decode_auto)
+ *   qd_gqa_decode_workspace_bytes     csrc/cuda/dense/gqa_decode.cu:152-154
+ *   qd_gqa_decode_launch              csrc/cuda/dense/gqa_decode.cu:140-183,
+ *                                     kernels :18-87
+ *
+ * Tensor layouts (all row-major, contiguous, on one device):
+ *   q            [batch, q_heads, head_dim]                   dtype
+ *   k/v cache    [num_blocks, block_size, kv_heads, head_dim] dtype
+ *   block_table  [batch, max_pages]                           int32
+ *   context_lens [batch]                                      int32
+ *   out          [batch, q_heads, head_dim]                   dtype
+ *   workspace    [batch, q_heads, splits, head_dim + 2]       float32
+ *                per (b, h, s): {max scaled score, sum exp, acc[head_dim]}
+ *
+ * Metadata contents (page ids, lengths) are caller-owned and never checked
+ * here: only table entries [0, ceil(len/block_size)) of each row are read,
+ * and a length <= 0 yields an all-zero output row.
+ */
+#ifndef QD_ATTENTION_H
+#define QD_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QD_ATTENTION_ABI_VERSION 1
+
+/* Element type codes shared by every entry point. */
+enum {
+  QD_DTYPE_F32 = 0,
+  QD_DTYPE_F16 = 1,
+  QD_DTYPE_BF16 = 2,
+  QD_DTYPE_I32 = 3,
+  QD_DTYPE_OTHER = -1
+};
+
+/* Status codes.  0 is success; any other value is a hipError_t code
+ * (hipErrorInvalidValue = 1 for argument errors).  qd_error_string() gives
+ * the message of the last failure on the calling thread. */
+enum { QD_OK = 0, QD_ERR_INVALID_VALUE = 1 };
+
+/* qd_gqa_decode_launch flags. */
+enum {
+  /* Use the portable VALU kernel even where the MFMA kernel applies. */
+  QD_FLAG_FORCE_GENERIC = 1
+};
+
+/* Shape/placement descriptor of one tensor, for validation only. */
+typedef struct qd_tensor_desc {
+  int32_t defined;      /* 0: argument absent (optional workspace)        */
+  int32_t is_device;    /* 1: GPU tensor                                   */
+  int32_t device_index; /* device ordinal (ignored when !is_device)        */
+  int32_t contiguous;   /* 1: row-major contiguous                         */
+  int32_t dtype;        /* QD_DTYPE_*                                      */
+  int32_t ndim;         /* number of dimensions, <= 8                      */
+  int64_t sizes[8];
+} qd_tensor_desc;
+
+/* ABI version of the loaded library (QD_ATTENTION_ABI_VERSION). */
+int qd_abi_version(void);
+
+/* Message for `status`: the detailed text of the calling thread's last
+ * failure when it matches, else the HIP error name. Never NULL. */
+const char* qd_error_string(int status);
+
+/* Checks shapes, dtypes and placement in the reference's order
+ * (gqa_decode.cu:103-138).  Returns 0, or QD_ERR_INVALID_VALUE with the
+ * reference's message copied into msg (NUL-terminated, truncated to
+ * msg_cap).  Reads no tensor contents. */
+int qd_gqa_decode_validate(const qd_tensor_desc* q, const qd_tensor_desc* k_cache,
+                           const qd_tensor_desc* v_cache, const qd_tensor_desc* block_table,
+                           const qd_tensor_desc* context_lens, double scale, int64_t splits,
+                           char* msg, size_t msg_cap);
+
+/* Workspace checks of the split path (gqa_decode.cu:148-152); call after
+ * qd_gqa_decode_validate succeeded and only when batch > 0. */
+int qd_gqa_decode_validate_workspace(const qd_tensor_desc* q, const qd_tensor_desc* workspace,
+                                     int64_t splits, char* msg, size_t msg_cap);
+
+/* Launch plan for the automatic path: number of context splits and pages
+ * per split, chosen from static shapes only (no device reads, no sync).
+ * cu_count <= 0 means 256 (MI355X).  Writes *splits >= 1 and
+ * *chunk_pages >= 1 (pages of block_size tokens per split). */
+int qd_gqa_decode_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size,
+                       int max_pages, int dtype, int cu_count, int* splits, int* chunk_pages);
+
+/* Bytes of float32 workspace [batch, q_heads, splits, head_dim + 2]; 0 when
+ * splits <= 1 (the single-split path needs none). */
+size_t qd_gqa_decode_workspace_bytes(int batch, int q_heads, int head_dim, int splits);
+
+/* Enqueues paged GQA decode on `stream` (a hipStream_t, NULL = null stream).
+ *   splits      >= 1.  1: each (sequence, kv-head) in one pass, no
+ *               workspace.  > 1: split-context partials into `workspace`
+ *               and a log-sum-exp combine.
+ *   chunk_pages 0: split s of a sequence with n pages covers pages
+ *               [s*c, (s+1)*c), c = ceil(n/splits) (reference split API);
+ *               > 0: fixed c = chunk_pages for every sequence (plan path;
+ *               requires splits * chunk_pages >= max_pages).
+ *   workspace   device float32 buffer of workspace_bytes >= the value of
+ *               qd_gqa_decode_workspace_bytes(); may be NULL if splits == 1.
+ * Does not allocate, does not synchronize and does not read metadata on
+ * the host.  Returns 0 or a status code (argument errors are reported
+ * before anything is enqueued). */
+int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* block_table, const int32_t* context_lens, void* out,
+                         float* workspace, size_t workspace_bytes, int batch, int q_heads,
+                         int kv_heads, int head_dim, int block_size, int max_pages,
+                         int64_t num_blocks, int dtype, float scale, int splits,
+                         int chunk_pages, int flags, void* stream);
+
+/* Which kernel qd_gqa_decode_launch would run for these shapes:
+ * 1 = MFMA kernel, 0 = portable VALU kernel. */
+int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block_size,
+                              int dtype, int flags);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QD_ATTENTION_H */

@@ -1,0 +1,257 @@
+"""CPU tests of the drop-in boundary: the C ABI library loads and exports
+every declared symbol, host-side validation reproduces the reference's
+checks in order (reference csrc/cuda/dense/gqa_decode.cu:103-138, :148-152),
+the launch plan, launch argument errors (reported before anything is
+enqueued), the torch op schemas, and the Python API's error behaviour
+(reference attention/core.py:30-35, :48-49, :86-87).  No kernel runs here.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+import attention_amd
+from attention_amd import cabi, core
+from attention_amd.cases import CONFIGS
+
+F32, F16, BF16, I32 = 0, 1, 2, 3
+
+
+def test_library_exports_every_header_symbol():
+    names = cabi.header_functions()
+    assert len(names) >= 8
+    L = ctypes.CDLL(cabi.LIB_PATH)
+    for n in names:
+        assert hasattr(L, n), n
+    assert cabi.lib().qd_abi_version() == 1
+
+
+def good():
+    return [cabi.desc([4, 8, 64], F16), cabi.desc([57, 16, 2, 64], F16),
+            cabi.desc([57, 16, 2, 64], F16), cabi.desc([4, 32], I32), cabi.desc([4], I32)]
+
+
+def test_validate_accepts_good_shapes():
+    assert cabi.validate(*good()) == (0, "")
+
+
+def _case(mutate, scale=0.125, splits=1):
+    d = good()
+    mutate(d)
+    return cabi.validate(*d, scale=scale, splits=splits)
+
+
+def _set(i, **kw):
+    def f(d):
+        for key, val in kw.items():
+            if key == "sizes":
+                d[i] = cabi.desc(val, d[i].dtype, d[i].is_device, d[i].device_index, d[i].contiguous)
+            else:
+                setattr(d[i], key, val)
+    return f
+
+
+VALIDATION_ORDER = [
+    # (mutation, scale, splits, expected message)
+    (lambda d: None, 0.125, 0, "splits must be in [1, 65535]"),
+    (lambda d: None, 0.125, 65536, "splits must be in [1, 65535]"),
+    (_set(0, is_device=0), 0.125, 1, "q must be a CUDA tensor"),
+    (_set(0, contiguous=0), 0.125, 1, "q must be contiguous"),
+    (_set(1, is_device=0), 0.125, 1, "k_cache must be a CUDA tensor"),
+    (_set(2, contiguous=0), 0.125, 1, "v_cache must be contiguous"),
+    (_set(3, is_device=0), 0.125, 1, "block_table must be a CUDA tensor"),
+    (_set(4, contiguous=0), 0.125, 1, "context_lens must be contiguous"),
+    (_set(0, sizes=[4, 8]), 0.125, 1, "q must be [B, Hq, D]"),
+    (_set(1, sizes=[57, 16, 128]), 0.125, 1, "k_cache must be [Nblocks, BlockSize, Hkv, D]"),
+    (_set(2, sizes=[57, 16, 2, 32]), 0.125, 1, "v_cache shape mismatch"),
+    (_set(3, sizes=[4, 32, 1]), 0.125, 1, "block_table must be [B, MaxPages]"),
+    (_set(4, sizes=[4, 1]), 0.125, 1, "context_lens must be [B]"),
+    (_set(2, device_index=1), 0.125, 1, "all tensors must use one CUDA device"),
+    (_set(1, dtype=BF16), 0.125, 1, "q/k/v dtype must match"),
+    (lambda d: [setattr(x, "dtype", 5) for x in d[:3]], 0.125, 1,
+     "q/k/v must be float32/float16/bfloat16"),
+    (_set(3, dtype=5), 0.125, 1, "block_table and context_lens must be int32"),
+    (_set(4, sizes=[3]), 0.125, 1, "batch sizes must match"),
+    (lambda d: (_set(1, sizes=[57, 16, 2, 32])(d), _set(2, sizes=[57, 16, 2, 32])(d)), 0.125, 1,
+     "q head_dim and cache head_dim must match"),
+    (lambda d: (_set(1, sizes=[57, 16, 3, 64])(d), _set(2, sizes=[57, 16, 3, 64])(d)), 0.125, 1,
+     "Hq must be divisible by Hkv"),
+    (lambda d: [_set(i, sizes=s)(d) for i, s in
+                [(0, [4, 8, 300]), (1, [57, 16, 2, 300]), (2, [57, 16, 2, 300])]], 0.125, 1,
+     "supported head_dim is [1, 256]"),
+    (lambda d: (_set(1, sizes=[0, 16, 2, 64])(d), _set(2, sizes=[0, 16, 2, 64])(d)), 0.125, 1,
+     "cache must have positive blocks and block_size"),
+    (_set(3, sizes=[4, 0]), 0.125, 1, "block_table must have at least one page"),
+    (lambda d: None, 0.0, 1, "scale must be positive and finite"),
+    (lambda d: None, float("inf"), 1, "scale must be positive and finite"),
+    (lambda d: None, float("nan"), 1, "scale must be positive and finite"),
+    (lambda d: [_set(i, sizes=s)(d) for i, s in
+                [(0, [2 ** 31, 8, 64]), (3, [2 ** 31, 32]), (4, [2 ** 31])]], 0.125, 1,
+     "tensor sizes exceed int32 CUDA launch limits"),
+]
+
+
+@pytest.mark.parametrize("i", range(len(VALIDATION_ORDER)))
+def test_validation_messages_in_reference_order(i):
+    mutate, scale, splits, want = VALIDATION_ORDER[i]
+    rc, msg = _case(mutate, scale, splits)
+    assert rc == 1 and msg == want
+    assert cabi.error_string(rc) == want
+
+
+def test_first_failing_check_wins():
+    d = good()
+    d[0].is_device = 0           # check 2 (q)
+    d[1].dtype = BF16            # check 9
+    d[3].sizes[1] = 0            # check 17
+    assert cabi.validate(*d)[1] == "q must be a CUDA tensor"
+
+
+def test_workspace_validation():
+    q = cabi.desc([4, 8, 64], F16)
+    ok = cabi.desc([4, 8, 4, 66], F32)
+    assert cabi.validate_workspace(q, ok, 4) == (0, "")
+    assert cabi.validate_workspace(q, ok, 1)[1] == "workspace requires splits > 1"
+    bad_dtype = cabi.desc([4, 8, 4, 66], F16)
+    assert cabi.validate_workspace(q, bad_dtype, 4)[1] == "workspace must be contiguous float32 on q device"
+    other_dev = cabi.desc([4, 8, 4, 66], F32, device=1)
+    assert cabi.validate_workspace(q, other_dev, 4)[1] == "workspace must be contiguous float32 on q device"
+    assert cabi.validate_workspace(q, cabi.desc([4, 8, 2, 66], F32), 4)[1] == \
+        "workspace shape must be [B,Hq,splits,D+2]"
+    assert cabi.validate_workspace(q, cabi.desc([4, 8, 4, 64], F32), 4)[1] == \
+        "workspace shape must be [B,Hq,splits,D+2]"
+
+
+# ----------------------------------------------------------------------------
+# Plan and workspace size
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_plan_covers_capacity(name):
+    cfg = CONFIGS[name]
+    max_pages = max(1, -(-max(cfg.lengths()) // cfg.block_size))
+    s, c = cabi.plan(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size, max_pages)
+    assert 1 <= s <= 65535 and 1 <= c <= 64 or (s == 1 and c == max_pages)
+    assert s * c >= max_pages
+    if s > 1:
+        assert c * cfg.block_size >= 256 or c == max_pages
+
+
+def test_plan_values_for_configs():
+    # cfg2: 256 (seq, kv-head) items, 256-page tables -> 8 splits of 32 pages.
+    assert cabi.plan(32, 32, 8, 128, 16, 256) == (8, 32)
+    # cfg4: 64 items, 8192-page tables -> 64-page splits.
+    assert cabi.plan(8, 64, 8, 128, 16, 8192) == (128, 64)
+    # cfg5: 2048 items already fill the GPU -> one pass.
+    assert cabi.plan(256, 40, 8, 128, 32, 32) == (1, 32)
+
+
+def test_plan_rejects_bad_shapes():
+    s, c = ctypes.c_int(), ctypes.c_int()
+    assert cabi.lib().qd_gqa_decode_plan(1, 8, 0, 64, 16, 4, 1, 256, ctypes.byref(s), ctypes.byref(c)) != 0
+
+
+def test_workspace_bytes():
+    assert cabi.lib().qd_gqa_decode_workspace_bytes(32, 32, 128, 8) == 32 * 32 * 8 * 130 * 4
+    assert cabi.lib().qd_gqa_decode_workspace_bytes(32, 32, 128, 1) == 0
+
+
+def test_kernel_kind_selection():
+    kind = cabi.lib().qd_gqa_decode_kernel_kind
+    assert kind(32, 8, 128, 16, BF16, 0) == 1
+    assert kind(40, 8, 128, 32, F16, 0) == 1
+    assert kind(8, 2, 64, 16, F16, 0) == 1
+    assert kind(32, 8, 128, 16, BF16, cabi.QD_FLAG_FORCE_GENERIC) == 0
+    assert kind(32, 8, 128, 16, F32, 0) == 0       # fp32 caches: VALU kernel
+    assert kind(32, 8, 100, 16, BF16, 0) == 0      # head_dim not 64/128/256
+    assert kind(32, 8, 128, 8, BF16, 0) == 0       # block_size not a multiple of 16
+    assert kind(34, 2, 128, 16, BF16, 0) == 0      # group of 17 > 16
+
+
+# ----------------------------------------------------------------------------
+# Launch argument errors (returned before any HIP call)
+# ----------------------------------------------------------------------------
+
+def _launch_args(**over):
+    a = dict(q=1, k=1, v=1, table=1, lens=1, out=1, ws=None, ws_bytes=0, B=4, Hq=8, Hkv=2, D=64,
+             P=16, maxP=32, N=57, dtype=F16, scale=0.125, splits=1, chunk=0, flags=0, stream=None)
+    a.update(over)
+    return [a[k] for k in ["q", "k", "v", "table", "lens", "out", "ws", "ws_bytes", "B", "Hq", "Hkv",
+                           "D", "P", "maxP", "N", "dtype", "scale", "splits", "chunk", "flags",
+                           "stream"]]
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(Hkv=3), "Hq must be divisible by Hkv"),
+    (dict(D=0), "supported head_dim is [1, 256]"),
+    (dict(P=0), "cache must have positive blocks and block_size"),
+    (dict(maxP=0), "block_table must have at least one page"),
+    (dict(dtype=3), "q/k/v must be float32/float16/bfloat16"),
+    (dict(scale=-1.0), "scale must be positive and finite"),
+    (dict(splits=0), "splits must be in [1, 65535]"),
+    (dict(splits=4, chunk=2), "splits * chunk_pages must cover max_pages"),
+    (dict(splits=4), "workspace too small for [B,Hq,splits,D+2] float32"),
+    (dict(B=70000), "batch and kv_heads must be <= 65535 (grid limit)"),
+    (dict(q=None), "null tensor pointer"),
+])
+def test_launch_argument_errors(over, msg):
+    rc = cabi.lib().qd_gqa_decode_launch(*_launch_args(**over))
+    assert rc == 1
+    assert cabi.error_string(rc) == msg
+
+
+def test_launch_batch_zero_is_a_no_op():
+    assert cabi.lib().qd_gqa_decode_launch(*_launch_args(B=0, q=None)) == 0
+
+
+# ----------------------------------------------------------------------------
+# Torch op surface and Python API
+# ----------------------------------------------------------------------------
+
+def test_op_schemas_match_reference():
+    ops = torch.ops.qd_attention
+    assert str(ops.gqa_decode.default._schema) == (
+        "qd_attention::gqa_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_table, "
+        "Tensor context_lens, float scale) -> Tensor")
+    assert str(ops.gqa_decode_split.default._schema) == (
+        "qd_attention::gqa_decode_split(Tensor q, Tensor k_cache, Tensor v_cache, "
+        "Tensor block_table, Tensor context_lens, float scale, int splits) -> Tensor")
+    assert str(ops.gqa_decode_split_workspace.default._schema) == (
+        "qd_attention::gqa_decode_split_workspace(Tensor q, Tensor k, Tensor v, Tensor table, "
+        "Tensor lengths, float scale, int splits, Tensor(a!) workspace) -> Tensor")
+
+
+def test_cpu_tensors_have_no_kernel():
+    q = torch.zeros(1, 8, 64, dtype=torch.float16)
+    k = torch.zeros(4, 16, 2, 64, dtype=torch.float16)
+    t = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises(NotImplementedError):
+        torch.ops.qd_attention.gqa_decode(q, k, k, t, torch.ones(1, dtype=torch.int32), 0.125)
+
+
+def test_public_api_surface():
+    assert attention_amd.is_cuda_extension_loaded()
+    for name in ["gqa_decode", "gqa_decode_split", "gqa_decode_auto", "is_cuda_extension_loaded"]:
+        assert name in attention_amd.__all__
+
+
+def test_missing_extension_raises_runtime_error(monkeypatch):
+    monkeypatch.setattr(core, "_LOAD_ERROR", OSError("libqd_attention_torch.so: missing"))
+    q = torch.zeros(1, 8, 64)
+    with pytest.raises(RuntimeError, match="HIP extension was not loaded"):
+        attention_amd.gqa_decode(q, q, q, q, q)
+    with pytest.raises(RuntimeError, match="HIP extension was not loaded"):
+        attention_amd.gqa_decode_split(q, q, q, q, q)
+    assert not attention_amd.is_cuda_extension_loaded()
+
+
+def test_backend_and_dimension_errors():
+    q = torch.zeros(1, 8, 64)
+    with pytest.raises(ValueError, match="triton"):
+        attention_amd.gqa_decode_split(q, q, q, q, q, backend="triton")
+    with pytest.raises(ValueError, match="backend must be cuda or triton"):
+        attention_amd.gqa_decode_split(q, q, q, q, q, backend="cpu")
+    with pytest.raises(ValueError, match="invalid decode input dimensions"):
+        attention_amd.gqa_decode_auto(q, q, q, q, q)

@@ -1,0 +1,354 @@
+"""GPU parity of the HIP decode path against the CPU oracle.
+
+Tolerance: |err| <= 2e-3 + 1e-2*|ref| for
+bf16/fp16 caches with fp32 accumulation; fp32 caches use 1e-5 + 1e-4*|ref|.
+Index handling (page permutation, poisoned unused slots, -1 padding) must be
+bit-exact.  Every case prints its name before touching the GPU.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import attention_amd
+from attention_amd.cases import CONFIGS, make_decode_case
+from oracle.gqa_oracle import oracle_decode, page_split_range, split_partials
+from attention_amd import cabi
+
+pytestmark = pytest.mark.gpu
+
+DT_NAME = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+TOL = {"f32": (1e-5, 1e-4), "f16": (2e-3, 1e-2), "bf16": (2e-3, 1e-2)}
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def subcase(case, batches):
+    """Compact CPU copy of the selected sequences (pages remapped 0..n-1)."""
+    q, k, v, table, lens = case
+    P = k.shape[1]
+    lens_c = lens.cpu()
+    tab_c = table.cpu()
+    sel_pages, rows, offset = [], [], 0
+    for b in batches:
+        n = max(0, math.ceil(int(lens_c[b]) / P))
+        sel_pages.append(tab_c[b, :n].long())
+        rows.append(list(range(offset, offset + n)))
+        offset += n
+    ids = torch.cat(sel_pages) if sel_pages else torch.zeros(0, dtype=torch.long)
+    if ids.numel() == 0:
+        ids = torch.zeros(1, dtype=torch.long)
+    k_s = k[ids.to(k.device)].float().cpu().numpy()
+    v_s = v[ids.to(v.device)].float().cpu().numpy()
+    maxp = max(1, max(len(r) for r in rows))
+    t_s = np.full((len(batches), maxp), -1, dtype=np.int32)
+    for i, r in enumerate(rows):
+        t_s[i, :len(r)] = r
+    q_s = q[list(batches)].float().cpu().numpy()
+    l_s = lens_c[list(batches)].numpy()
+    return q_s, k_s, v_s, t_s, l_s
+
+
+def oracle_rows(case, batches=None, scale=None):
+    q = case[0]
+    bsz = q.shape[0]
+    batches = list(range(bsz)) if batches is None else list(batches)
+    q_s, k_s, v_s, t_s, l_s = subcase(case, batches)
+    return oracle_decode(q_s, k_s, v_s, t_s, l_s, scale=scale, out_dtype=DT_NAME[q.dtype]), batches
+
+
+def assert_close(out, ref, dtype_name, rows=None, what=""):
+    got = out.float().cpu().numpy()
+    if rows is not None:
+        got = got[rows]
+    atol, rtol = TOL[dtype_name]
+    err = np.abs(got - ref)
+    bad = ~(err <= atol + rtol * np.abs(ref))
+    assert not bad.any(), (f"{what}: {bad.sum()} mismatches, max abs err {np.nanmax(err):.3e} "
+                           f"at {np.argwhere(bad)[:3].tolist()}")
+
+
+def to_dev(case, dev):
+    return tuple(x.to(dev) for x in case)
+
+
+# ----------------------------------------------------------------------------
+# Benchmark configurations
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg2", "cfg3", "cfg5"])
+def test_config_matches_oracle(gpu, name):
+    cfg = CONFIGS[name]
+    say(f"config {name} full oracle")
+    case = to_dev(cfg.make(device="cpu"), gpu)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    ref, rows = oracle_rows(case)
+    assert out.shape == case[0].shape and out.dtype == case[0].dtype
+    assert_close(out, ref, DT_NAME[cfg.dtype], rows, name)
+
+
+def test_cfg4_long_context(gpu):
+    cfg = CONFIGS["cfg4"]
+    say("config cfg4 (device-generated, oracle on 3 sequences)")
+    case = cfg.make(device=gpu, device_gen=True)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    lens = case[4].cpu().tolist()
+    pick = [int(np.argmax(lens)), int(np.argmin(lens)), 3]
+    ref, rows = oracle_rows(case, pick)
+    assert_close(out, ref, "bf16", rows, "cfg4")
+    assert torch.isfinite(out).all()
+
+
+# ----------------------------------------------------------------------------
+# Both kernels, through the C ABI
+# ----------------------------------------------------------------------------
+
+SHAPES = [
+    # (dtype, Hq, Hkv, D, P, lengths)
+    (torch.bfloat16, 32, 8, 128, 16, [1, 15, 16, 17, 300, 1024, 0, 33]),
+    (torch.float16, 28, 4, 128, 16, [5, 700, 4097, 1]),
+    (torch.float16, 40, 8, 128, 32, [128, 31, 32, 33, 1000]),
+    (torch.bfloat16, 8, 2, 64, 16, [17, 100, 255, 512]),
+    (torch.bfloat16, 16, 1, 256, 16, [1, 90, 513]),
+    (torch.float16, 16, 16, 64, 48, [47, 48, 49, 200]),
+    (torch.bfloat16, 17, 1, 128, 16, [40, 1, 300]),
+    (torch.float32, 32, 8, 128, 16, [1, 300, 1025]),
+    (torch.float32, 6, 3, 100, 7, [1, 6, 7, 8, 100]),
+    (torch.float16, 12, 4, 17, 5, [3, 19, 64]),
+    (torch.bfloat16, 4, 4, 1, 1, [1, 2, 9]),
+    (torch.float16, 64, 8, 128, 16, [2000, 1]),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{DT_NAME[s[0]]}-Hq{s[1]}-Hkv{s[2]}-D{s[3]}-P{s[4]}")
+@pytest.mark.parametrize("flags", [0, cabi.QD_FLAG_FORCE_GENERIC], ids=["auto", "generic"])
+def test_shapes_cabi(gpu, shape, flags):
+    dtype, hq, hkv, d, p, lengths = shape
+    kind = cabi.lib().qd_gqa_decode_kernel_kind(hq, hkv, d, p, cabi.DTYPE[dtype], flags)
+    say(f"shape {shape[1:5]} {DT_NAME[dtype]} kernel={'mfma' if kind else 'generic'}")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
+                                   block_size=p, dtype=dtype, seed=7), gpu)
+    q, k, v, table, lens = case
+    scale = 1.0 / math.sqrt(d)
+    ref, rows = oracle_rows(case)
+    for splits, chunk in [(1, 0), (3, 0), (table.shape[1], 1)]:
+        out = torch.full_like(q, float("nan"))
+        ws = torch.empty(max(1, q.shape[0] * hq * splits * (d + 2)), device=gpu, dtype=torch.float32)
+        rc = cabi.launch(q, k, v, table, lens, out, scale=scale, splits=splits, chunk_pages=chunk,
+                         workspace=ws if splits > 1 else None, flags=flags)
+        assert rc == 0, cabi.error_string(rc)
+        torch.cuda.synchronize()
+        assert_close(out, ref, DT_NAME[dtype], rows, f"splits={splits} chunk={chunk}")
+
+
+# ----------------------------------------------------------------------------
+# Split API, workspace contents
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4, 8, 16, 64])
+def test_split_api(gpu, splits):
+    say(f"gqa_decode_split splits={splits}")
+    case = to_dev(make_decode_case(lengths=[1, 17, 300, 1000, 64, 0], q_heads=32, kv_heads=8,
+                                   head_dim=128, block_size=16, dtype=torch.bfloat16, seed=3), gpu)
+    ref, rows = oracle_rows(case)
+    out = attention_amd.gqa_decode_split(*case, splits=splits)
+    torch.cuda.synchronize()
+    assert_close(out, ref, "bf16", rows, f"split {splits}")
+    if splits > 1:
+        ws = torch.full((6, 32, splits, 130), float("nan"), device=gpu)
+        out2 = attention_amd.gqa_decode_split(*case, splits=splits, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out2)
+
+
+def test_workspace_partials_match_oracle(gpu):
+    say("workspace partial contents vs oracle split_partials")
+    splits = 4
+    case_cpu = make_decode_case(lengths=[300, 1000, 64], q_heads=8, kv_heads=2, head_dim=64,
+                                block_size=16, dtype=torch.float16, seed=11)
+    case = to_dev(case_cpu, gpu)
+    ws = torch.full((3, 8, splits, 66), float("nan"), device=gpu)
+    attention_amd.gqa_decode_split(*case, splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    q, k, v, table, lens = (x.float().numpy() if x.is_floating_point() else x.numpy() for x in case_cpu)
+    maxp = table.shape[1]
+    ranges = lambda b, z: page_split_range(int(lens[b]), 16, maxp, splits, 0, z)
+    part = split_partials(q, k, v, table, lens, splits=splits, ranges=ranges)
+    got = ws.cpu().numpy()
+    for b in range(3):
+        n = math.ceil(int(lens[b]) / 16)
+        nch = min(splits, math.ceil(n / math.ceil(n / splits)))
+        if nch <= 1:
+            continue
+        np.testing.assert_allclose(got[b, :, :nch, 0], part[b, :, :nch, 0], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(got[b, :, :nch, 1], part[b, :, :nch, 1], rtol=2e-3)
+        np.testing.assert_allclose(got[b, :, :nch, 2:], part[b, :, :nch, 2:], rtol=2e-2, atol=2e-2)
+
+
+# ----------------------------------------------------------------------------
+# Bit-exact index handling
+# ----------------------------------------------------------------------------
+
+def _poisoned_case(dev, dtype=torch.bfloat16, lengths=(1, 17, 31, 300, 0, 64), hq=32, hkv=8, d=128, p=16):
+    q, k, v, table, lens = make_decode_case(lengths=list(lengths), q_heads=hq, kv_heads=hkv,
+                                            head_dim=d, block_size=p, dtype=dtype, seed=5)
+    used = torch.zeros(k.shape[0], p, dtype=torch.bool)
+    for b, L in enumerate(lengths):
+        for t in range(L):
+            used[table[b, t // p], t % p] = True
+    kp, vp = k.clone(), v.clone()
+    kp[~used] = float("nan")
+    vp[~used] = float("inf")
+    return (q, k, v, table, lens), (q, kp, vp, table, lens)
+
+
+@pytest.mark.parametrize("flags", [0, cabi.QD_FLAG_FORCE_GENERIC], ids=["auto", "generic"])
+def test_poisoned_unused_slots_bitwise(gpu, flags):
+    say(f"poisoned unused slots flags={flags}")
+    clean, poison = _poisoned_case("cpu")
+    outs = []
+    for case in (clean, poison):
+        q, k, v, table, lens = to_dev(case, gpu)
+        out = torch.empty_like(q)
+        ws = torch.empty(q.shape[0] * q.shape[1] * 4 * (q.shape[2] + 2), device=gpu)
+        rc = cabi.launch(q, k, v, table, lens, out, scale=1 / math.sqrt(q.shape[2]), splits=4,
+                         chunk_pages=0, workspace=ws, flags=flags)
+        assert rc == 0, cabi.error_string(rc)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.isfinite(outs[1]).all()
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_physical_permutation_bitwise(gpu):
+    say("physical block permutation invariance")
+    q, k, v, table, lens = make_decode_case(lengths=[1, 77, 500, 1024], q_heads=32, kv_heads=8,
+                                            head_dim=128, block_size=16, dtype=torch.bfloat16, seed=9)
+    perm = torch.randperm(k.shape[0], generator=torch.Generator().manual_seed(1))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    k2, v2 = k[perm], v[perm]                      # new block i holds old block perm[i]
+    t2 = torch.where(table >= 0, inv[table.clamp(min=0).long()].int(), table)
+    out1 = attention_amd.gqa_decode(*to_dev((q, k, v, table, lens), gpu))
+    out2 = attention_amd.gqa_decode(*to_dev((q, k2, v2, t2, lens), gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+
+
+def test_len_one_is_exact_value(gpu):
+    say("len=1 -> exactly v")
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        q, k, v, table, lens = make_decode_case(lengths=[1, 1, 1], q_heads=16, kv_heads=4,
+                                                head_dim=128, block_size=16, dtype=dtype, seed=2)
+        out = attention_amd.gqa_decode(*to_dev((q, k, v, table, lens), gpu)).cpu()
+        for b in range(3):
+            for h in range(16):
+                assert torch.equal(out[b, h], v[table[b, 0], 0, h // 4]), (dtype, b, h)
+
+
+def test_zero_and_negative_lengths_give_zeros(gpu):
+    say("len <= 0 -> zeros")
+    case = make_decode_case(lengths=[0, 5, 0], q_heads=8, kv_heads=2, head_dim=64, block_size=16,
+                            dtype=torch.float16, seed=4)
+    q, k, v, table, lens = to_dev(case, gpu)
+    lens[2] = -7
+    out = attention_amd.gqa_decode(q, k, v, table, lens)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2]) == 0
+    assert torch.count_nonzero(out[1]) > 0
+
+
+def test_batch_zero(gpu):
+    say("batch 0")
+    q = torch.empty(0, 8, 64, device=gpu, dtype=torch.float16)
+    k = torch.randn(4, 16, 2, 64, device=gpu).half()
+    out = attention_amd.gqa_decode(q, k, k.clone(), torch.empty(0, 3, dtype=torch.int32, device=gpu),
+                                   torch.empty(0, dtype=torch.int32, device=gpu))
+    assert out.shape == (0, 8, 64)
+
+
+def test_large_pool_64bit_offsets(gpu):
+    say("pool > 2^31 bytes, pages at the end")
+    hkv, d, p = 8, 128, 16
+    nblocks = (1 << 31) // (p * hkv * d * 2) + 64       # K pool just above 2 GiB
+    k = torch.empty(nblocks, p, hkv, d, device=gpu, dtype=torch.bfloat16)
+    v = torch.empty_like(k)
+    lengths = [700, 33]
+    pages = [list(range(nblocks - 44, nblocks - 44 + 44))[:44], [nblocks - 1, nblocks - 2, nblocks - 3]]
+    table = torch.full((2, 44), -1, dtype=torch.int32)
+    table[0, :44] = torch.tensor(pages[0], dtype=torch.int32)
+    table[1, :3] = torch.tensor(pages[1], dtype=torch.int32)
+    gen = torch.Generator(device=gpu).manual_seed(0)
+    used = sorted(set(pages[0] + pages[1]))
+    for blk in used:
+        k[blk].normal_(generator=gen)
+        v[blk].normal_(generator=gen)
+    q = torch.randn(2, 32, d, device=gpu, generator=gen).bfloat16()
+    lens = torch.tensor(lengths, dtype=torch.int32, device=gpu)
+    out = attention_amd.gqa_decode(q, k, v, table.to(gpu), lens)
+    torch.cuda.synchronize()
+    ref, rows = oracle_rows((q, k, v, table.to(gpu), lens))
+    assert_close(out, ref, "bf16", rows, "large pool")
+    del k, v
+    torch.cuda.empty_cache()
+
+
+# ----------------------------------------------------------------------------
+# Boundary behaviour on device tensors
+# ----------------------------------------------------------------------------
+
+def test_validation_messages_on_device(gpu):
+    say("validation messages")
+    q, k, v, table, lens = to_dev(make_decode_case(lengths=[3, 5], q_heads=8, kv_heads=2,
+                                                   head_dim=64, dtype=torch.float16), gpu)
+    with pytest.raises(RuntimeError, match="q/k/v dtype must match"):
+        attention_amd.gqa_decode(q.float(), k, v, table, lens)
+    with pytest.raises(RuntimeError, match="k_cache must be contiguous"):
+        attention_amd.gqa_decode(q, k.transpose(1, 2), v, table, lens)
+    with pytest.raises(RuntimeError, match="block_table and context_lens must be int32"):
+        attention_amd.gqa_decode(q, k, v, table.long(), lens)
+    with pytest.raises(RuntimeError, match="batch sizes must match"):
+        attention_amd.gqa_decode(q[:1], k, v, table, lens)
+    with pytest.raises(RuntimeError, match="scale must be positive and finite"):
+        attention_amd.gqa_decode(q, k, v, table, lens, scale=-1.0)
+    with pytest.raises(RuntimeError, match=r"splits must be in \[1, 65535\]"):
+        attention_amd.gqa_decode_split(q, k, v, table, lens, splits=0)
+    ws = torch.empty(2, 8, 2, 66, device=gpu)
+    with pytest.raises(RuntimeError, match="workspace requires splits > 1"):
+        attention_amd.gqa_decode_split(q, k, v, table, lens, splits=1, workspace=ws[:, :, :1].contiguous())
+    with pytest.raises(RuntimeError, match=r"workspace shape must be \[B,Hq,splits,D\+2\]"):
+        attention_amd.gqa_decode_split(q, k, v, table, lens, splits=4, workspace=ws)
+    with pytest.raises(RuntimeError, match="workspace must be contiguous float32 on q device"):
+        attention_amd.gqa_decode_split(q, k, v, table, lens, splits=2, workspace=ws.double())
+
+
+def test_cabi_matches_torch_op_bitwise(gpu):
+    say("C ABI plan path vs torch op")
+    cfg = CONFIGS["cfg2"]
+    q, k, v, table, lens = to_dev(cfg.make(device="cpu"), gpu)
+    out_op = attention_amd.gqa_decode(q, k, v, table, lens)
+    s, c = cabi.plan(32, 32, 8, 128, 16, table.shape[1],
+                     cu_count=torch.cuda.get_device_properties(gpu).multi_processor_count)
+    ws = torch.empty(32 * 32 * s * 130, device=gpu)
+    out = torch.empty_like(q)
+    rc = cabi.launch(q, k, v, table, lens, out, scale=1 / math.sqrt(128), splits=s, chunk_pages=c,
+                     workspace=ws)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_op)
+
+
+def test_repeat_calls_deterministic(gpu):
+    say("determinism across calls")
+    case = to_dev(CONFIGS["cfg3"].make(device="cpu"), gpu)
+    a = attention_amd.gqa_decode(*case)
+    b = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
