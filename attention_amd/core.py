@@ -14,11 +14,27 @@ import torch
 
 from . import _loader
 
-try:
-    _loader.load_ops()
-    _LOAD_ERROR: BaseException | None = None
-except (OSError, RuntimeError) as exc:  # missing or unloadable library
-    _LOAD_ERROR = exc
+_LOAD_ERROR: BaseException | None = None
+
+
+def _try_load() -> None:
+    global _LOAD_ERROR
+    try:
+        _loader.load_ops()
+        _LOAD_ERROR = None
+    except (OSError, RuntimeError) as exc:  # missing or unloadable library
+        _LOAD_ERROR = exc
+
+
+_try_load()
+
+
+def reload_extension() -> bool:
+    """Retries loading the op library (after an in-process build); returns
+    :func:`is_cuda_extension_loaded`."""
+    if _LOAD_ERROR is not None:
+        _try_load()
+    return _LOAD_ERROR is None
 
 
 def is_cuda_extension_loaded() -> bool:
