@@ -71,6 +71,14 @@ def lib():
             [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
             + [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                ctypes.c_void_p])
+        L.qd_gqa_decode_auto_workspace_bytes.restype = ctypes.c_size_t
+        L.qd_gqa_decode_auto_workspace_bytes.argtypes = [ctypes.c_int] * 7
+        L.qd_gqa_decode_auto.restype = ctypes.c_int
+        L.qd_gqa_decode_auto.argtypes = (
+            [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
+            + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p])
+        L.qd_gqa_decode_auto_info.restype = ctypes.c_int
+        L.qd_gqa_decode_auto_info.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int)] * 3
         _lib = L
     return _lib
 
@@ -115,3 +123,32 @@ def launch(q, k, v, table, lens, out, *, scale, splits=1, chunk_pages=0, workspa
 
 def error_string(rc: int) -> str:
     return lib().qd_error_string(rc).decode()
+
+
+def auto_workspace_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype=2):
+    return lib().qd_gqa_decode_auto_workspace_bytes(batch, q_heads, kv_heads, head_dim, block_size,
+                                                    max_pages, dtype)
+
+
+def auto_info(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype=2):
+    """(kind, waves, splits, chunk_pages); kind 1 = balanced MFMA path, 0 = split path."""
+    w, s, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    kind = lib().qd_gqa_decode_auto_info(batch, q_heads, kv_heads, head_dim, block_size, max_pages,
+                                         dtype, ctypes.byref(w), ctypes.byref(s), ctypes.byref(c))
+    return kind, w.value, s.value, c.value
+
+
+def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None):
+    """Calls qd_gqa_decode_auto on torch device tensors (no validation).
+
+    ``workspace`` (any dtype, contiguous) must hold auto_workspace_bytes()."""
+    B, Hq, D = q.shape
+    _, P, Hkv, _ = k.shape
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else 0
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    return lib().qd_gqa_decode_auto(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), lens.data_ptr(), out.data_ptr(),
+        ws_ptr, ws_bytes, B, Hq, Hkv, D, P, table.shape[1], k.shape[0], DTYPE[q.dtype], float(scale),
+        stream)

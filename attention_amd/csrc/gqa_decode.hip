@@ -1,22 +1,32 @@
 // Paged grouped-query decode attention for MI355X (gfx950 / CDNA4).
 //
-// Three kernels and the C ABI declared in include/qd_attention.h:
+// Kernels and the C ABI declared in include/qd_attention.h:
 //
-//   decode_mfma_kernel     16-bit caches, head_dim 64/128/256, block_size a
-//                          multiple of 16, group size <= 16.  One wave64 per
-//                          (sequence, kv-head, context split).  Each 16-token
-//                          group is two MFMA passes: S^T = K.Q^T with
-//                          v_mfma_f32_16x16x32 (K rows feed the A operand
-//                          straight from 16-byte global loads), then
-//                          O^T += V^T.P^T with v_mfma_f32_16x16x16 (the QK
-//                          accumulator layout is already the B operand; V is
-//                          repacked in registers with v_perm_b32).  Softmax
-//                          state stays per lane in fp32.
+//   decode_mfma_sk_kernel  the automatic path for 16-bit caches, head_dim
+//                          64/128/256, block_size a multiple of 16, group
+//                          size <= 16.  The (sequence, kv-head, 16-token
+//                          group) space of the whole batch is cut into W
+//                          equal ranges, one per resident wave, so every
+//                          wave (and every XCD) streams the same number of
+//                          K/V bytes whatever the length mix.  A range may
+//                          cover parts of several (sequence, kv-head) items;
+//                          partial items leave {m, l, acc} partials that
+//                          merge_sk_kernel combines.
+//   decode_mfma_kernel     the same per-wave pipeline over the reference's
+//                          explicit split layout: one wave per (sequence,
+//                          kv-head, split), partials [B,Hq,S,D+2].
 //   decode_generic_kernel  every other shape/dtype the reference accepts
 //                          (fp32, any head_dim in [1,256], any block_size,
 //                          any group size) on the VALU: 16 lanes per token
 //                          row, DPP row reductions.
-//   combine_kernel         log-sum-exp merge of split partials.
+//   combine_kernel         log-sum-exp merge of [B,Hq,S,D+2] partials.
+//
+// MFMA pipeline (one wave): each 16-token group is S^T = K.Q^T with
+// v_mfma_f32_16x16x32 (K rows feed the A operand straight from 16-byte
+// global loads), then O^T += V^T.P^T with v_mfma_f32_16x16x16 (the QK
+// accumulator layout is already the B operand; V is repacked in registers
+// with v_perm_b32).  Softmax state stays per lane in fp32; kPrefetch groups
+// of K/V are in flight.
 //
 // Reference semantics followed (paths relative to the reference tree):
 //   kv-head map h / (Hq/Hkv)                    csrc/cuda/dense/gqa_decode.cu:31
@@ -37,6 +47,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "qd_attention.h"
@@ -91,26 +102,34 @@ struct DecodeParams {
   void* out;
   float* ws;
   int B, Hq, Hkv, D, P, maxP, g;
-  int splits;       // launched splits per (sequence, kv-head)
+  int splits;       // launched splits per (sequence, kv-head); waves W on the stream-K path
   int chunk_pages;  // 0: ceil(npages / splits) per sequence, else fixed
   int head_chunks;  // generic kernel: ceil(g / kGenericHeads)
   int64_t num_blocks;
   float sl2;  // scale * log2(e)
+  int* meta;  // stream-K path: per item {first wave, last wave}
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Valid tokens of a sequence: lengths are clamped to the table capacity
+// max_pages*block_size so that a length beyond the table never reads past
+// the table row; a length <= 0 has none.
+__device__ __forceinline__ int clamp_len(const DecodeParams& p, int len_raw) {
+  const int64_t cap = static_cast<int64_t>(p.maxP) * p.P;
+  if (len_raw <= 0) return 0;
+  return static_cast<int>(len_raw < cap ? static_cast<int64_t>(len_raw) : cap);
+}
+
 // Token range [tb, te) of split z and the number of non-empty splits of a
-// sequence.  Lengths are clamped to the table capacity max_pages*block_size
-// so that a length beyond the table never reads past the table row.
+// sequence.
 struct ChunkInfo {
   int tb, te, nch;
 };
 
 __device__ __forceinline__ ChunkInfo chunk_info(const DecodeParams& p, int len_raw, int z) {
   ChunkInfo c{0, 0, 0};
-  const int64_t cap = static_cast<int64_t>(p.maxP) * p.P;
-  const int64_t len = len_raw < cap ? static_cast<int64_t>(len_raw) : cap;
+  const int64_t len = clamp_len(p, len_raw);
   if (len <= 0) return c;
   const int64_t npages = (len + p.P - 1) / p.P;
   const int64_t cp = p.chunk_pages > 0 ? p.chunk_pages : (npages + p.splits - 1) / p.splits;
@@ -154,6 +173,20 @@ __device__ __forceinline__ float wave_max(float x) {
 
 __device__ __forceinline__ float wave_sum(float x) {
   for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t x, int lane) {
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t t = __shfl_up(x, off);
+    if (lane >= off) x += t;
+  }
   return x;
 }
 
@@ -308,7 +341,8 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
 }
 
 // ----------------------------------------------------------------------------
-// MFMA kernel
+// ----------------------------------------------------------------------------
+// MFMA pipeline
 // ----------------------------------------------------------------------------
 
 template <int DT>
@@ -383,7 +417,7 @@ struct GroupBuf {
   int tg;          // first token of the group
 };
 
-// grid: (splits, Hkv, B), block 64 (one wave per work item).
+// One wave's decode state for one (sequence, kv-head) item.
 //
 // Lane l, r16 = l % 16, q4 = l / 16:
 //   QK  A = K      lane holds K[token r16][8 elems]     (16x16x32 A layout)
@@ -393,74 +427,70 @@ struct GroupBuf {
 //       B = P^T    lane holds P[head r16][token 4*q4+i]  == C layout of QK
 //       C = O^T    lane holds O[head r16][d = DV*(4*q4+i) + j]
 // so every lane owns one head's softmax state and a contiguous slice of
-// DV*4 output elements of that head.
+// DV*4 output elements of that head.  Heads r16 >= group size carry zero
+// queries and are never stored.
 template <int D, int DT, int PF>
-__global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
+struct MfmaWave {
   using Ops = MfmaOps<DT>;
-  constexpr int KC = D / 32;
-  constexpr int DV = D / 16;
-  constexpr int VB = DV * 2;  // bytes per lane per V row
-  const int lane = threadIdx.x;
-  const int r16 = lane & 15;
-  const int q4 = lane >> 4;
-  const int z = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  static constexpr int KC = D / 32;
+  static constexpr int DV = D / 16;
+  static constexpr int VB = DV * 2;  // bytes per lane per V row
 
-  const ChunkInfo ci = chunk_info(p, p.lens[b], z);
-  const bool direct = ci.nch <= 1;
-  if (z >= (ci.nch > 1 ? ci.nch : 1)) return;
-
-  const int g = p.g;
-  const int head = kvh * g + r16;
-  const bool head_ok = r16 < g;
-
+  int lane, r16, q4;
   u32x4 qv[KC];
-  {
+  float m_run, l_run;
+  f32x4 acc[DV];
+  // Item being processed.
+  const char* kbase;
+  const char* vbase;
+  const int32_t* trow;
+  int len;    // valid tokens of the item (or of the split)
+  int wbase;  // first page of the table window held in tblv
+  int tblv;   // table entry (wbase + lane)
+
+  __device__ void init_lane() {
+    lane = threadIdx.x;
+    r16 = lane & 15;
+    q4 = lane >> 4;
+  }
+
+  __device__ void begin_item(const DecodeParams& p, int b, int kvh, int valid_tokens) {
+    const int g = p.g;
+    const bool head_ok = r16 < g;
     const char* qp = static_cast<const char*>(p.q) +
-                     (static_cast<int64_t>(b) * p.Hq + (head_ok ? head : kvh * g)) * D * 2;
+                     (static_cast<int64_t>(b) * p.Hq + kvh * g + (head_ok ? r16 : 0)) * D * 2;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const u32x4 x = *reinterpret_cast<const u32x4*>(qp + (32 * c + 8 * q4) * 2);
       const u32x4 zero = {0u, 0u, 0u, 0u};
       qv[c] = head_ok ? x : zero;
     }
+    m_run = -INFINITY;
+    l_run = 0.f;
+#pragma unroll
+    for (int j = 0; j < DV; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh) * D * 2;
+    vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh) * D * 2;
+    trow = p.table + static_cast<int64_t>(b) * p.maxP;
+    len = valid_tokens;
   }
 
-  const int64_t row_bytes = static_cast<int64_t>(p.Hkv) * D * 2;
-  const int64_t page_bytes = row_bytes * p.P;
-  const char* kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh) * D * 2;
-  const char* vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh) * D * 2;
-  const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
-  const int32_t* trow = p.table + static_cast<int64_t>(b) * p.maxP;
-
-  const int ng = (ci.te - ci.tb + 15) >> 4;
-  const int page0 = ci.tb / p.P;  // tb is page aligned
-  // Table window: entry (page0 + wbase + lane) in lane, 64 pages at a time.
-  int wbase = 0;
-  int tblv = (lane < p.maxP - page0) ? trow[page0 + lane] : 0;
-
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  f32x4 acc[DV];
-#pragma unroll
-  for (int j = 0; j < DV; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  auto issue = [&](GroupBuf<D>& buf, int gi) {
-    const int tg = ci.tb + 16 * gi;
+  // Issues the K/V loads of group gi (tokens 16*gi .. 16*gi+15 of the item).
+  // The group lies inside one page (block_size is a multiple of 16); rows at
+  // or past `len` re-read the last valid row and are masked in compute().
+  __device__ void issue(const DecodeParams& p, GroupBuf<D>& buf, int gi) {
+    const int gpp = p.P >> 4;
+    const int tg = 16 * gi;
     buf.tg = tg;
-    const int rel = tg - ci.tb;            // token offset from the page-aligned start
-    const int pl = rel / p.P;              // page within the split
-    const int row0 = rel - pl * p.P;       // first row inside the page
-    if (pl - wbase >= 64) {
-      wbase = pl & ~63;
-      tblv = (lane < p.maxP - page0 - wbase) ? trow[page0 + wbase + lane] : 0;
-    }
+    const int pl = gi / gpp;               // page index within the item
+    const int row0 = 16 * (gi - pl * gpp);  // first row inside the page
     const int phys = clamp_page(__builtin_amdgcn_readlane(tblv, pl - wbase), p.num_blocks);
-    const int64_t off = static_cast<int64_t>(phys) * page_bytes + static_cast<int64_t>(row0) * row_bytes;
+    const int64_t row_bytes = static_cast<int64_t>(p.Hkv) * D * 2;
+    const int64_t off = (static_cast<int64_t>(phys) * p.P + row0) * row_bytes;
     const char* kp = kbase + off;
     const char* vp = vbase + off;
-    const int last = ci.te - 1 - tg;  // rows > last are past the end: reuse row `last`
+    const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
+    const int last = len - 1 - tg;  // rows > last are past the end: reuse row `last`
     const uint32_t rk = static_cast<uint32_t>(min(r16, last));
     const uint32_t ko = rk * rb32 + 16u * q4;
 #pragma unroll
@@ -470,13 +500,16 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
       const uint32_t rv = static_cast<uint32_t>(min(4 * q4 + i, last));
       buf.v[i] = load_vrow<D>(vp + rv * rb32 + VB * r16);
     }
-  };
+    // Keep each group's loads in program order relative to the other
+    // groups': the wait before a compute then covers only that group.
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
-  auto compute = [&](const GroupBuf<D>& buf) {
+  __device__ void compute(const DecodeParams& p, const GroupBuf<D>& buf) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < KC; ++c) s = Ops::qk(buf.k[c], qv[c], s);
-    const int last = ci.te - 1 - buf.tg;
+    const int last = len - 1 - buf.tg;
     float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (4 * q4 + i <= last) ? s[i] : -INFINITY;
@@ -504,32 +537,65 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
                        __builtin_amdgcn_perm(buf.v[3].w[w], buf.v[2].w[w], sel)};
       acc[j] = Ops::pv(a, pb, acc[j]);
     }
-  };
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
-  if (ng > 0) {
-    GroupBuf<D> buf[PF];
+  // Streams groups [ga, gb) of the current item.  Groups are processed in
+  // runs that stay inside one 64-page table window; the window is loaded
+  // only between runs, never while K/V loads are in flight, so waiting for
+  // it never drains the K/V prefetch.  Within a run PF groups are in
+  // flight: the steady-state loop issues unconditionally (static buffer
+  // slots, no branches around loads) so the compiler's wait counts cover
+  // only the group being consumed.
+  __device__ void run(const DecodeParams& p, int ga, int gb) {
+    const int gpp = p.P >> 4;
+    for (int g_lo = ga; g_lo < gb;) {
+      wbase = g_lo / gpp;
+      const int g_hi = min(gb, (wbase + 64) * gpp);
+      const int n = g_hi - g_lo;
+      tblv = (lane < p.maxP - wbase) ? trow[wbase + lane] : 0;
+      GroupBuf<D> buf[PF];
+      int i = 0;
+      if (n >= 2 * PF - 1) {
 #pragma unroll
-    for (int u = 0; u < PF - 1; ++u)
-      if (u < ng) issue(buf[u], u);
-    for (int gi = 0; gi < ng; gi += PF) {
+        for (int u = 0; u < PF - 1; ++u) issue(p, buf[u], g_lo + u);
+        for (; i + 2 * PF - 2 < n; i += PF) {
 #pragma unroll
-      for (int u = 0; u < PF; ++u) {
-        const int nxt = gi + u + PF - 1;
-        if (nxt < ng) issue(buf[(u + PF - 1) % PF], nxt);
-        if (gi + u < ng) compute(buf[u]);
+          for (int u = 0; u < PF; ++u) {
+            issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
+            compute(p, buf[u]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < PF - 1; ++u)
+          if (u < n) issue(p, buf[u], g_lo + u);
       }
+      // Tail: the remaining (< 2*PF-1) groups, with guarded issues.
+      for (; i < n; i += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+          if (i + u + PF - 1 < n) issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
+          if (i + u < n) compute(p, buf[u]);
+        }
+      }
+      g_lo = g_hi;
     }
   }
 
-  // Per-lane partial sums of l cover this lane's 4 tokens of every group.
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  // Softmax denominator of this lane's head (lanes of one head hold partial
+  // sums over their 4 tokens of every group).
+  __device__ float total_l() const {
+    float l = l_run + __shfl_xor(l_run, 16);
+    return l + __shfl_xor(l, 32);
+  }
 
-  if (!head_ok) return;
-  if (direct) {
+  // out[b, kvh*g + r16, :] = acc / l (zeros when l == 0), one rounding.
+  __device__ void store_direct(const DecodeParams& p, int b, int kvh, float l_tot) {
     using S = typename Elem<DT>::S;
+    if (r16 >= p.g) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + head) * D;
+    S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + kvh * p.g + r16) * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t wv[DV / 2];
@@ -547,8 +613,14 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
               u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
       }
     }
-  } else {
-    float* w = p.ws + ((static_cast<int64_t>(b) * p.Hq + head) * p.splits + z) * (D + 2);
+  }
+
+  // Partial {m (natural-log units), l, acc[D]} of this lane's head at
+  // w + head*head_stride.
+  __device__ void store_partial(const DecodeParams& p, float* w, int64_t head_stride,
+                                float l_tot) {
+    if (r16 >= p.g) return;
+    w += r16 * head_stride;
     if (q4 == 0) {
       w[0] = m_run * kLn2;
       w[1] = l_tot;
@@ -561,65 +633,242 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
         *reinterpret_cast<f32x2*>(dst + j) = f32x2{acc[j][i], acc[j + 1][i]};
     }
   }
+};
+
+// Explicit split layout.  grid: (splits, Hkv, B), block 64 (one wave per
+// (sequence, kv-head, split)).  Split z of a sequence covers whole pages
+// (chunk_info); a sequence with a single non-empty split is written
+// directly, otherwise every non-empty split writes its partial to
+// ws[b, h, z, :] for combine_kernel.
+template <int D, int DT, int PF>
+__global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
+  const int z = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const ChunkInfo ci = chunk_info(p, p.lens[b], z);
+  if (z >= (ci.nch > 1 ? ci.nch : 1)) return;
+
+  MfmaWave<D, DT, PF> wv;
+  wv.init_lane();
+  wv.begin_item(p, b, kvh, ci.te);
+  wv.run(p, ci.tb >> 4, (ci.te + 15) >> 4);  // tb is page aligned
+  const float l_tot = wv.total_l();
+  if (ci.nch <= 1) {
+    wv.store_direct(p, b, kvh, l_tot);
+  } else {
+    float* w = p.ws + ((static_cast<int64_t>(b) * p.Hq + kvh * p.g) * p.splits + z) * (D + 2);
+    wv.store_partial(p, w, static_cast<int64_t>(p.splits) * (D + 2), l_tot);
+  }
+}
+
+// 16-token groups of a sequence with `len` valid tokens.
+__device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
+  return (clamp_len(p, len_raw) + 15) >> 4;
+}
+
+// Balanced ("stream-K") layout.  grid: W = p.splits waves, block 64.
+//
+// Item i = b*Hkv + kvh has n_b = ceil(len_b/16) groups; the items are laid
+// end to end (b-major) into G = Hkv * sum_b n_b groups and wave w takes
+// groups [w*G/W, (w+1)*G/W).  For every item it touches, the wave either
+// writes the output rows directly (it holds the whole item) or writes a
+// partial for the item's g heads into slot (w + i) of p.ws, each slot
+// g*(D+2) floats; the waves holding an item's first and last groups record
+// themselves in p.meta[2i] and p.meta[2i+1].  Slot w+i is unique per (item, wave): the
+// waves of item i+1 start at or after the last wave of item i, so the
+// slots of i+1 start above those of i; W + B*Hkv slots suffice.
+// merge_sk_kernel combines slots first+i .. last+i of every split item and
+// writes the zero rows of empty sequences.
+template <int D, int DT, int PF>
+__global__ __launch_bounds__(64) void decode_mfma_sk_kernel(DecodeParams p) {
+  const int lane = threadIdx.x;
+  const int w = blockIdx.x;
+  const int W = p.splits;
+  const int B = p.B;
+
+  // Pass 1: total groups G.
+  int64_t tot = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int bb = c + lane;
+    tot += bb < B ? seq_groups(p, p.lens[bb]) : 0;
+  }
+  const int64_t G = wave_sum_i64(tot) * p.Hkv;
+  const int64_t g0 = static_cast<int64_t>(w) * G / W;
+  const int64_t g1 = static_cast<int64_t>(w + 1) * G / W;
+  if (g0 >= g1) return;
+
+  // Pass 2: the sequence holding group g0 (first b whose running group end
+  // exceeds g0) and the offset into its Hkv*n_b groups.
+  int b = B;
+  int64_t start_b = 0;
+  int64_t carry = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int bb = c + lane;
+    const int64_t n = bb < B ? static_cast<int64_t>(seq_groups(p, p.lens[bb])) * p.Hkv : 0;
+    const int64_t incl = carry + wave_incl_scan_i64(n, lane);
+    const uint64_t before = __ballot(bb < B && incl <= g0);  // sequences ending at or before g0
+    const int cnt = __popcll(before);
+    if (cnt < min(64, B - c)) {
+      b = c + cnt;
+      start_b = __shfl(incl - n, cnt);
+      break;
+    }
+    carry = __shfl(incl, 63);
+  }
+  if (b >= B) return;  // unreachable when G is consistent
+
+  MfmaWave<D, DT, PF> wv;
+  wv.init_lane();
+  int len = clamp_len(p, p.lens[b]);
+  int nb = (len + 15) >> 4;
+  int64_t local = g0 - start_b;
+  int kvh = static_cast<int>(local / nb);
+  int gi = static_cast<int>(local - static_cast<int64_t>(kvh) * nb);
+  int64_t remaining = g1 - g0;
+  const int64_t slot_floats = static_cast<int64_t>(p.g) * (D + 2);
+  while (remaining > 0) {
+    const int seg = static_cast<int>(min(static_cast<int64_t>(nb - gi), remaining));
+    wv.begin_item(p, b, kvh, len);
+    wv.run(p, gi, gi + seg);
+    const float l_tot = wv.total_l();
+    const int item = b * p.Hkv + kvh;
+    const bool first = gi == 0;
+    const bool last = gi + seg == nb;
+    if (first && last) {
+      wv.store_direct(p, b, kvh, l_tot);
+    } else {
+      wv.store_partial(p, p.ws + static_cast<int64_t>(w + item) * slot_floats, D + 2, l_tot);
+    }
+    // Every item with tokens gets both entries in every call (a whole item
+    // records first == last), so no entry survives from an earlier call.
+    if (lane == 0) {
+      if (first) p.meta[2 * item] = w;
+      if (last) p.meta[2 * item + 1] = w;
+    }
+    remaining -= seg;
+    gi = 0;
+    if (++kvh == p.Hkv && remaining > 0) {
+      kvh = 0;
+      do {
+        if (++b >= B) return;  // unreachable when G is consistent
+        len = clamp_len(p, p.lens[b]);
+        nb = (len + 15) >> 4;
+      } while (nb == 0);
+    }
+  }
 }
 
 // ----------------------------------------------------------------------------
-// Combine kernel: grid (Hq, B), block 64.
+// Log-sum-exp merge of partials {m, l, acc[D]}
 // ----------------------------------------------------------------------------
 
+// Merges `nrows` partial rows (row r at base + r*row_stride) of one head
+// into out[0..D): skip rows with l == 0 (online_softmax.cuh:18), weights
+// exp(m_r - max m), output sum_r w_r*acc_r / sum_r w_r*l_r, or zeros when
+// the total is 0 (gqa_decode.cu:84-86).  One wave; the m/l of all rows
+// (lane r) and the first kCombineBatch rows of acc are loaded together, so
+// one memory round trip covers a typical merge.
 template <int DT>
-__global__ __launch_bounds__(64) void combine_kernel(DecodeParams p) {
+__device__ __forceinline__ void merge_rows(const float* base, int64_t row_stride, int nrows, int D,
+                                           typename Elem<DT>::S* o) {
   using E = Elem<DT>;
-  using S = typename E::S;
+  constexpr int kCombineBatch = 8;
   const int lane = threadIdx.x;
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const ChunkInfo ci = chunk_info(p, p.lens[b], 0);
-  const int nch = ci.nch;
-  if (nch <= 1) return;  // written directly by the decode kernel
-  const int D = p.D;
-  const int stride = D + 2;
-  const float* base = p.ws + (static_cast<int64_t>(b) * p.Hq + h) * p.splits * stride;
-
-  // Pass 1: global max over non-empty partials (online_softmax.cuh:18 skips l == 0).
+  float accv[kCombineBatch][4];
+  auto load_rows = [&](int s0) {
+#pragma unroll
+    for (int t = 0; t < kCombineBatch; ++t) {
+      const int s = min(s0 + t, nrows - 1);
+      const float* row = base + static_cast<int64_t>(s) * row_stride + 2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = lane + 64 * r;
+        accv[t][r] = d < D ? row[d] : 0.f;
+      }
+    }
+  };
+  float lown = 0.f, mown = -INFINITY;
+  if (lane < nrows) {
+    lown = base[static_cast<int64_t>(lane) * row_stride + 1];
+    mown = base[static_cast<int64_t>(lane) * row_stride];
+  }
+  load_rows(0);
   float mloc = -INFINITY;
-  for (int s = lane; s < nch; s += 64) {
-    const float ls = base[static_cast<int64_t>(s) * stride + 1];
-    if (ls != 0.f) mloc = fmaxf(mloc, base[static_cast<int64_t>(s) * stride]);
+  for (int s = lane; s < nrows; s += 64) {
+    const float ls = s == lane ? lown : base[static_cast<int64_t>(s) * row_stride + 1];
+    const float ms = s == lane ? mown : base[static_cast<int64_t>(s) * row_stride];
+    if (ls != 0.f) mloc = fmaxf(mloc, ms);
   }
   const float M = wave_max(mloc);
   const float Mref = M == -INFINITY ? 0.f : M;
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
-  for (int s0 = 0; s0 < nch; s0 += 64) {
+  for (int s0 = 0; s0 < nrows; s0 += 64) {
     const int s = s0 + lane;
     float wgt = 0.f;
-    if (s < nch) {
-      const float ls = base[static_cast<int64_t>(s) * stride + 1];
+    if (s < nrows) {
+      const float ls = s0 == 0 ? lown : base[static_cast<int64_t>(s) * row_stride + 1];
+      const float ms = s0 == 0 ? mown : base[static_cast<int64_t>(s) * row_stride];
       if (ls != 0.f) {
-        wgt = fast_exp2((base[static_cast<int64_t>(s) * stride] - Mref) * kLog2e);
+        wgt = fast_exp2((ms - Mref) * kLog2e);
         lsum = fmaf(wgt, ls, lsum);
       }
     }
-    const int n = min(64, nch - s0);
-    for (int t = 0; t < n; ++t) {
-      const float wt = __shfl(wgt, t);
-      const float* row = base + static_cast<int64_t>(s0 + t) * stride + 2;
+    const int n = min(64, nrows - s0);
+    for (int t0 = 0; t0 < n; t0 += kCombineBatch) {
+      if (s0 + t0 > 0) load_rows(s0 + t0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = lane + 64 * r;
-        if (d < D) acc[r] = fmaf(wt, row[d], acc[r]);
+      for (int t = 0; t < kCombineBatch; ++t) {
+        const float wt = t0 + t < n ? __shfl(wgt, t0 + t) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(wt, accv[t][r], acc[r]);
       }
     }
   }
   const float L = wave_sum(lsum);
-  S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int d = lane + 64 * r;
     if (d < D) o[d] = E::from_f(L > 0.f ? acc[r] / L : 0.f);
   }
+}
+
+// Explicit split layout: grid (Hq, B), block 64; ws [B, Hq, splits, D+2].
+template <int DT>
+__global__ __launch_bounds__(64) void combine_kernel(DecodeParams p) {
+  using S = typename Elem<DT>::S;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const ChunkInfo ci = chunk_info(p, p.lens[b], 0);
+  if (ci.nch <= 1) return;  // written directly by the decode kernel
+  const int D = p.D;
+  const float* base = p.ws + (static_cast<int64_t>(b) * p.Hq + h) * p.splits * (D + 2);
+  merge_rows<DT>(base, D + 2, ci.nch, D, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
+}
+
+// Stream-K layout: grid (Hq, B), block 64.  Rows of empty sequences are
+// zero-filled here; items held whole by one wave were written directly.
+template <int DT>
+__global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
+  using S = typename Elem<DT>::S;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int D = p.D;
+  S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D;
+  if (clamp_len(p, p.lens[b]) == 0) {
+    for (int d = threadIdx.x; d < D; d += 64) o[d] = Elem<DT>::from_f(0.f);
+    return;
+  }
+  const int kvh = h / p.g;
+  const int item = b * p.Hkv + kvh;
+  const int first = p.meta[2 * item];
+  const int last = p.meta[2 * item + 1];
+  if (first == last) return;
+  const int64_t slot_floats = static_cast<int64_t>(p.g) * (D + 2);
+  const float* base = p.ws + static_cast<int64_t>(first + item) * slot_floats +
+                      static_cast<int64_t>(h - kvh * p.g) * (D + 2);
+  merge_rows<DT>(base, slot_floats, last - first + 1, D, o);
 }
 
 // ----------------------------------------------------------------------------
@@ -666,7 +915,16 @@ bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int d
   return q_heads / kv_heads <= kMfmaHeads;
 }
 
-constexpr int kPrefetch = 3;
+#ifndef QD_PREFETCH
+#define QD_PREFETCH 3
+#endif
+// 16-token groups in flight per wave (D <= 128).
+constexpr int kPrefetch = QD_PREFETCH;
+
+// Stream-K path limits: each wave scans all lengths, so the batch is capped;
+// a wave gets at least kSkMinGroups groups of the largest possible batch.
+constexpr int kSkMaxBatch = 4096;
+constexpr int64_t kSkMinGroups = 16;
 
 using KernelFn = void (*)(DecodeParams);
 
@@ -680,9 +938,20 @@ KernelFn pick_mfma(int D) {
 }
 
 template <int DT>
+KernelFn pick_mfma_sk(int D) {
+  switch (D) {
+    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch>;
+    case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch>;
+    default: return decode_mfma_sk_kernel<256, DT, 2>;
+  }
+}
+
+KernelFn pick_mfma_sk_dt(int dtype, int D) {
+  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D) : pick_mfma_sk<QD_DTYPE_BF16>(D);
+}
+
+template <int DT>
 KernelFn pick_generic(int D) {
-  const bool v16 = DT != QD_DTYPE_F32;
-  (void)v16;
   if (D <= 16) return D == 16 ? decode_generic_kernel<DT, 1, true> : decode_generic_kernel<DT, 1, false>;
   if (D <= 32) return D == 32 ? decode_generic_kernel<DT, 2, true> : decode_generic_kernel<DT, 2, false>;
   if (D <= 64) return D == 64 ? decode_generic_kernel<DT, 4, true> : decode_generic_kernel<DT, 4, false>;
@@ -698,7 +967,134 @@ KernelFn pick_combine(int dtype) {
   }
 }
 
+KernelFn pick_merge_sk(int dtype) {
+  return dtype == QD_DTYPE_F16 ? merge_sk_kernel<QD_DTYPE_F16> : merge_sk_kernel<QD_DTYPE_BF16>;
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Resident waves of `fn` on the current device: CUs x blocks per CU at
+// 64 threads, from the HIP occupancy calculator; cached per (device, fn).
+int resident_waves(KernelFn fn) {
+  struct Entry {
+    int device;
+    KernelFn fn;
+    int waves;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].device == dev && cache[i].fn == fn) return cache[i].waves;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), 64, 0) !=
+          hipSuccess ||
+      per_cu <= 0)
+    per_cu = 8;
+  (void)hipGetLastError();
+  const int waves = cus * per_cu;
+  if (used < 64) cache[used++] = Entry{dev, fn, waves};
+  return waves;
+}
+
+struct AutoPlan {
+  bool stream_k;
+  int waves;        // stream-K grid
+  int splits;       // explicit-split path
+  int chunk_pages;
+  size_t ws_bytes;
+  size_t meta_offset;  // stream-K: byte offset of the meta table in the workspace
+};
+
+// Chooses the automatic path from static shapes only.  `aligned` says
+// whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
+int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
+              int dtype, bool aligned, AutoPlan* ap) {
+  *ap = AutoPlan{false, 0, 1, 0, 0, 0};
+  if (batch <= 0) return QD_OK;
+  const int g = q_heads / kv_heads;
+  if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
+      batch <= kSkMaxBatch) {
+    const int64_t gmax = static_cast<int64_t>(batch) * kv_heads *
+                         ((static_cast<int64_t>(max_pages) * block_size + 15) / 16);
+    int64_t w = resident_waves(pick_mfma_sk_dt(dtype, head_dim));
+    const int64_t by_work = (gmax + kSkMinGroups - 1) / kSkMinGroups;
+    if (w > by_work) w = by_work;
+    if (w < 1) w = 1;
+    const int64_t items = static_cast<int64_t>(batch) * kv_heads;
+    ap->stream_k = true;
+    ap->waves = static_cast<int>(w);
+    ap->meta_offset = static_cast<size_t>((w + items) * g * (head_dim + 2)) * sizeof(float);
+    ap->ws_bytes = ap->meta_offset + static_cast<size_t>(items) * 2 * sizeof(int);
+    return QD_OK;
+  }
+  int s = 1, c = 0;
+  const int st = qd_gqa_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype,
+                                    0, &s, &c);
+  if (st != QD_OK) return st;
+  ap->splits = s;
+  ap->chunk_pages = c;
+  ap->ws_bytes = qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, s);
+  return QD_OK;
+}
+
+int check_launch_shapes(int batch, int q_heads, int kv_heads, int head_dim, int block_size,
+                        int max_pages, int64_t num_blocks, int dtype, float scale) {
+  if (batch < 0) return fail(QD_ERR_INVALID_VALUE, "batch must be >= 0");
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
+    return fail(QD_ERR_INVALID_VALUE, "Hq must be divisible by Hkv");
+  if (head_dim < 1 || head_dim > 256) return fail(QD_ERR_INVALID_VALUE, "supported head_dim is [1, 256]");
+  if (block_size <= 0 || num_blocks <= 0)
+    return fail(QD_ERR_INVALID_VALUE, "cache must have positive blocks and block_size");
+  if (max_pages <= 0) return fail(QD_ERR_INVALID_VALUE, "block_table must have at least one page");
+  if (dtype != QD_DTYPE_F32 && dtype != QD_DTYPE_F16 && dtype != QD_DTYPE_BF16)
+    return fail(QD_ERR_INVALID_VALUE, "q/k/v must be float32/float16/bfloat16");
+  if (!(isfinite(scale) && scale > 0.f)) return fail(QD_ERR_INVALID_VALUE, "scale must be positive and finite");
+  if (batch > 65535 || kv_heads > 65535 || q_heads > 65535)
+    return fail(QD_ERR_INVALID_VALUE, "batch and head counts must be <= 65535 (grid limit)");
+  return QD_OK;
+}
+
+DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* block_table, const int32_t* context_lens, void* out,
+                         void* workspace, int batch, int q_heads, int kv_heads, int head_dim,
+                         int block_size, int max_pages, int64_t num_blocks, float scale, int splits,
+                         int chunk_pages) {
+  DecodeParams prm;
+  prm.q = q;
+  prm.k = k_cache;
+  prm.v = v_cache;
+  prm.table = block_table;
+  prm.lens = context_lens;
+  prm.out = out;
+  prm.ws = static_cast<float*>(workspace);
+  prm.B = batch;
+  prm.Hq = q_heads;
+  prm.Hkv = kv_heads;
+  prm.D = head_dim;
+  prm.P = block_size;
+  prm.maxP = max_pages;
+  prm.g = q_heads / kv_heads;
+  prm.splits = splits;
+  prm.chunk_pages = chunk_pages;
+  prm.head_chunks = (prm.g + kGenericHeads - 1) / kGenericHeads;
+  prm.num_blocks = num_blocks;
+  prm.sl2 = scale * kLog2e;
+  prm.meta = nullptr;
+  return prm;
+}
+
+int launch_error() {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(static_cast<int>(e), std::string("gqa_decode kernel launch failed: ") + hipGetErrorString(e));
+  return QD_OK;
+}
 
 }  // namespace
 
@@ -824,22 +1220,13 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
                          int kv_heads, int head_dim, int block_size, int max_pages,
                          int64_t num_blocks, int dtype, float scale, int splits, int chunk_pages,
                          int flags, void* stream) {
-  if (batch < 0) return fail(QD_ERR_INVALID_VALUE, "batch must be >= 0");
-  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
-    return fail(QD_ERR_INVALID_VALUE, "Hq must be divisible by Hkv");
-  if (head_dim < 1 || head_dim > 256) return fail(QD_ERR_INVALID_VALUE, "supported head_dim is [1, 256]");
-  if (block_size <= 0 || num_blocks <= 0)
-    return fail(QD_ERR_INVALID_VALUE, "cache must have positive blocks and block_size");
-  if (max_pages <= 0) return fail(QD_ERR_INVALID_VALUE, "block_table must have at least one page");
-  if (dtype != QD_DTYPE_F32 && dtype != QD_DTYPE_F16 && dtype != QD_DTYPE_BF16)
-    return fail(QD_ERR_INVALID_VALUE, "q/k/v must be float32/float16/bfloat16");
-  if (!(isfinite(scale) && scale > 0.f)) return fail(QD_ERR_INVALID_VALUE, "scale must be positive and finite");
+  int st = check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
+                               dtype, scale);
+  if (st != QD_OK) return st;
   if (splits < 1 || splits > 65535) return fail(QD_ERR_INVALID_VALUE, "splits must be in [1, 65535]");
   if (chunk_pages < 0) return fail(QD_ERR_INVALID_VALUE, "chunk_pages must be >= 0");
   if (chunk_pages > 0 && static_cast<int64_t>(chunk_pages) * splits < max_pages)
     return fail(QD_ERR_INVALID_VALUE, "splits * chunk_pages must cover max_pages");
-  if (batch > 65535 || kv_heads > 65535)
-    return fail(QD_ERR_INVALID_VALUE, "batch and kv_heads must be <= 65535 (grid limit)");
   if (batch == 0) return QD_OK;
   if (!q || !k_cache || !v_cache || !block_table || !context_lens || !out)
     return fail(QD_ERR_INVALID_VALUE, "null tensor pointer");
@@ -849,35 +1236,17 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
       return fail(QD_ERR_INVALID_VALUE, "workspace too small for [B,Hq,splits,D+2] float32");
   }
 
-  DecodeParams prm;
-  prm.q = q;
-  prm.k = k_cache;
-  prm.v = v_cache;
-  prm.table = block_table;
-  prm.lens = context_lens;
-  prm.out = out;
-  prm.ws = workspace;
-  prm.B = batch;
-  prm.Hq = q_heads;
-  prm.Hkv = kv_heads;
-  prm.D = head_dim;
-  prm.P = block_size;
-  prm.maxP = max_pages;
-  prm.g = q_heads / kv_heads;
-  prm.splits = splits;
-  prm.chunk_pages = chunk_pages;
-  prm.head_chunks = (prm.g + kGenericHeads - 1) / kGenericHeads;
-  prm.num_blocks = num_blocks;
-  prm.sl2 = scale * kLog2e;
-
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, workspace, batch,
+                                 q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
+                                 splits, chunk_pages);
+  hipStream_t stm = static_cast<hipStream_t>(stream);
   const bool use_mfma = qd_gqa_decode_kernel_kind(q_heads, kv_heads, head_dim, block_size, dtype, flags) &&
                         aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out);
   (void)hipGetLastError();  // start from a clean error state
   if (use_mfma) {
     const KernelFn fn = dtype == QD_DTYPE_F16 ? pick_mfma<QD_DTYPE_F16>(head_dim)
                                               : pick_mfma<QD_DTYPE_BF16>(head_dim);
-    hipLaunchKernelGGL(fn, dim3(splits, kv_heads, batch), dim3(64), 0, st, prm);
+    hipLaunchKernelGGL(fn, dim3(splits, kv_heads, batch), dim3(64), 0, stm, prm);
   } else {
     KernelFn fn;
     switch (dtype) {
@@ -887,16 +1256,73 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
     }
     const int64_t gx = static_cast<int64_t>(splits) * prm.head_chunks;
     if (gx > 2147483647) return fail(QD_ERR_INVALID_VALUE, "splits * head chunks exceed the grid limit");
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(gx), kv_heads, batch), dim3(64), 0, st, prm);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(gx), kv_heads, batch), dim3(64), 0, stm, prm);
   }
   if (splits > 1) {
-    hipLaunchKernelGGL(pick_combine(dtype), dim3(q_heads, batch), dim3(64), 0, st, prm);
+    hipLaunchKernelGGL(pick_combine(dtype), dim3(q_heads, batch), dim3(64), 0, stm, prm);
   }
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    return fail(static_cast<int>(e), std::string("gqa_decode kernel launch failed: ") + hipGetErrorString(e));
-  }
-  return QD_OK;
+  return launch_error();
+}
+
+size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
+                                          int block_size, int max_pages, int dtype) {
+  if (check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, 1, dtype, 1.f) !=
+      QD_OK)
+    return 0;
+  // The larger of the two paths, so that the size does not depend on
+  // pointer alignment.
+  AutoPlan a, b;
+  if (auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &a) != QD_OK ||
+      auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, false, &b) != QD_OK)
+    return 0;
+  return a.ws_bytes > b.ws_bytes ? a.ws_bytes : b.ws_bytes;
+}
+
+int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
+                       const int32_t* block_table, const int32_t* context_lens, void* out,
+                       void* workspace, size_t workspace_bytes, int batch, int q_heads, int kv_heads,
+                       int head_dim, int block_size, int max_pages, int64_t num_blocks, int dtype,
+                       float scale, void* stream) {
+  int st = check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
+                               dtype, scale);
+  if (st != QD_OK) return st;
+  if (batch == 0) return QD_OK;
+  if (!q || !k_cache || !v_cache || !block_table || !context_lens || !out)
+    return fail(QD_ERR_INVALID_VALUE, "null tensor pointer");
+  const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out);
+  AutoPlan ap;
+  st = auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, aligned, &ap);
+  if (st != QD_OK) return st;
+  if (ap.ws_bytes > 0 && (!workspace || workspace_bytes < ap.ws_bytes || !aligned16(workspace)))
+    return fail(QD_ERR_INVALID_VALUE, "workspace smaller than qd_gqa_decode_auto_workspace_bytes()");
+  if (!ap.stream_k)
+    return qd_gqa_decode_launch(q, k_cache, v_cache, block_table, context_lens, out,
+                                static_cast<float*>(workspace), workspace_bytes, batch, q_heads, kv_heads,
+                                head_dim, block_size, max_pages, num_blocks, dtype, scale, ap.splits,
+                                ap.chunk_pages, 0, stream);
+  DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, workspace, batch,
+                                 q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
+                                 ap.waves, 0);
+  prm.meta = reinterpret_cast<int*>(static_cast<char*>(workspace) + ap.meta_offset);
+  hipStream_t stm = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim), dim3(ap.waves), dim3(64), 0, stm, prm);
+  hipLaunchKernelGGL(pick_merge_sk(dtype), dim3(q_heads, batch), dim3(64), 0, stm, prm);
+  return launch_error();
+}
+
+int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, int block_size,
+                            int max_pages, int dtype, int* waves, int* splits, int* chunk_pages) {
+  if (check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, 1, dtype, 1.f) !=
+      QD_OK)
+    return -1;
+  AutoPlan ap;
+  if (auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &ap) != QD_OK)
+    return -1;
+  if (waves) *waves = ap.stream_k ? ap.waves : 0;
+  if (splits) *splits = ap.splits;
+  if (chunk_pages) *chunk_pages = ap.chunk_pages;
+  return ap.stream_k ? 1 : 0;
 }
 
 }  // extern "C"

@@ -14,9 +14,6 @@
 #include <hip/hip_runtime_api.h>
 #include <torch/library.h>
 
-#include <mutex>
-#include <vector>
-
 #include "qd_attention.h"
 
 namespace {
@@ -44,29 +41,14 @@ qd_tensor_desc describe(const at::Tensor& t) {
   return d;
 }
 
-int cu_count(int device) {
-  static std::mutex mu;
-  static std::vector<int> cache;
-  std::lock_guard<std::mutex> lock(mu);
-  if (device >= static_cast<int>(cache.size())) cache.resize(device + 1, 0);
-  if (cache[device] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0)
-      n = 256;
-    cache[device] = n;
-  }
-  return cache[device];
-}
-
-// splits <= 0 selects the automatic plan (qd_gqa_decode_plan).
+// Explicit-split path (gqa_decode.cu:96-183 with splits >= 1).
 at::Tensor decode_impl(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                        const at::Tensor& table, const at::Tensor& lens, double scale,
                        int64_t splits, const c10::optional<at::Tensor>& workspace) {
   const qd_tensor_desc dq = describe(q), dk = describe(k), dv = describe(v), dt = describe(table),
                        dl = describe(lens);
   char msg[256];
-  int st = qd_gqa_decode_validate(&dq, &dk, &dv, &dt, &dl, scale, splits <= 0 ? 1 : splits, msg,
-                                  sizeof(msg));
+  int st = qd_gqa_decode_validate(&dq, &dk, &dv, &dt, &dl, scale, splits, msg, sizeof(msg));
   TORCH_CHECK(st == QD_OK, msg);
 
   // PyTorch-ROCm reports HIP devices as device type "cuda".
@@ -82,18 +64,14 @@ at::Tensor decode_impl(const at::Tensor& q, const at::Tensor& k, const at::Tenso
   const int maxP = static_cast<int>(table.size(1));
 
   at::Tensor ws;
-  int nsplit = static_cast<int>(splits);
-  int chunk = 0;
+  const int nsplit = static_cast<int>(splits);
+  const int chunk = 0;
   if (workspace.has_value()) {
     const qd_tensor_desc dw = describe(*workspace);
     st = qd_gqa_decode_validate_workspace(&dq, &dw, splits, msg, sizeof(msg));
     TORCH_CHECK(st == QD_OK, msg);
     ws = *workspace;
   } else {
-    if (splits <= 0) {
-      st = qd_gqa_decode_plan(B, Hq, Hkv, D, P, maxP, dq.dtype, cu_count(q.get_device()), &nsplit, &chunk);
-      TORCH_CHECK(st == QD_OK, qd_error_string(st));
-    }
     if (nsplit > 1) ws = at::empty({B, Hq, nsplit, D + 2}, q.options().dtype(at::kFloat));
   }
   const size_t ws_bytes = ws.defined() ? static_cast<size_t>(ws.numel()) * sizeof(float) : 0;
@@ -107,9 +85,37 @@ at::Tensor decode_impl(const at::Tensor& q, const at::Tensor& k, const at::Tenso
   return out;
 }
 
+// The reference's gqa_decode (gqa_decode.cu:186-188): same validation and
+// output, body replaced by the library's automatic path (balanced MFMA
+// partition or planned splits), with a per-call workspace from the caching
+// allocator.
 at::Tensor gqa_decode_hip(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                           const at::Tensor& table, const at::Tensor& lens, double scale) {
-  return decode_impl(q, k, v, table, lens, scale, 0, c10::nullopt);
+  const qd_tensor_desc dq = describe(q), dk = describe(k), dv = describe(v), dt = describe(table),
+                       dl = describe(lens);
+  char msg[256];
+  int st = qd_gqa_decode_validate(&dq, &dk, &dv, &dt, &dl, scale, 1, msg, sizeof(msg));
+  TORCH_CHECK(st == QD_OK, msg);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty_like(q);
+  if (q.size(0) == 0) return out;
+  const int B = static_cast<int>(q.size(0));
+  const int Hq = static_cast<int>(q.size(1));
+  const int D = static_cast<int>(q.size(2));
+  const int P = static_cast<int>(k.size(1));
+  const int Hkv = static_cast<int>(k.size(2));
+  const int maxP = static_cast<int>(table.size(1));
+  const size_t ws_bytes = qd_gqa_decode_auto_workspace_bytes(B, Hq, Hkv, D, P, maxP, dq.dtype);
+  at::Tensor ws;
+  if (ws_bytes > 0)
+    ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  st = qd_gqa_decode_auto(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr<int32_t>(),
+                          lens.data_ptr<int32_t>(), out.data_ptr(), ws.defined() ? ws.data_ptr() : nullptr,
+                          ws_bytes, B, Hq, Hkv, D, P, maxP, k.size(0), dq.dtype, static_cast<float>(scale),
+                          stream);
+  TORCH_CHECK(st == QD_OK, qd_error_string(st));
+  return out;
 }
 
 at::Tensor gqa_decode_split_hip(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,

@@ -181,12 +181,12 @@ def main() -> None:
                                   cfg.block_size, elem)
     scale = 1.0 / math.sqrt(cfg.head_dim)
     stream = torch.cuda.current_stream(dev)
-    cu = torch.cuda.get_device_properties(dev).multi_processor_count
-    splits, chunk = cabi.plan(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size,
-                              table.shape[1], cabi.DTYPE[q.dtype], cu)
+    auto_kind, auto_waves, splits, chunk = cabi.auto_info(cfg.batch, cfg.q_heads, cfg.kv_heads,
+                                                          cfg.head_dim, cfg.block_size, table.shape[1],
+                                                          cabi.DTYPE[q.dtype])
 
     if args.kernel == "auto" and args.splits == 0:
-        path = "torch.ops.qd_attention.gqa_decode (plan)"
+        path = "torch.ops.qd_attention.gqa_decode (automatic path)"
 
         def step(i):
             attention_amd.gqa_decode(q, ks[i % pools], vs[i % pools], table, lens)
@@ -207,8 +207,12 @@ def main() -> None:
     kind = cabi.lib().qd_gqa_decode_kernel_kind(cfg.q_heads, cfg.kv_heads, cfg.head_dim,
                                                 cfg.block_size, cabi.DTYPE[q.dtype],
                                                 cabi.QD_FLAG_FORCE_GENERIC if args.kernel == "generic" else 0)
-    kname = "decode_mfma_kernel" if kind == 1 else "decode_generic_kernel"
-    log(f"path: {path}; kernel {kname}; splits={splits} chunk_pages={chunk}; "
+    if args.kernel == "auto" and args.splits == 0 and auto_kind == 1:
+        kname, kernels = "decode_mfma_sk_kernel", "decode_mfma_sk_kernel+merge_sk_kernel"
+    else:
+        kname = "decode_mfma_kernel" if kind == 1 else "decode_generic_kernel"
+        kernels = kname + ("+combine_kernel" if splits > 1 else "")
+    log(f"path: {path}; kernels {kernels}; waves={auto_waves} splits={splits} chunk_pages={chunk}; "
         f"warmup {args.warmup}, steps {args.steps}")
     ms = time_loop(step, args.steps, args.warmup, stream)
     us = ms * 1e3
@@ -238,13 +242,14 @@ def main() -> None:
             "context_lens": (list(cfg.fixed_lengths) if cfg.fixed_lengths else
                              f"U{list(cfg.len_range)} seed {10_000 + cfg.seed}: sum {sum(lengths)}, "
                              f"min {min(lengths)}, max {max(lengths)}"),
-            "kv_pools_rotated": pools, "splits": splits, "chunk_pages": chunk, "path": path,
+            "kv_pools_rotated": pools, "path": path, "kernels": kernels,
+            "waves": auto_waves if auto_kind == 1 else None, "splits": splits, "chunk_pages": chunk,
             "algorithmic_bytes_per_call": alg_bytes,
             "flops_per_call": algorithmic_flops(lengths, cfg.q_heads, cfg.head_dim),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": kname + ("+combine_kernel" if splits > 1 else ""),
+            "kernel": kernels,
             "achieved": round(gbs, 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

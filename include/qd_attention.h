@@ -129,6 +129,39 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
 int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block_size,
                               int dtype, int flags);
 
+/* ---- Automatic path: the body of attention.gqa_decode ----------------
+ * Replaces csrc/cuda/dense/gqa_decode.cu:186-188 (gqa_decode_cuda, always
+ * one split) and the split heuristic of attention/core.py:80-96.  The
+ * partition is chosen from static shapes and the device (CU count and
+ * kernel occupancy), never from context_lens on the host:
+ *   - 16-bit caches with head_dim 64/128/256, block_size a multiple of 16,
+ *     group size <= 16 and batch <= 4096: the (sequence, kv-head,
+ *     16-token group) space is cut into one equal range per resident wave;
+ *     partial items are merged by a log-sum-exp kernel;
+ *   - otherwise: the split layout of qd_gqa_decode_launch with the plan of
+ *     qd_gqa_decode_plan.
+ * The workspace is opaque device memory, 16-byte aligned, of at least
+ * qd_gqa_decode_auto_workspace_bytes() bytes; it needs no initialisation
+ * and its contents are dead after the call's kernels finish.  Workspace
+ * size and partition depend on the current device (hipGetDevice), so query
+ * and launch with the same device current.  Does not allocate or
+ * synchronize.  Calls on different streams need different workspaces. */
+size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
+                                          int block_size, int max_pages, int dtype);
+
+int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
+                       const int32_t* block_table, const int32_t* context_lens, void* out,
+                       void* workspace, size_t workspace_bytes, int batch, int q_heads,
+                       int kv_heads, int head_dim, int block_size, int max_pages,
+                       int64_t num_blocks, int dtype, float scale, void* stream);
+
+/* Describes the automatic path's choice (assuming aligned pointers):
+ * returns 1 for the balanced MFMA path (*waves = its wave count), 0 for
+ * the split path (*splits, *chunk_pages), -1 for invalid shapes.  Any
+ * output pointer may be NULL. */
+int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, int block_size,
+                            int max_pages, int dtype, int* waves, int* splits, int* chunk_pages);
+
 #ifdef __cplusplus
 }
 #endif

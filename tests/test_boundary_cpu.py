@@ -193,7 +193,7 @@ def _launch_args(**over):
     (dict(splits=0), "splits must be in [1, 65535]"),
     (dict(splits=4, chunk=2), "splits * chunk_pages must cover max_pages"),
     (dict(splits=4), "workspace too small for [B,Hq,splits,D+2] float32"),
-    (dict(B=70000), "batch and kv_heads must be <= 65535 (grid limit)"),
+    (dict(B=70000), "batch and head counts must be <= 65535 (grid limit)"),
     (dict(q=None), "null tensor pointer"),
 ])
 def test_launch_argument_errors(over, msg):

@@ -330,19 +330,72 @@ def test_validation_messages_on_device(gpu):
 
 
 def test_cabi_matches_torch_op_bitwise(gpu):
-    say("C ABI plan path vs torch op")
+    say("C ABI automatic path vs torch op")
     cfg = CONFIGS["cfg2"]
     q, k, v, table, lens = to_dev(cfg.make(device="cpu"), gpu)
     out_op = attention_amd.gqa_decode(q, k, v, table, lens)
-    s, c = cabi.plan(32, 32, 8, 128, 16, table.shape[1],
-                     cu_count=torch.cuda.get_device_properties(gpu).multi_processor_count)
-    ws = torch.empty(32 * 32 * s * 130, device=gpu)
+    nbytes = cabi.auto_workspace_bytes(32, 32, 8, 128, 16, table.shape[1], cabi.DTYPE[q.dtype])
+    ws = torch.empty(max(1, nbytes), device=gpu, dtype=torch.uint8)
     out = torch.empty_like(q)
-    rc = cabi.launch(q, k, v, table, lens, out, scale=1 / math.sqrt(128), splits=s, chunk_pages=c,
-                     workspace=ws)
+    rc = cabi.auto_launch(q, k, v, table, lens, out, scale=1 / math.sqrt(128), workspace=ws)
     assert rc == 0, cabi.error_string(rc)
     torch.cuda.synchronize()
     assert torch.equal(out, out_op)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{DT_NAME[s[0]]}-Hq{s[1]}-Hkv{s[2]}-D{s[3]}-P{s[4]}")
+def test_shapes_auto_cabi(gpu, shape):
+    dtype, hq, hkv, d, p, lengths = shape
+    kind, waves, splits, chunk = cabi.auto_info(len(lengths), hq, hkv, d, p,
+                                                max(1, -(-max(lengths) // p)), cabi.DTYPE[dtype])
+    say(f"auto shape {shape[1:5]} {DT_NAME[dtype]} kind={kind} waves={waves} splits={splits}")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
+                                   block_size=p, dtype=dtype, seed=8), gpu)
+    q, k, v, table, lens = case
+    ref, rows = oracle_rows(case)
+    nbytes = cabi.auto_workspace_bytes(q.shape[0], hq, hkv, d, p, table.shape[1], cabi.DTYPE[dtype])
+    ws = torch.full((max(16, nbytes),), 0xFF, device=gpu, dtype=torch.uint8)  # NaN / -1 poison
+    out = torch.full_like(q, float("nan"))
+    rc = cabi.auto_launch(q, k, v, table, lens, out, scale=1 / math.sqrt(d), workspace=ws)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert_close(out, ref, DT_NAME[dtype], rows, "auto")
+
+
+def test_auto_workspace_reuse_across_length_mixes(gpu):
+    """One workspace, three calls whose lengths split the items differently:
+    an item held whole by one wave in a later call must not be merged from
+    an earlier call's leftovers."""
+    hq, hkv, d, p = 32, 8, 128, 16
+    mixes = [[4096, 4096, 1, 3000, 17, 2048], [16, 4096, 4096, 1, 0, 5000], [300, 1, 1, 1, 1, 6000]]
+    maxp = -(-max(max(m) for m in mixes) // p)
+    nbytes = cabi.auto_workspace_bytes(6, hq, hkv, d, p, maxp, cabi.DTYPE[torch.bfloat16])
+    ws = torch.full((nbytes,), 0x7F, device=gpu, dtype=torch.uint8)
+    for i, lengths in enumerate(mixes):
+        say(f"workspace reuse mix {i}: {lengths}")
+        q, k, v, table, lens = make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
+                                                block_size=p, dtype=torch.bfloat16, seed=20 + i)
+        tpad = torch.full((6, maxp), -1, dtype=torch.int32)
+        tpad[:, :table.shape[1]] = table
+        case = to_dev((q, k, v, tpad, lens), gpu)
+        ref, rows = oracle_rows(case)
+        out = torch.full_like(case[0], float("nan"))
+        rc = cabi.auto_launch(*case, out, scale=1 / math.sqrt(d), workspace=ws)
+        assert rc == 0, cabi.error_string(rc)
+        torch.cuda.synchronize()
+        assert_close(out, ref, "bf16", rows, f"mix {i}")
+
+
+@pytest.mark.parametrize("lengths", [[1] * 300, [0] * 5 + [33], [16] * 64, [1, 0, 2, 0, 15, 16, 17]],
+                         ids=["ones", "zeros-then-one", "one-group-each", "tiny-mix"])
+def test_auto_tiny_items(gpu, lengths):
+    say(f"auto tiny items {lengths[:8]}... (B={len(lengths)})")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=16, kv_heads=2, head_dim=64, block_size=16,
+                                   dtype=torch.float16, seed=31), gpu)
+    ref, rows = oracle_rows(case)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    assert_close(out, ref, "f16", rows, "tiny")
 
 
 def test_repeat_calls_deterministic(gpu):
