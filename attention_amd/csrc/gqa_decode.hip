@@ -4,14 +4,15 @@
 //
 //   decode_mfma_sk_kernel  the automatic path for 16-bit caches, head_dim
 //                          64/128/256, block_size a multiple of 16, group
-//                          size <= 16.  The (sequence, kv-head, 16-token
-//                          group) space of the whole batch is cut into W
-//                          equal ranges, one per resident wave, so every
-//                          wave (and every XCD) streams the same number of
-//                          K/V bytes whatever the length mix.  A range may
-//                          cover parts of several (sequence, kv-head) items;
-//                          partial items leave {m, l, acc} partials that
-//                          merge_sk_kernel combines.
+//                          size <= 16.  The (sequence, 16-token group)
+//                          space of the whole batch is cut into W equal
+//                          ranges, one per resident workgroup, so every
+//                          workgroup (and every XCD) streams the same number
+//                          of K/V bytes whatever the length mix; the waves of
+//                          a workgroup cover all kv-heads of the same tokens.
+//                          A sequence split across workgroups leaves
+//                          {m, l, acc} partials that merge_sk_kernel
+//                          combines.
 //   decode_mfma_kernel     the same per-wave pipeline over the reference's
 //                          explicit split layout: one wave per (sequence,
 //                          kv-head, split), partials [B,Hq,S,D+2].
@@ -107,7 +108,9 @@ struct DecodeParams {
   int head_chunks;  // generic kernel: ceil(g / kGenericHeads)
   int64_t num_blocks;
   float sl2;  // scale * log2(e)
-  int* meta;  // stream-K path: per item {first wave, last wave}
+  int* counters;  // stream-K path: control region (zero between calls)
+  int* meta;      // stream-K path: per sequence {first workgroup, workgroups}
+  int wg_waves;   // stream-K path: waves per workgroup
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -179,6 +182,30 @@ __device__ __forceinline__ float wave_sum(float x) {
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
   for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
   return x;
+}
+
+// Partials exchanged between workgroups inside one kernel are written and
+// read with agent-scope relaxed atomic accesses (the sc1 cache policy):
+// each access is coherent across the XCDs' separate L2s by itself, so no
+// cache-wide writeback or invalidate (an agent-scope fence) is needed.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void store_agent2(float* p, f32x2 v) {  // p 8-byte aligned
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ f32x2 load_agent2(const float* p) {  // p 8-byte aligned
+  return __builtin_bit_cast(f32x2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
 }
 
 // Inclusive prefix sum over the 64 lanes.
@@ -388,17 +415,28 @@ struct VRow {
   uint32_t w[kWords];
 };
 
+// K/V are streamed once per call: nontemporal loads (the NT cache policy)
+// keep them from displacing reusable lines and measure ~15% more read
+// bandwidth than plain loads on MI355X.
+__device__ __forceinline__ u32x4 stream_load16(const char* ptr) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
+}
+
+__device__ __forceinline__ u32x2 stream_load8(const char* ptr) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(ptr));
+}
+
 template <int D>
 __device__ __forceinline__ VRow<D> load_vrow(const char* ptr) {
   VRow<D> r;
   if constexpr (VRow<D>::kWords == 2) {
-    const u32x2 x = *reinterpret_cast<const u32x2*>(ptr);
+    const u32x2 x = stream_load8(ptr);
     r.w[0] = x[0];
     r.w[1] = x[1];
   } else {
 #pragma unroll
     for (int i = 0; i < VRow<D>::kWords / 4; ++i) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(ptr + 16 * i);
+      const u32x4 x = stream_load16(ptr + 16 * i);
       r.w[4 * i + 0] = x[0];
       r.w[4 * i + 1] = x[1];
       r.w[4 * i + 2] = x[2];
@@ -412,15 +450,34 @@ __device__ __forceinline__ VRow<D> load_vrow(const char* ptr) {
 template <int D>
 struct GroupBuf {
   static constexpr int KC = D / 32;
-  u32x4 k[KC];     // K row (lane%16) at elements 32c + 8*(lane/16) .. +8
+  u32x4 k[KC];     // K, coalesced: 16 bytes of row KTile<D>::row(c, lane)
   VRow<D> v[4];    // V rows 4*(lane/16)+i, elements (D/16)*(lane%16) ..
   int tg;          // first token of the group
+};
+
+// K of one 16-token group moves HBM -> VGPR -> LDS -> VGPR.  The global
+// loads are coalesced (each instruction reads whole 2*D-byte row segments,
+// 1 KB per instruction), which streams measurably faster than loading the
+// MFMA operand layout directly (16 rows x 64 bytes per instruction).  The
+// LDS tile re-reads it in the MFMA A layout.  Rows are padded by 16 bytes
+// so that both the row-major writes and the operand reads touch 64
+// distinct banks per 16 lanes (D = 64, 128, 256).
+template <int D>
+struct KTile {
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kStride = kRowBytes + 16;
+  static constexpr int kLanesPerRow = kRowBytes / 16;  // 8, 16, 32
+  static constexpr int kRowsPerLoad = 64 / kLanesPerRow;
+  static constexpr int kBytes = 16 * kStride;
+  __device__ static int row(int c, int lane) { return c * kRowsPerLoad + lane / kLanesPerRow; }
+  __device__ static int col_bytes(int lane) { return 16 * (lane % kLanesPerRow); }
 };
 
 // One wave's decode state for one (sequence, kv-head) item.
 //
 // Lane l, r16 = l % 16, q4 = l / 16:
-//   QK  A = K      lane holds K[token r16][8 elems]     (16x16x32 A layout)
+//   QK  A = K      lane holds K[token r16][8 elems]     (16x16x32 A layout,
+//                  read from the LDS tile)
 //       B = Q^T    lane holds Q[head  r16][same elems]
 //       C = S^T    lane holds S[token 4*q4+i][head r16], i = 0..3
 //   PV  A = V^T    lane holds V[token 4*q4+i][d = DV*r16 + j], i = 0..3
@@ -449,7 +506,7 @@ struct MfmaWave {
   int tblv;   // table entry (wbase + lane)
 
   __device__ void init_lane() {
-    lane = threadIdx.x;
+    lane = threadIdx.x & 63;  // lane within the wave (workgroups may hold several)
     r16 = lane & 15;
     q4 = lane >> 4;
   }
@@ -491,10 +548,12 @@ struct MfmaWave {
     const char* vp = vbase + off;
     const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
     const int last = len - 1 - tg;  // rows > last are past the end: reuse row `last`
-    const uint32_t rk = static_cast<uint32_t>(min(r16, last));
-    const uint32_t ko = rk * rb32 + 16u * q4;
+    const uint32_t kcol = static_cast<uint32_t>(KTile<D>::col_bytes(lane));
 #pragma unroll
-    for (int c = 0; c < KC; ++c) buf.k[c] = *reinterpret_cast<const u32x4*>(kp + ko + 64 * c);
+    for (int c = 0; c < KC; ++c) {
+      const uint32_t rk = static_cast<uint32_t>(min(KTile<D>::row(c, lane), last));
+      buf.k[c] = stream_load16(kp + rk * rb32 + kcol);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t rv = static_cast<uint32_t>(min(4 * q4 + i, last));
@@ -505,10 +564,20 @@ struct MfmaWave {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  __device__ void compute(const DecodeParams& p, const GroupBuf<D>& buf) {
+  __device__ void compute(const DecodeParams& p, const GroupBuf<D>& buf, char* ktile) {
+    // Transpose K through LDS into the A layout: lane (r16, q4), chunk c
+    // holds row r16, bytes [64c + 16q4, +16).
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      *reinterpret_cast<u32x4*>(ktile + KTile<D>::row(c, lane) * KTile<D>::kStride +
+                                KTile<D>::col_bytes(lane)) = buf.k[c];
+    u32x4 ka[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      ka[c] = *reinterpret_cast<const u32x4*>(ktile + r16 * KTile<D>::kStride + 64 * c + 16 * q4);
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < KC; ++c) s = Ops::qk(buf.k[c], qv[c], s);
+    for (int c = 0; c < KC; ++c) s = Ops::qk(ka[c], qv[c], s);
     const int last = len - 1 - buf.tg;
     float x[4];
 #pragma unroll
@@ -547,7 +616,7 @@ struct MfmaWave {
   // flight: the steady-state loop issues unconditionally (static buffer
   // slots, no branches around loads) so the compiler's wait counts cover
   // only the group being consumed.
-  __device__ void run(const DecodeParams& p, int ga, int gb) {
+  __device__ void run(const DecodeParams& p, int ga, int gb, char* ktile) {
     const int gpp = p.P >> 4;
     for (int g_lo = ga; g_lo < gb;) {
       wbase = g_lo / gpp;
@@ -563,7 +632,7 @@ struct MfmaWave {
 #pragma unroll
           for (int u = 0; u < PF; ++u) {
             issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
-            compute(p, buf[u]);
+            compute(p, buf[u], ktile);
           }
         }
       } else {
@@ -576,7 +645,7 @@ struct MfmaWave {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
           if (i + u + PF - 1 < n) issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
-          if (i + u < n) compute(p, buf[u]);
+          if (i + u < n) compute(p, buf[u], ktile);
         }
       }
       g_lo = g_hi;
@@ -616,21 +685,32 @@ struct MfmaWave {
   }
 
   // Partial {m (natural-log units), l, acc[D]} of this lane's head at
-  // w + head*head_stride.
-  __device__ void store_partial(const DecodeParams& p, float* w, int64_t head_stride,
-                                float l_tot) {
+  // w + head*head_stride (head_stride even).  AGENT: coherent stores for a
+  // reader in another workgroup of the same kernel.
+  template <bool AGENT>
+  __device__ void store_partial(const DecodeParams& p, float* w, int64_t head_stride, float l_tot) {
     if (r16 >= p.g) return;
     w += r16 * head_stride;
     if (q4 == 0) {
-      w[0] = m_run * kLn2;
-      w[1] = l_tot;
+      if constexpr (AGENT) {
+        store_agent(w, m_run * kLn2);
+        store_agent(w + 1, l_tot);
+      } else {
+        w[0] = m_run * kLn2;
+        w[1] = l_tot;
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float* dst = w + 2 + DV * (4 * q4 + i);
 #pragma unroll
-      for (int j = 0; j < DV; j += 2)
-        *reinterpret_cast<f32x2*>(dst + j) = f32x2{acc[j][i], acc[j + 1][i]};
+      for (int j = 0; j < DV; j += 2) {
+        const f32x2 v = {acc[j][i], acc[j + 1][i]};
+        if constexpr (AGENT)
+          store_agent2(dst + j, v);
+        else
+          *reinterpret_cast<f32x2*>(dst + j) = v;
+      }
     }
   }
 };
@@ -648,16 +728,17 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
   const ChunkInfo ci = chunk_info(p, p.lens[b], z);
   if (z >= (ci.nch > 1 ? ci.nch : 1)) return;
 
+  __shared__ __align__(16) char ktile[KTile<D>::kBytes];
   MfmaWave<D, DT, PF> wv;
   wv.init_lane();
   wv.begin_item(p, b, kvh, ci.te);
-  wv.run(p, ci.tb >> 4, (ci.te + 15) >> 4);  // tb is page aligned
+  wv.run(p, ci.tb >> 4, (ci.te + 15) >> 4, ktile);  // tb is page aligned
   const float l_tot = wv.total_l();
   if (ci.nch <= 1) {
     wv.store_direct(p, b, kvh, l_tot);
   } else {
     float* w = p.ws + ((static_cast<int64_t>(b) * p.Hq + kvh * p.g) * p.splits + z) * (D + 2);
-    wv.store_partial(p, w, static_cast<int64_t>(p.splits) * (D + 2), l_tot);
+    wv.template store_partial<false>(p, w, static_cast<int64_t>(p.splits) * (D + 2), l_tot);
   }
 }
 
@@ -666,25 +747,95 @@ __device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
   return (clamp_len(p, len_raw) + 15) >> 4;
 }
 
-// Balanced ("stream-K") layout.  grid: W = p.splits waves, block 64.
+// Merges the partials of the g heads of one kv-head, in place of the
+// reference's merge kernel (gqa_decode.cu:74-87): rows r = 0..nrows-1 at
+// base + r*row_stride, head j at + j*(D+2), each {m (natural log), l,
+// acc[D]}.  Rows are folded in order with SoftmaxState::merge
+// (online_softmax.cuh:17-24): a row with l == 0 is skipped, the running
+// state is rescaled by exp(m - max).  Output acc/l rounded once, zeros when
+// l == 0 (gqa_decode.cu:84-86).  One wave: 16 lanes per head, D/16
+// elements per lane, 4 heads per pass; the rows are loaded 8 at a time so
+// that one memory round trip covers a typical merge.
+template <int D, int DT>
+__device__ __forceinline__ void merge_kv_group(const float* base, int64_t row_stride, int nrows, int g,
+                                               typename Elem<DT>::S* out) {
+  // Partials come from an earlier kernel on the same stream: plain loads.
+  using E = Elem<DT>;
+  constexpr int EPL = D / 16;
+  constexpr int kBatch = 8;
+  const int lane = threadIdx.x & 63;
+  const int j4 = lane >> 4;
+  const int c16 = lane & 15;
+  for (int h0 = 0; h0 < g; h0 += 4) {
+    const int h = h0 + j4;
+    const float* hb = base + static_cast<int64_t>(h < g ? h : 0) * (D + 2);
+    float M = -INFINITY, L = 0.f;
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+    for (int s0 = 0; s0 < nrows; s0 += kBatch) {
+      float ms[kBatch], ls[kBatch], av[kBatch][EPL];
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        const float* row = hb + static_cast<int64_t>(min(s0 + t, nrows - 1)) * row_stride;
+        ms[t] = row[0];
+        ls[t] = row[1];
+        // Rows are D+2 floats (D even): acc is 8-byte aligned.
+#pragma unroll
+        for (int e = 0; e < EPL; e += 2) {
+          const f32x2 x = *reinterpret_cast<const f32x2*>(row + 2 + c16 * EPL + e);
+          av[t][e] = x[0];
+          av[t][e + 1] = x[1];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        if (s0 + t >= nrows || ls[t] == 0.f) continue;
+        const float mn = fmaxf(M, ms[t]);
+        const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
+        const float bb = fast_exp2((ms[t] - mn) * kLog2e);
+        L = a * L + bb * ls[t];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = a * acc[e] + bb * av[t][e];
+        M = mn;
+      }
+    }
+    if (h < g) {
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      typename E::S* o = out + static_cast<int64_t>(h) * D + c16 * EPL;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[e] = E::from_f(L > 0.f ? acc[e] * inv : 0.f);
+    }
+  }
+}
+
+constexpr int kMaxWgWaves = 8;
+
+// Balanced ("stream-K") layout.  grid: W = p.splits workgroups of
+// p.wg_waves waves; wave j of a workgroup serves kv-heads j, j + wg_waves,
+// ... so that a workgroup reads whole cache rows (all kv-heads of a token)
+// at once, which streams faster from HBM than kv-head slices read at
+// unrelated times.
 //
-// Item i = b*Hkv + kvh has n_b = ceil(len_b/16) groups; the items are laid
-// end to end (b-major) into G = Hkv * sum_b n_b groups and wave w takes
-// groups [w*G/W, (w+1)*G/W).  For every item it touches, the wave either
-// writes the output rows directly (it holds the whole item) or writes a
-// partial for the item's g heads into slot (w + i) of p.ws, each slot
-// g*(D+2) floats; the waves holding an item's first and last groups record
-// themselves in p.meta[2i] and p.meta[2i+1].  Slot w+i is unique per (item, wave): the
-// waves of item i+1 start at or after the last wave of item i, so the
-// slots of i+1 start above those of i; W + B*Hkv slots suffice.
-// merge_sk_kernel combines slots first+i .. last+i of every split item and
-// writes the zero rows of empty sequences.
+// Sequence b has n_b = ceil(len_b/16) groups; the sequences are laid end to
+// end into G = sum_b n_b groups and workgroup w takes groups
+// [w*G/W, (w+1)*G/W).  For every sequence it touches, the workgroup either
+// writes the output rows directly (it holds the whole sequence) or writes a
+// partial for all Hq heads into slot (w + b) of the workspace (Hq*(D+2)
+// floats per slot; the slot is unique per (sequence, workgroup) because the
+// workgroups of sequence b+1 start at or after the last one of b, so
+// W + B slots suffice).  merge_sk_kernel combines the slots of every split
+// sequence.  Rows of empty sequences are zero-filled by workgroup b % W.
 template <int D, int DT, int PF>
-__global__ __launch_bounds__(64) void decode_mfma_sk_kernel(DecodeParams p) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kMaxWgWaves) void decode_mfma_sk_kernel(DecodeParams p) {
+  using S = typename Elem<DT>::S;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = p.wg_waves;
   const int w = blockIdx.x;
   const int W = p.splits;
   const int B = p.B;
+  __shared__ __align__(16) char ktile[kMaxWgWaves][KTile<D>::kBytes];
 
   // Pass 1: total groups G.
   int64_t tot = 0;
@@ -692,63 +843,74 @@ __global__ __launch_bounds__(64) void decode_mfma_sk_kernel(DecodeParams p) {
     const int bb = c + lane;
     tot += bb < B ? seq_groups(p, p.lens[bb]) : 0;
   }
-  const int64_t G = wave_sum_i64(tot) * p.Hkv;
+  const int64_t G = wave_sum_i64(tot);
+
+  // Zero rows of empty sequences (no workgroup holds them).
+  for (int bb = w; bb < B; bb += W) {
+    if (seq_groups(p, p.lens[bb]) == 0) {
+      S* o = static_cast<S*>(p.out) + static_cast<int64_t>(bb) * p.Hq * p.D;
+      for (int i = threadIdx.x; i < p.Hq * p.D; i += 64 * nw) o[i] = Elem<DT>::from_f(0.f);
+    }
+  }
+
   const int64_t g0 = static_cast<int64_t>(w) * G / W;
   const int64_t g1 = static_cast<int64_t>(w + 1) * G / W;
-  if (g0 >= g1) return;
+  if (g0 >= g1) return;  // uniform across the workgroup
 
-  // Pass 2: the sequence holding group g0 (first b whose running group end
-  // exceeds g0) and the offset into its Hkv*n_b groups.
+  // Pass 2: the sequence holding group g0 and its first group gs.
   int b = B;
-  int64_t start_b = 0;
+  int64_t gs = 0;
   int64_t carry = 0;
   for (int c = 0; c < B; c += 64) {
     const int bb = c + lane;
-    const int64_t n = bb < B ? static_cast<int64_t>(seq_groups(p, p.lens[bb])) * p.Hkv : 0;
+    const int64_t n = bb < B ? static_cast<int64_t>(seq_groups(p, p.lens[bb])) : 0;
     const int64_t incl = carry + wave_incl_scan_i64(n, lane);
     const uint64_t before = __ballot(bb < B && incl <= g0);  // sequences ending at or before g0
     const int cnt = __popcll(before);
     if (cnt < min(64, B - c)) {
       b = c + cnt;
-      start_b = __shfl(incl - n, cnt);
+      gs = __shfl(incl - n, cnt);
       break;
     }
     carry = __shfl(incl, 63);
   }
   if (b >= B) return;  // unreachable when G is consistent
 
+  // Workgroup holding flattened group x.
+  auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * W - 1) / G); };
+
   MfmaWave<D, DT, PF> wv;
   wv.init_lane();
   int len = clamp_len(p, p.lens[b]);
   int nb = (len + 15) >> 4;
-  int64_t local = g0 - start_b;
-  int kvh = static_cast<int>(local / nb);
-  int gi = static_cast<int>(local - static_cast<int64_t>(kvh) * nb);
+  int gi = static_cast<int>(g0 - gs);
   int64_t remaining = g1 - g0;
-  const int64_t slot_floats = static_cast<int64_t>(p.g) * (D + 2);
+  const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
   while (remaining > 0) {
     const int seg = static_cast<int>(min(static_cast<int64_t>(nb - gi), remaining));
-    wv.begin_item(p, b, kvh, len);
-    wv.run(p, gi, gi + seg);
-    const float l_tot = wv.total_l();
-    const int item = b * p.Hkv + kvh;
-    const bool first = gi == 0;
-    const bool last = gi + seg == nb;
-    if (first && last) {
-      wv.store_direct(p, b, kvh, l_tot);
-    } else {
-      wv.store_partial(p, p.ws + static_cast<int64_t>(w + item) * slot_floats, D + 2, l_tot);
+    const bool whole = gi == 0 && gi + seg == nb;
+    float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
+    for (int kvh = wid; kvh < p.Hkv; kvh += nw) {
+      wv.begin_item(p, b, kvh, len);
+      wv.run(p, gi, gi + seg, ktile[wid]);
+      const float l_tot = wv.total_l();
+      if (whole)
+        wv.store_direct(p, b, kvh, l_tot);
+      else
+        wv.template store_partial<false>(p, slot + static_cast<int64_t>(kvh) * p.g * (D + 2), D + 2, l_tot);
     }
-    // Every item with tokens gets both entries in every call (a whole item
-    // records first == last), so no entry survives from an earlier call.
-    if (lane == 0) {
-      if (first) p.meta[2 * item] = w;
-      if (last) p.meta[2 * item + 1] = w;
+    // The workgroup holding a sequence's first group records which
+    // workgroups span it, for merge_sk_kernel (also for a whole sequence, so
+    // that nothing from an earlier call survives).
+    if (gi == 0 && threadIdx.x == 0) {
+      const int first = wg_of(gs);
+      p.meta[2 * b] = first;
+      p.meta[2 * b + 1] = wg_of(gs + nb - 1) - first + 1;
     }
     remaining -= seg;
-    gi = 0;
-    if (++kvh == p.Hkv && remaining > 0) {
-      kvh = 0;
+    if (remaining > 0) {
+      gs += nb;
+      gi = 0;
       do {
         if (++b >= B) return;  // unreachable when G is consistent
         len = clamp_len(p, p.lens[b]);
@@ -756,6 +918,23 @@ __global__ __launch_bounds__(64) void decode_mfma_sk_kernel(DecodeParams p) {
       } while (nb == 0);
     }
   }
+}
+
+// Stream-K merge: grid (Hkv, B), block 64; one wave merges the g heads of
+// one kv-head of one sequence from slots first+b .. first+b+nwg-1.
+template <int D, int DT>
+__global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
+  using S = typename Elem<DT>::S;
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  if (clamp_len(p, p.lens[b]) == 0) return;  // zero-filled by the decode kernel
+  const int first = p.meta[2 * b];
+  const int nwg = p.meta[2 * b + 1];
+  if (nwg <= 1) return;  // written directly
+  const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
+  const int64_t h0 = static_cast<int64_t>(kvh) * p.g;
+  merge_kv_group<D, DT>(p.ws + static_cast<int64_t>(first + b) * slot_floats + h0 * (D + 2), slot_floats, nwg,
+                        p.g, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h0) * D);
 }
 
 // ----------------------------------------------------------------------------
@@ -847,30 +1026,6 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeParams p) {
   merge_rows<DT>(base, D + 2, ci.nch, D, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
 }
 
-// Stream-K layout: grid (Hq, B), block 64.  Rows of empty sequences are
-// zero-filled here; items held whole by one wave were written directly.
-template <int DT>
-__global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
-  using S = typename Elem<DT>::S;
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int D = p.D;
-  S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D;
-  if (clamp_len(p, p.lens[b]) == 0) {
-    for (int d = threadIdx.x; d < D; d += 64) o[d] = Elem<DT>::from_f(0.f);
-    return;
-  }
-  const int kvh = h / p.g;
-  const int item = b * p.Hkv + kvh;
-  const int first = p.meta[2 * item];
-  const int last = p.meta[2 * item + 1];
-  if (first == last) return;
-  const int64_t slot_floats = static_cast<int64_t>(p.g) * (D + 2);
-  const float* base = p.ws + static_cast<int64_t>(first + item) * slot_floats +
-                      static_cast<int64_t>(h - kvh * p.g) * (D + 2);
-  merge_rows<DT>(base, slot_floats, last - first + 1, D, o);
-}
-
 // ----------------------------------------------------------------------------
 // Host side
 // ----------------------------------------------------------------------------
@@ -924,7 +1079,16 @@ constexpr int kPrefetch = QD_PREFETCH;
 // Stream-K path limits: each wave scans all lengths, so the batch is capped;
 // a wave gets at least kSkMinGroups groups of the largest possible batch.
 constexpr int kSkMaxBatch = 4096;
-constexpr int64_t kSkMinGroups = 16;
+#ifndef QD_SK_MIN_GROUPS
+#define QD_SK_MIN_GROUPS 16
+#endif
+constexpr int64_t kSkMinGroups = QD_SK_MIN_GROUPS;
+// Waves launched per resident wave slot.  Above 1 the hardware dispatcher
+// hands the later waves to whichever CUs finish first.
+#ifndef QD_SK_OVERSUB
+#define QD_SK_OVERSUB 1
+#endif
+constexpr int kSkOversubscribe = QD_SK_OVERSUB;
 
 using KernelFn = void (*)(DecodeParams);
 
@@ -951,6 +1115,19 @@ KernelFn pick_mfma_sk_dt(int dtype, int D) {
 }
 
 template <int DT>
+KernelFn pick_merge_sk(int D) {
+  switch (D) {
+    case 64: return merge_sk_kernel<64, DT>;
+    case 128: return merge_sk_kernel<128, DT>;
+    default: return merge_sk_kernel<256, DT>;
+  }
+}
+
+KernelFn pick_merge_sk_dt(int dtype, int D) {
+  return dtype == QD_DTYPE_F16 ? pick_merge_sk<QD_DTYPE_F16>(D) : pick_merge_sk<QD_DTYPE_BF16>(D);
+}
+
+template <int DT>
 KernelFn pick_generic(int D) {
   if (D <= 16) return D == 16 ? decode_generic_kernel<DT, 1, true> : decode_generic_kernel<DT, 1, false>;
   if (D <= 32) return D == 32 ? decode_generic_kernel<DT, 2, true> : decode_generic_kernel<DT, 2, false>;
@@ -967,19 +1144,17 @@ KernelFn pick_combine(int dtype) {
   }
 }
 
-KernelFn pick_merge_sk(int dtype) {
-  return dtype == QD_DTYPE_F16 ? merge_sk_kernel<QD_DTYPE_F16> : merge_sk_kernel<QD_DTYPE_BF16>;
-}
-
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// Resident waves of `fn` on the current device: CUs x blocks per CU at
-// 64 threads, from the HIP occupancy calculator; cached per (device, fn).
-int resident_waves(KernelFn fn) {
+// Resident workgroups of `fn` (block of `threads`) on the current device:
+// CUs x blocks per CU from the HIP occupancy calculator; cached per
+// (device, fn, threads).
+int resident_blocks(KernelFn fn, int threads) {
   struct Entry {
     int device;
     KernelFn fn;
-    int waves;
+    int threads;
+    int blocks;
   };
   static std::mutex mu;
   static Entry cache[64];
@@ -988,49 +1163,64 @@ int resident_waves(KernelFn fn) {
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < used; ++i)
-    if (cache[i].device == dev && cache[i].fn == fn) return cache[i].waves;
+    if (cache[i].device == dev && cache[i].fn == fn && cache[i].threads == threads) return cache[i].blocks;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), 64, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), threads, 0) !=
           hipSuccess ||
       per_cu <= 0)
-    per_cu = 8;
+    per_cu = 1;
   (void)hipGetLastError();
-  const int waves = cus * per_cu;
-  if (used < 64) cache[used++] = Entry{dev, fn, waves};
-  return waves;
+  const int blocks = cus * per_cu;
+  if (used < 64) cache[used++] = Entry{dev, fn, threads, blocks};
+  return blocks;
 }
+
+// Waves per stream-K workgroup: the largest divisor of kv_heads <= 8, so
+// every wave serves the same number of kv-heads.
+int sk_wg_waves(int kv_heads) {
+  for (int n = kMaxWgWaves; n > 1; --n)
+    if (kv_heads % n == 0) return n;
+  return 1;
+}
+
+// Bytes of the automatic path's control region (per-sequence counters),
+// which must be zero when a call starts and is zero when it ends.
+size_t control_bytes(int batch) { return (static_cast<size_t>(batch) * sizeof(int) + 255) / 256 * 256; }
 
 struct AutoPlan {
   bool stream_k;
-  int waves;        // stream-K grid
+  int wgs;          // stream-K grid (workgroups)
+  int wg_waves;     // stream-K waves per workgroup
   int splits;       // explicit-split path
   int chunk_pages;
-  size_t ws_bytes;
-  size_t meta_offset;  // stream-K: byte offset of the meta table in the workspace
+  size_t ws_bytes;  // control region + scratch
+  size_t meta_offset;  // stream-K: byte offset of the meta table in the scratch
 };
 
 // Chooses the automatic path from static shapes only.  `aligned` says
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
               int dtype, bool aligned, AutoPlan* ap) {
-  *ap = AutoPlan{false, 0, 1, 0, 0, 0};
+  *ap = AutoPlan{false, 0, 1, 1, 0, 0, 0};
   if (batch <= 0) return QD_OK;
-  const int g = q_heads / kv_heads;
+  const size_t ctrl = control_bytes(batch);
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
-    const int64_t gmax = static_cast<int64_t>(batch) * kv_heads *
+    const int nw = sk_wg_waves(kv_heads);
+    const int64_t gmax = static_cast<int64_t>(batch) *
                          ((static_cast<int64_t>(max_pages) * block_size + 15) / 16);
-    int64_t w = resident_waves(pick_mfma_sk_dt(dtype, head_dim));
+    int64_t w = static_cast<int64_t>(resident_blocks(pick_mfma_sk_dt(dtype, head_dim), 64 * nw)) *
+                kSkOversubscribe;
     const int64_t by_work = (gmax + kSkMinGroups - 1) / kSkMinGroups;
     if (w > by_work) w = by_work;
     if (w < 1) w = 1;
-    const int64_t items = static_cast<int64_t>(batch) * kv_heads;
     ap->stream_k = true;
-    ap->waves = static_cast<int>(w);
-    ap->meta_offset = static_cast<size_t>((w + items) * g * (head_dim + 2)) * sizeof(float);
-    ap->ws_bytes = ap->meta_offset + static_cast<size_t>(items) * 2 * sizeof(int);
+    ap->wgs = static_cast<int>(w);
+    ap->wg_waves = nw;
+    ap->meta_offset = static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
+    ap->ws_bytes = ctrl + ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
     return QD_OK;
   }
   int s = 1, c = 0;
@@ -1039,7 +1229,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
   if (st != QD_OK) return st;
   ap->splits = s;
   ap->chunk_pages = c;
-  ap->ws_bytes = qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, s);
+  ap->ws_bytes = ctrl + qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, s);
   return QD_OK;
 }
 
@@ -1085,7 +1275,9 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.head_chunks = (prm.g + kGenericHeads - 1) / kGenericHeads;
   prm.num_blocks = num_blocks;
   prm.sl2 = scale * kLog2e;
+  prm.counters = nullptr;
   prm.meta = nullptr;
+  prm.wg_waves = 1;
   return prm;
 }
 
@@ -1264,6 +1456,8 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
   return launch_error();
 }
 
+size_t qd_gqa_decode_auto_control_bytes(int batch) { return batch > 0 ? control_bytes(batch) : 0; }
+
 size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
                                           int block_size, int max_pages, int dtype) {
   if (check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, 1, dtype, 1.f) !=
@@ -1293,21 +1487,24 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
   AutoPlan ap;
   st = auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, aligned, &ap);
   if (st != QD_OK) return st;
-  if (ap.ws_bytes > 0 && (!workspace || workspace_bytes < ap.ws_bytes || !aligned16(workspace)))
+  if (!workspace || workspace_bytes < ap.ws_bytes || !aligned16(workspace))
     return fail(QD_ERR_INVALID_VALUE, "workspace smaller than qd_gqa_decode_auto_workspace_bytes()");
+  char* scratch = static_cast<char*>(workspace) + control_bytes(batch);
   if (!ap.stream_k)
     return qd_gqa_decode_launch(q, k_cache, v_cache, block_table, context_lens, out,
-                                static_cast<float*>(workspace), workspace_bytes, batch, q_heads, kv_heads,
-                                head_dim, block_size, max_pages, num_blocks, dtype, scale, ap.splits,
-                                ap.chunk_pages, 0, stream);
-  DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, workspace, batch,
+                                reinterpret_cast<float*>(scratch), ap.ws_bytes - control_bytes(batch),
+                                batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
+                                dtype, scale, ap.splits, ap.chunk_pages, 0, stream);
+  DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, scratch, batch,
                                  q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
-                                 ap.waves, 0);
-  prm.meta = reinterpret_cast<int*>(static_cast<char*>(workspace) + ap.meta_offset);
+                                 ap.wgs, 0);
+  prm.counters = static_cast<int*>(workspace);
+  prm.meta = reinterpret_cast<int*>(scratch + ap.meta_offset);
+  prm.wg_waves = ap.wg_waves;
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim), dim3(ap.waves), dim3(64), 0, stm, prm);
-  hipLaunchKernelGGL(pick_merge_sk(dtype), dim3(q_heads, batch), dim3(64), 0, stm, prm);
+  hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
+  hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim), dim3(kv_heads, batch), dim3(64), 0, stm, prm);
   return launch_error();
 }
 
@@ -1319,7 +1516,7 @@ int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, 
   AutoPlan ap;
   if (auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &ap) != QD_OK)
     return -1;
-  if (waves) *waves = ap.stream_k ? ap.waves : 0;
+  if (waves) *waves = ap.stream_k ? ap.wgs * ap.wg_waves : 0;
   if (splits) *splits = ap.splits;
   if (chunk_pages) *chunk_pages = ap.chunk_pages;
   return ap.stream_k ? 1 : 0;

@@ -14,6 +14,11 @@
 #include <hip/hip_runtime_api.h>
 #include <torch/library.h>
 
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "qd_attention.h"
 
 namespace {
@@ -39,6 +44,28 @@ qd_tensor_desc describe(const at::Tensor& t) {
   d.ndim = static_cast<int32_t>(t.dim());
   for (int64_t i = 0; i < t.dim() && i < 8; ++i) d.sizes[i] = t.size(i);
   return d;
+}
+
+// The automatic path's workspace, one per (device, stream), kept for the
+// life of the process like a BLAS handle's workspace.  It is zero-filled on
+// the stream when created or grown (the library needs its control region
+// zero on entry and leaves it zero), so only the first call on a stream, or
+// one that needs a larger workspace, pays for an allocation and a fill.
+// Calls on one stream run in order and share it; calls on different
+// streams never share one.
+at::Tensor stream_workspace(const at::Tensor& like, hipStream_t stream, size_t bytes) {
+  static std::mutex mu;
+  // Never destroyed: tensors must not be freed after the allocator is gone
+  // at process exit.
+  static auto* cache = new std::map<std::pair<int, hipStream_t>, at::Tensor>();
+  const std::pair<int, hipStream_t> key{like.get_device(), stream};
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache->find(key);
+  if (it != cache->end() && static_cast<size_t>(it->second.numel()) >= bytes) return it->second;
+  at::Tensor ws = at::zeros({static_cast<int64_t>(std::max<size_t>(bytes, 256))},
+                            like.options().dtype(at::kByte));
+  (*cache)[key] = ws;
+  return ws;
 }
 
 // Explicit-split path (gqa_decode.cu:96-183 with splits >= 1).
@@ -106,14 +133,11 @@ at::Tensor gqa_decode_hip(const at::Tensor& q, const at::Tensor& k, const at::Te
   const int Hkv = static_cast<int>(k.size(2));
   const int maxP = static_cast<int>(table.size(1));
   const size_t ws_bytes = qd_gqa_decode_auto_workspace_bytes(B, Hq, Hkv, D, P, maxP, dq.dtype);
-  at::Tensor ws;
-  if (ws_bytes > 0)
-    ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  const at::Tensor ws = stream_workspace(q, stream, ws_bytes);
   st = qd_gqa_decode_auto(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr<int32_t>(),
-                          lens.data_ptr<int32_t>(), out.data_ptr(), ws.defined() ? ws.data_ptr() : nullptr,
-                          ws_bytes, B, Hq, Hkv, D, P, maxP, k.size(0), dq.dtype, static_cast<float>(scale),
-                          stream);
+                          lens.data_ptr<int32_t>(), out.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv, D,
+                          P, maxP, k.size(0), dq.dtype, static_cast<float>(scale), stream);
   TORCH_CHECK(st == QD_OK, qd_error_string(st));
   return out;
 }

@@ -14,7 +14,10 @@
  *   qd_gqa_decode_plan                attention/core.py:80-96 (gqa_decode_auto)
  *   qd_gqa_decode_workspace_bytes     csrc/cuda/dense/gqa_decode.cu:152-154
  *   qd_gqa_decode_launch              csrc/cuda/dense/gqa_decode.cu:140-183,
- *                                     kernels :18-87
+ *                                     kernels :18-87 (explicit splits)
+ *   qd_gqa_decode_auto(+_workspace_bytes, _control_bytes, _info)
+ *                                     csrc/cuda/dense/gqa_decode.cu:186-188
+ *                                     and attention/core.py:80-96
  *
  * Tensor layouts (all row-major, contiguous, on one device):
  *   q            [batch, q_heads, head_dim]                   dtype
@@ -135,19 +138,27 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  * partition is chosen from static shapes and the device (CU count and
  * kernel occupancy), never from context_lens on the host:
  *   - 16-bit caches with head_dim 64/128/256, block_size a multiple of 16,
- *     group size <= 16 and batch <= 4096: the (sequence, kv-head,
- *     16-token group) space is cut into one equal range per resident wave;
- *     partial items are merged by a log-sum-exp kernel;
+ *     group size <= 16 and batch <= 4096: the (sequence, 16-token group)
+ *     space is cut into one equal range per resident workgroup; a sequence
+ *     split across workgroups is merged (log-sum-exp) by the last of them
+ *     to finish, inside the same kernel;
  *   - otherwise: the split layout of qd_gqa_decode_launch with the plan of
  *     qd_gqa_decode_plan.
- * The workspace is opaque device memory, 16-byte aligned, of at least
- * qd_gqa_decode_auto_workspace_bytes() bytes; it needs no initialisation
- * and its contents are dead after the call's kernels finish.  Workspace
- * size and partition depend on the current device (hipGetDevice), so query
- * and launch with the same device current.  Does not allocate or
- * synchronize.  Calls on different streams need different workspaces. */
+ * The workspace is device memory, 16-byte aligned, of at least
+ * qd_gqa_decode_auto_workspace_bytes() bytes.  Its first
+ * qd_gqa_decode_auto_control_bytes(batch) bytes hold arrival counters: they
+ * must be zero when a call starts, and every call leaves them zero (zero a
+ * new workspace once, then reuse it).  The rest is scratch.  Calls that may
+ * run concurrently (different streams) need different workspaces.
+ * Workspace size and partition depend on the current device (hipGetDevice),
+ * so query and launch with the same device current.  Does not allocate or
+ * synchronize. */
 size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
                                           int block_size, int max_pages, int dtype);
+
+/* Bytes at the start of the automatic path's workspace that must be zero
+ * between calls (0 when batch <= 0). */
+size_t qd_gqa_decode_auto_control_bytes(int batch);
 
 int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
                        const int32_t* block_table, const int32_t* context_lens, void* out,
@@ -156,7 +167,7 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
                        int64_t num_blocks, int dtype, float scale, void* stream);
 
 /* Describes the automatic path's choice (assuming aligned pointers):
- * returns 1 for the balanced MFMA path (*waves = its wave count), 0 for
+ * returns 1 for the balanced MFMA path (*waves = its total wave count), 0 for
  * the split path (*splits, *chunk_pages), -1 for invalid shapes.  Any
  * output pointer may be NULL. */
 int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, int block_size,

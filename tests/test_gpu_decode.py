@@ -335,7 +335,7 @@ def test_cabi_matches_torch_op_bitwise(gpu):
     q, k, v, table, lens = to_dev(cfg.make(device="cpu"), gpu)
     out_op = attention_amd.gqa_decode(q, k, v, table, lens)
     nbytes = cabi.auto_workspace_bytes(32, 32, 8, 128, 16, table.shape[1], cabi.DTYPE[q.dtype])
-    ws = torch.empty(max(1, nbytes), device=gpu, dtype=torch.uint8)
+    ws = torch.zeros(max(1, nbytes), device=gpu, dtype=torch.uint8)
     out = torch.empty_like(q)
     rc = cabi.auto_launch(q, k, v, table, lens, out, scale=1 / math.sqrt(128), workspace=ws)
     assert rc == 0, cabi.error_string(rc)
@@ -354,12 +354,15 @@ def test_shapes_auto_cabi(gpu, shape):
     q, k, v, table, lens = case
     ref, rows = oracle_rows(case)
     nbytes = cabi.auto_workspace_bytes(q.shape[0], hq, hkv, d, p, table.shape[1], cabi.DTYPE[dtype])
-    ws = torch.full((max(16, nbytes),), 0xFF, device=gpu, dtype=torch.uint8)  # NaN / -1 poison
+    ctrl = cabi.auto_control_bytes(q.shape[0])
+    ws = torch.full((max(16, nbytes),), 0xFF, device=gpu, dtype=torch.uint8)  # NaN / -1 scratch
+    ws[:ctrl] = 0
     out = torch.full_like(q, float("nan"))
     rc = cabi.auto_launch(q, k, v, table, lens, out, scale=1 / math.sqrt(d), workspace=ws)
     assert rc == 0, cabi.error_string(rc)
     torch.cuda.synchronize()
     assert_close(out, ref, DT_NAME[dtype], rows, "auto")
+    assert torch.count_nonzero(ws[:ctrl]) == 0, "control region not left zero" 
 
 
 def test_auto_workspace_reuse_across_length_mixes(gpu):
@@ -370,7 +373,9 @@ def test_auto_workspace_reuse_across_length_mixes(gpu):
     mixes = [[4096, 4096, 1, 3000, 17, 2048], [16, 4096, 4096, 1, 0, 5000], [300, 1, 1, 1, 1, 6000]]
     maxp = -(-max(max(m) for m in mixes) // p)
     nbytes = cabi.auto_workspace_bytes(6, hq, hkv, d, p, maxp, cabi.DTYPE[torch.bfloat16])
+    ctrl = cabi.auto_control_bytes(6)
     ws = torch.full((nbytes,), 0x7F, device=gpu, dtype=torch.uint8)
+    ws[:ctrl] = 0
     for i, lengths in enumerate(mixes):
         say(f"workspace reuse mix {i}: {lengths}")
         q, k, v, table, lens = make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
@@ -384,6 +389,7 @@ def test_auto_workspace_reuse_across_length_mixes(gpu):
         assert rc == 0, cabi.error_string(rc)
         torch.cuda.synchronize()
         assert_close(out, ref, "bf16", rows, f"mix {i}")
+        assert torch.count_nonzero(ws[:ctrl]) == 0, "control region not left zero" 
 
 
 @pytest.mark.parametrize("lengths", [[1] * 300, [0] * 5 + [33], [16] * 64, [1, 0, 2, 0, 15, 16, 17]],
