@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(PKG, "lib", "libqd_attention.so")
 
 DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.int32: 3}
 QD_FLAG_FORCE_GENERIC = 1
+QD_STAGE_DECODE, QD_STAGE_MERGE, QD_STAGE_ALL = 1, 2, 3
 
 
 class TensorDesc(ctypes.Structure):
@@ -79,6 +80,10 @@ def lib():
         L.qd_gqa_decode_auto.argtypes = (
             [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
             + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p])
+        L.qd_gqa_decode_auto_stages.restype = ctypes.c_int
+        L.qd_gqa_decode_auto_stages.argtypes = (
+            [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
+            + [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_void_p])
         L.qd_gqa_decode_auto_info.restype = ctypes.c_int
         L.qd_gqa_decode_auto_info.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int)] * 3
         _lib = L
@@ -144,7 +149,7 @@ def auto_info(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype=2
     return kind, w.value, s.value, c.value
 
 
-def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None):
+def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None, stages=QD_STAGE_ALL):
     """Calls qd_gqa_decode_auto on torch device tensors (no validation).
 
     ``workspace`` (any dtype, contiguous) must hold auto_workspace_bytes(),
@@ -156,7 +161,7 @@ def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None
         stream = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else 0
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    return lib().qd_gqa_decode_auto(
+    return lib().qd_gqa_decode_auto_stages(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), lens.data_ptr(), out.data_ptr(),
         ws_ptr, ws_bytes, B, Hq, Hkv, D, P, table.shape[1], k.shape[0], DTYPE[q.dtype], float(scale),
-        stream)
+        stages, stream)

@@ -1472,11 +1472,13 @@ size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, 
   return a.ws_bytes > b.ws_bytes ? a.ws_bytes : b.ws_bytes;
 }
 
-int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
-                       const int32_t* block_table, const int32_t* context_lens, void* out,
-                       void* workspace, size_t workspace_bytes, int batch, int q_heads, int kv_heads,
-                       int head_dim, int block_size, int max_pages, int64_t num_blocks, int dtype,
-                       float scale, void* stream) {
+int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, const int32_t* context_lens, void* out,
+                              void* workspace, size_t workspace_bytes, int batch, int q_heads,
+                              int kv_heads, int head_dim, int block_size, int max_pages,
+                              int64_t num_blocks, int dtype, float scale, int stages, void* stream) {
+  if ((stages & ~QD_STAGE_ALL) != 0 || stages == 0)
+    return fail(QD_ERR_INVALID_VALUE, "stages must be a non-empty mask of QD_STAGE_*");
   int st = check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
                                dtype, scale);
   if (st != QD_OK) return st;
@@ -1490,11 +1492,14 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
   if (!workspace || workspace_bytes < ap.ws_bytes || !aligned16(workspace))
     return fail(QD_ERR_INVALID_VALUE, "workspace smaller than qd_gqa_decode_auto_workspace_bytes()");
   char* scratch = static_cast<char*>(workspace) + control_bytes(batch);
-  if (!ap.stream_k)
+  if (!ap.stream_k) {
+    if (stages != QD_STAGE_ALL)
+      return fail(QD_ERR_INVALID_VALUE, "stages apply to the balanced MFMA path only");
     return qd_gqa_decode_launch(q, k_cache, v_cache, block_table, context_lens, out,
                                 reinterpret_cast<float*>(scratch), ap.ws_bytes - control_bytes(batch),
                                 batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
                                 dtype, scale, ap.splits, ap.chunk_pages, 0, stream);
+  }
   DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, scratch, batch,
                                  q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
                                  ap.wgs, 0);
@@ -1503,9 +1508,21 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
   prm.wg_waves = ap.wg_waves;
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
-  hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim), dim3(kv_heads, batch), dim3(64), 0, stm, prm);
+  if (stages & QD_STAGE_DECODE)
+    hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
+  if (stages & QD_STAGE_MERGE)
+    hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim), dim3(kv_heads, batch), dim3(64), 0, stm, prm);
   return launch_error();
+}
+
+int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
+                       const int32_t* block_table, const int32_t* context_lens, void* out,
+                       void* workspace, size_t workspace_bytes, int batch, int q_heads, int kv_heads,
+                       int head_dim, int block_size, int max_pages, int64_t num_blocks, int dtype,
+                       float scale, void* stream) {
+  return qd_gqa_decode_auto_stages(q, k_cache, v_cache, block_table, context_lens, out, workspace,
+                                   workspace_bytes, batch, q_heads, kv_heads, head_dim, block_size,
+                                   max_pages, num_blocks, dtype, scale, QD_STAGE_ALL, stream);
 }
 
 int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, int block_size,

@@ -15,7 +15,7 @@
  *   qd_gqa_decode_workspace_bytes     csrc/cuda/dense/gqa_decode.cu:152-154
  *   qd_gqa_decode_launch              csrc/cuda/dense/gqa_decode.cu:140-183,
  *                                     kernels :18-87 (explicit splits)
- *   qd_gqa_decode_auto(+_workspace_bytes, _control_bytes, _info)
+ *   qd_gqa_decode_auto(+_stages, _workspace_bytes, _control_bytes, _info)
  *                                     csrc/cuda/dense/gqa_decode.cu:186-188
  *                                     and attention/core.py:80-96
  *
@@ -165,6 +165,19 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
                        void* workspace, size_t workspace_bytes, int batch, int q_heads,
                        int kv_heads, int head_dim, int block_size, int max_pages,
                        int64_t num_blocks, int dtype, float scale, void* stream);
+
+/* The automatic path's kernels, for callers that time or schedule them
+ * separately (the balanced MFMA path only; the split path needs
+ * QD_STAGE_ALL).  QD_STAGE_DECODE alone leaves split sequences unmerged;
+ * a following QD_STAGE_MERGE call with the same arguments and workspace on
+ * the same stream completes the output. */
+enum { QD_STAGE_DECODE = 1, QD_STAGE_MERGE = 2, QD_STAGE_ALL = 3 };
+
+int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, const int32_t* context_lens, void* out,
+                              void* workspace, size_t workspace_bytes, int batch, int q_heads,
+                              int kv_heads, int head_dim, int block_size, int max_pages,
+                              int64_t num_blocks, int dtype, float scale, int stages, void* stream);
 
 /* Describes the automatic path's choice (assuming aligned pointers):
  * returns 1 for the balanced MFMA path (*waves = its total wave count), 0 for

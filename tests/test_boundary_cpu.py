@@ -207,6 +207,74 @@ def test_launch_batch_zero_is_a_no_op():
 
 
 # ----------------------------------------------------------------------------
+# Automatic path (qd_gqa_decode_auto*): plan, workspace layout, argument errors
+# ----------------------------------------------------------------------------
+
+def test_auto_control_bytes():
+    assert cabi.auto_control_bytes(0) == 0
+    assert cabi.auto_control_bytes(1) == 256
+    assert cabi.auto_control_bytes(64) == 256
+    assert cabi.auto_control_bytes(65) == 512
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_auto_plan_for_configs(name):
+    cfg = CONFIGS[name]
+    max_pages = max(1, -(-max(cfg.lengths()) // cfg.block_size))
+    dt = {torch.float16: F16, torch.bfloat16: BF16}[cfg.dtype]
+    kind, waves, splits, chunk = cabi.auto_info(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                                                cfg.block_size, max_pages, dt)
+    assert kind == 1                                   # every benchmark config takes the MFMA path
+    assert waves > 0 and waves % min(cfg.kv_heads, 8) == 0
+    nbytes = cabi.auto_workspace_bytes(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                                       cfg.block_size, max_pages, dt)
+    wgs = waves // min(cfg.kv_heads, 8)
+    slots = (wgs + cfg.batch) * cfg.q_heads * (cfg.head_dim + 2) * 4
+    assert nbytes >= cabi.auto_control_bytes(cfg.batch) + slots + 8 * cfg.batch
+
+
+def test_auto_plan_falls_back_to_splits():
+    # fp32 caches take the split layout with the split plan.
+    kind, waves, splits, chunk = cabi.auto_info(32, 32, 8, 128, 16, 256, F32)
+    assert (kind, waves) == (0, 0) and (splits, chunk) == cabi.plan(32, 32, 8, 128, 16, 256)
+    assert cabi.auto_info(4, 8, 3, 64, 16, 4, F16)[0] == -1   # Hq % Hkv != 0
+
+
+def test_auto_waves_per_workgroup_divide_kv_heads():
+    for hkv, per_wg in [(1, 1), (2, 2), (4, 4), (8, 8), (12, 6), (16, 8), (7, 7), (9, 3)]:
+        kind, waves, _, _ = cabi.auto_info(4, hkv, hkv, 64, 16, 64, F16)
+        assert kind == 1 and waves % per_wg == 0, (hkv, waves)
+
+
+def _auto_args(**over):
+    a = dict(q=1, k=1, v=1, table=1, lens=1, out=1, ws=None, ws_bytes=0, B=4, Hq=8, Hkv=2, D=64,
+             P=16, maxP=32, N=57, dtype=F16, scale=0.125, stages=cabi.QD_STAGE_ALL, stream=None)
+    a.update(over)
+    return [a[k] for k in ["q", "k", "v", "table", "lens", "out", "ws", "ws_bytes", "B", "Hq", "Hkv",
+                           "D", "P", "maxP", "N", "dtype", "scale", "stages", "stream"]]
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(Hkv=3), "Hq must be divisible by Hkv"),
+    (dict(scale=float("inf")), "scale must be positive and finite"),
+    (dict(stages=0), "stages must be a non-empty mask of QD_STAGE_*"),
+    (dict(stages=4), "stages must be a non-empty mask of QD_STAGE_*"),
+    (dict(q=None), "null tensor pointer"),
+    (dict(), "workspace smaller than qd_gqa_decode_auto_workspace_bytes()"),
+    (dict(dtype=F32, ws=16, ws_bytes=1 << 30, stages=cabi.QD_STAGE_DECODE),
+     "stages apply to the balanced MFMA path only"),
+])
+def test_auto_argument_errors(over, msg):
+    rc = cabi.lib().qd_gqa_decode_auto_stages(*_auto_args(**over))
+    assert rc == 1
+    assert cabi.error_string(rc) == msg
+
+
+def test_auto_batch_zero_is_a_no_op():
+    assert cabi.lib().qd_gqa_decode_auto_stages(*_auto_args(B=0, q=None)) == 0
+
+
+# ----------------------------------------------------------------------------
 # Torch op surface and Python API
 # ----------------------------------------------------------------------------
 
