@@ -446,13 +446,13 @@ __device__ __forceinline__ VRow<D> load_vrow(const char* ptr) {
   return r;
 }
 
-// Registers for one 16-token group in flight.
-template <int D>
+// Registers for one 16-token group in flight, for NKV kv-heads.
+template <int D, int NKV>
 struct GroupBuf {
   static constexpr int KC = D / 32;
-  u32x4 k[KC];     // K, coalesced: 16 bytes of row KTile<D>::row(c, lane)
-  VRow<D> v[4];    // V rows 4*(lane/16)+i, elements (D/16)*(lane%16) ..
-  int tg;          // first token of the group
+  u32x4 k[NKV][KC];   // K, coalesced: 16 bytes of row KTile<D>::row(c, lane)
+  VRow<D> v[NKV][4];  // V rows 4*(lane/16)+i, elements (D/16)*(lane%16) ..
+  int tg;             // first token of the group
 };
 
 // K of one 16-token group moves HBM -> VGPR -> LDS -> VGPR.  The global
@@ -473,9 +473,13 @@ struct KTile {
   __device__ static int col_bytes(int lane) { return 16 * (lane % kLanesPerRow); }
 };
 
-// One wave's decode state for one (sequence, kv-head) item.
+// One wave's decode state for NKV adjacent kv-heads (kvh0 .. kvh0+NKV-1) of
+// one sequence.  Serving two kv-heads from one wave (one wave per SIMD)
+// keeps the K/V streams of a SIMD in one instruction stream: two waves on a
+// SIMD were served unevenly (the older one finished ~30% earlier, leaving
+// half the loads in flight for the rest of the kernel).
 //
-// Lane l, r16 = l % 16, q4 = l / 16:
+// Lane l, r16 = l % 16, q4 = l / 16, for each kv-head:
 //   QK  A = K      lane holds K[token r16][8 elems]     (16x16x32 A layout,
 //                  read from the LDS tile)
 //       B = Q^T    lane holds Q[head  r16][same elems]
@@ -486,19 +490,20 @@ struct KTile {
 // so every lane owns one head's softmax state and a contiguous slice of
 // DV*4 output elements of that head.  Heads r16 >= group size carry zero
 // queries and are never stored.
-template <int D, int DT, int PF>
+template <int D, int DT, int PF, int NKV>
 struct MfmaWave {
   using Ops = MfmaOps<DT>;
+  using Buf = GroupBuf<D, NKV>;
   static constexpr int KC = D / 32;
   static constexpr int DV = D / 16;
   static constexpr int VB = DV * 2;  // bytes per lane per V row
 
   int lane, r16, q4;
-  u32x4 qv[KC];
-  float m_run, l_run;
-  f32x4 acc[DV];
+  u32x4 qv[NKV][KC];
+  float m_run[NKV], l_run[NKV];
+  f32x4 acc[NKV][DV];
   // Item being processed.
-  const char* kbase;
+  const char* kbase;  // kv-head kvh0; kv-head kvh0+j is 2*D*j bytes further
   const char* vbase;
   const int32_t* trow;
   int len;    // valid tokens of the item (or of the split)
@@ -511,23 +516,26 @@ struct MfmaWave {
     q4 = lane >> 4;
   }
 
-  __device__ void begin_item(const DecodeParams& p, int b, int kvh, int valid_tokens) {
+  __device__ void begin_item(const DecodeParams& p, int b, int kvh0, int valid_tokens) {
     const int g = p.g;
     const bool head_ok = r16 < g;
-    const char* qp = static_cast<const char*>(p.q) +
-                     (static_cast<int64_t>(b) * p.Hq + kvh * g + (head_ok ? r16 : 0)) * D * 2;
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(qp + (32 * c + 8 * q4) * 2);
-      const u32x4 zero = {0u, 0u, 0u, 0u};
-      qv[c] = head_ok ? x : zero;
+    for (int j = 0; j < NKV; ++j) {
+      const char* qp = static_cast<const char*>(p.q) +
+                       (static_cast<int64_t>(b) * p.Hq + (kvh0 + j) * g + (head_ok ? r16 : 0)) * D * 2;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(qp + (32 * c + 8 * q4) * 2);
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        qv[j][c] = head_ok ? x : zero;
+      }
+      m_run[j] = -INFINITY;
+      l_run[j] = 0.f;
+#pragma unroll
+      for (int d = 0; d < DV; ++d) acc[j][d] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    m_run = -INFINITY;
-    l_run = 0.f;
-#pragma unroll
-    for (int j = 0; j < DV; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh) * D * 2;
-    vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh) * D * 2;
+    kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh0) * D * 2;
+    vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh0) * D * 2;
     trow = p.table + static_cast<int64_t>(b) * p.maxP;
     len = valid_tokens;
   }
@@ -535,7 +543,7 @@ struct MfmaWave {
   // Issues the K/V loads of group gi (tokens 16*gi .. 16*gi+15 of the item).
   // The group lies inside one page (block_size is a multiple of 16); rows at
   // or past `len` re-read the last valid row and are masked in compute().
-  __device__ void issue(const DecodeParams& p, GroupBuf<D>& buf, int gi) {
+  __device__ void issue(const DecodeParams& p, Buf& buf, int gi) {
     const int gpp = p.P >> 4;
     const int tg = 16 * gi;
     buf.tg = tg;
@@ -550,61 +558,67 @@ struct MfmaWave {
     const int last = len - 1 - tg;  // rows > last are past the end: reuse row `last`
     const uint32_t kcol = static_cast<uint32_t>(KTile<D>::col_bytes(lane));
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const uint32_t rk = static_cast<uint32_t>(min(KTile<D>::row(c, lane), last));
-      buf.k[c] = stream_load16(kp + rk * rb32 + kcol);
-    }
+    for (int j = 0; j < NKV; ++j) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t rv = static_cast<uint32_t>(min(4 * q4 + i, last));
-      buf.v[i] = load_vrow<D>(vp + rv * rb32 + VB * r16);
+      for (int c = 0; c < KC; ++c) {
+        const uint32_t rk = static_cast<uint32_t>(min(KTile<D>::row(c, lane), last));
+        buf.k[j][c] = stream_load16(kp + j * 2 * D + rk * rb32 + kcol);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t rv = static_cast<uint32_t>(min(4 * q4 + i, last));
+        buf.v[j][i] = load_vrow<D>(vp + j * 2 * D + rv * rb32 + VB * r16);
+      }
     }
     // Keep each group's loads in program order relative to the other
     // groups': the wait before a compute then covers only that group.
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  __device__ void compute(const DecodeParams& p, const GroupBuf<D>& buf, char* ktile) {
-    // Transpose K through LDS into the A layout: lane (r16, q4), chunk c
-    // holds row r16, bytes [64c + 16q4, +16).
-#pragma unroll
-    for (int c = 0; c < KC; ++c)
-      *reinterpret_cast<u32x4*>(ktile + KTile<D>::row(c, lane) * KTile<D>::kStride +
-                                KTile<D>::col_bytes(lane)) = buf.k[c];
-    u32x4 ka[KC];
-#pragma unroll
-    for (int c = 0; c < KC; ++c)
-      ka[c] = *reinterpret_cast<const u32x4*>(ktile + r16 * KTile<D>::kStride + 64 * c + 16 * q4);
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < KC; ++c) s = Ops::qk(ka[c], qv[c], s);
+  __device__ void compute(const DecodeParams& p, const Buf& buf, char* ktile) {
     const int last = len - 1 - buf.tg;
-    float x[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = (4 * q4 + i <= last) ? s[i] : -INFINITY;
-    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m_run, mx * p.sl2);
-    const float mref = mn == -INFINITY ? 0.f : mn;
-    const float alpha = fast_exp2(m_run - mref);
-    float pr[4];
+    for (int j = 0; j < NKV; ++j) {
+      // Transpose K through LDS into the A layout: lane (r16, q4), chunk c
+      // holds row r16, bytes [64c + 16q4, +16).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(fmaf(x[i], p.sl2, -mref));
-    l_run = fmaf(l_run, alpha, (pr[0] + pr[1]) + (pr[2] + pr[3]));
-    m_run = mn;
-    if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.f)) {
+      for (int c = 0; c < KC; ++c)
+        *reinterpret_cast<u32x4*>(ktile + KTile<D>::row(c, lane) * KTile<D>::kStride +
+                                  KTile<D>::col_bytes(lane)) = buf.k[j][c];
+      u32x4 ka[KC];
 #pragma unroll
-      for (int j = 0; j < DV; ++j) acc[j] *= alpha;
-    }
-    const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
+      for (int c = 0; c < KC; ++c)
+        ka[c] = *reinterpret_cast<const u32x4*>(ktile + r16 * KTile<D>::kStride + 64 * c + 16 * q4);
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < DV; ++j) {
-      const int w = j >> 1;
-      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-      const u32x2 a = {__builtin_amdgcn_perm(buf.v[1].w[w], buf.v[0].w[w], sel),
-                       __builtin_amdgcn_perm(buf.v[3].w[w], buf.v[2].w[w], sel)};
-      acc[j] = Ops::pv(a, pb, acc[j]);
+      for (int c = 0; c < KC; ++c) s = Ops::qk(ka[c], qv[j][c], s);
+      float x[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = (4 * q4 + i <= last) ? s[i] : -INFINITY;
+      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m_run[j], mx * p.sl2);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = fast_exp2(m_run[j] - mref);
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(fmaf(x[i], p.sl2, -mref));
+      l_run[j] = fmaf(l_run[j], alpha, (pr[0] + pr[1]) + (pr[2] + pr[3]));
+      m_run[j] = mn;
+      if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.f)) {
+#pragma unroll
+        for (int d = 0; d < DV; ++d) acc[j][d] *= alpha;
+      }
+      const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
+#pragma unroll
+      for (int d = 0; d < DV; ++d) {
+        const int w = d >> 1;
+        const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+        const u32x2 a = {__builtin_amdgcn_perm(buf.v[j][1].w[w], buf.v[j][0].w[w], sel),
+                         __builtin_amdgcn_perm(buf.v[j][3].w[w], buf.v[j][2].w[w], sel)};
+        acc[j][d] = Ops::pv(a, pb, acc[j][d]);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -623,7 +637,7 @@ struct MfmaWave {
       const int g_hi = min(gb, (wbase + 64) * gpp);
       const int n = g_hi - g_lo;
       tblv = (lane < p.maxP - wbase) ? trow[wbase + lane] : 0;
-      GroupBuf<D> buf[PF];
+      Buf buf[PF];
       int i = 0;
       if (n >= 2 * PF - 1) {
 #pragma unroll
@@ -654,24 +668,24 @@ struct MfmaWave {
 
   // Softmax denominator of this lane's head (lanes of one head hold partial
   // sums over their 4 tokens of every group).
-  __device__ float total_l() const {
-    float l = l_run + __shfl_xor(l_run, 16);
+  __device__ float total_l(int j) const {
+    float l = l_run[j] + __shfl_xor(l_run[j], 16);
     return l + __shfl_xor(l, 32);
   }
 
-  // out[b, kvh*g + r16, :] = acc / l (zeros when l == 0), one rounding.
-  __device__ void store_direct(const DecodeParams& p, int b, int kvh, float l_tot) {
+  // out[b, (kvh0+jk)*g + r16, :] = acc / l (zeros when l == 0), one rounding.
+  __device__ void store_direct(const DecodeParams& p, int b, int kvh0, int jk, float l_tot) {
     using S = typename Elem<DT>::S;
     if (r16 >= p.g) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + kvh * p.g + r16) * D;
+    S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + (kvh0 + jk) * p.g + r16) * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t wv[DV / 2];
 #pragma unroll
       for (int j = 0; j < DV; j += 2)
-        wv[j / 2] = Ops::pack2(l_tot > 0.f ? acc[j][i] * inv : 0.f,
-                               l_tot > 0.f ? acc[j + 1][i] * inv : 0.f);
+        wv[j / 2] = Ops::pack2(l_tot > 0.f ? acc[jk][j][i] * inv : 0.f,
+                               l_tot > 0.f ? acc[jk][j + 1][i] * inv : 0.f);
       char* dst = reinterpret_cast<char*>(o + DV * (4 * q4 + i));
       if constexpr (DV / 2 == 2) {
         *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
@@ -684,19 +698,19 @@ struct MfmaWave {
     }
   }
 
-  // Partial {m (natural-log units), l, acc[D]} of this lane's head at
-  // w + head*head_stride (head_stride even).  AGENT: coherent stores for a
-  // reader in another workgroup of the same kernel.
+  // Partial {m (natural-log units), l, acc[D]} of kv-head kvh0+jk, this
+  // lane's head, at w + head*head_stride (head_stride even).  AGENT:
+  // coherent stores for a reader in another workgroup of the same kernel.
   template <bool AGENT>
-  __device__ void store_partial(const DecodeParams& p, float* w, int64_t head_stride, float l_tot) {
+  __device__ void store_partial(const DecodeParams& p, int jk, float* w, int64_t head_stride, float l_tot) {
     if (r16 >= p.g) return;
     w += r16 * head_stride;
     if (q4 == 0) {
       if constexpr (AGENT) {
-        store_agent(w, m_run * kLn2);
+        store_agent(w, m_run[jk] * kLn2);
         store_agent(w + 1, l_tot);
       } else {
-        w[0] = m_run * kLn2;
+        w[0] = m_run[jk] * kLn2;
         w[1] = l_tot;
       }
     }
@@ -705,7 +719,7 @@ struct MfmaWave {
       float* dst = w + 2 + DV * (4 * q4 + i);
 #pragma unroll
       for (int j = 0; j < DV; j += 2) {
-        const f32x2 v = {acc[j][i], acc[j + 1][i]};
+        const f32x2 v = {acc[jk][j][i], acc[jk][j + 1][i]};
         if constexpr (AGENT)
           store_agent2(dst + j, v);
         else
@@ -729,16 +743,16 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
   if (z >= (ci.nch > 1 ? ci.nch : 1)) return;
 
   __shared__ __align__(16) char ktile[KTile<D>::kBytes];
-  MfmaWave<D, DT, PF> wv;
+  MfmaWave<D, DT, PF, 1> wv;
   wv.init_lane();
   wv.begin_item(p, b, kvh, ci.te);
   wv.run(p, ci.tb >> 4, (ci.te + 15) >> 4, ktile);  // tb is page aligned
-  const float l_tot = wv.total_l();
+  const float l_tot = wv.total_l(0);
   if (ci.nch <= 1) {
-    wv.store_direct(p, b, kvh, l_tot);
+    wv.store_direct(p, b, kvh, 0, l_tot);
   } else {
     float* w = p.ws + ((static_cast<int64_t>(b) * p.Hq + kvh * p.g) * p.splits + z) * (D + 2);
-    wv.template store_partial<false>(p, w, static_cast<int64_t>(p.splits) * (D + 2), l_tot);
+    wv.template store_partial<false>(p, 0, w, static_cast<int64_t>(p.splits) * (D + 2), l_tot);
   }
 }
 
@@ -754,15 +768,14 @@ __device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
 // (online_softmax.cuh:17-24): a row with l == 0 is skipped, the running
 // state is rescaled by exp(m - max).  Output acc/l rounded once, zeros when
 // l == 0 (gqa_decode.cu:84-86).  One wave: 16 lanes per head, D/16
-// elements per lane, 4 heads per pass; the rows are loaded 8 at a time so
-// that one memory round trip covers a typical merge.
-template <int D, int DT>
+// elements per lane, 4 heads per pass; the rows are loaded kBatch at a time
+// so that one memory round trip covers a typical merge.
+template <int D, int DT, int kBatch>
 __device__ __forceinline__ void merge_kv_group(const float* base, int64_t row_stride, int nrows, int g,
                                                typename Elem<DT>::S* out) {
   // Partials come from an earlier kernel on the same stream: plain loads.
   using E = Elem<DT>;
   constexpr int EPL = D / 16;
-  constexpr int kBatch = 8;
   const int lane = threadIdx.x & 63;
   const int j4 = lane >> 4;
   const int c16 = lane & 15;
@@ -811,11 +824,19 @@ __device__ __forceinline__ void merge_kv_group(const float* base, int64_t row_st
 
 constexpr int kMaxWgWaves = 8;
 
+// Waves per stream-K workgroup at most: 8 serving one kv-head each, or 4
+// (one per SIMD, so each may use 512 registers) serving two each or with
+// head_dim 256.
+template <int D, int NKV>
+constexpr int sk_max_waves() {
+  return (NKV == 1 && D <= 128) ? kMaxWgWaves : kMaxWgWaves / 2;
+}
+
 // Balanced ("stream-K") layout.  grid: W = p.splits workgroups of
-// p.wg_waves waves; wave j of a workgroup serves kv-heads j, j + wg_waves,
-// ... so that a workgroup reads whole cache rows (all kv-heads of a token)
-// at once, which streams faster from HBM than kv-head slices read at
-// unrelated times.
+// p.wg_waves waves; wave j of a workgroup serves kv-heads j*NKV .. j*NKV +
+// NKV-1, then the same plus wg_waves*NKV, ... so that a workgroup reads
+// whole cache rows (all kv-heads of a token) at once, which streams faster
+// from HBM than kv-head slices read at unrelated times.
 //
 // Sequence b has n_b = ceil(len_b/16) groups; the sequences are laid end to
 // end into G = sum_b n_b groups and workgroup w takes groups
@@ -826,8 +847,8 @@ constexpr int kMaxWgWaves = 8;
 // workgroups of sequence b+1 start at or after the last one of b, so
 // W + B slots suffice).  merge_sk_kernel combines the slots of every split
 // sequence.  Rows of empty sequences are zero-filled by workgroup b % W.
-template <int D, int DT, int PF>
-__global__ __launch_bounds__(64 * kMaxWgWaves) void decode_mfma_sk_kernel(DecodeParams p) {
+template <int D, int DT, int PF, int NKV>
+__global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -835,51 +856,95 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) void decode_mfma_sk_kernel(Decode
   const int w = blockIdx.x;
   const int W = p.splits;
   const int B = p.B;
-  __shared__ __align__(16) char ktile[kMaxWgWaves][KTile<D>::kBytes];
+  __shared__ __align__(16) char ktile[sk_max_waves<D, NKV>()][KTile<D>::kBytes];
 
-  // Pass 1: total groups G.
-  int64_t tot = 0;
-  for (int c = 0; c < B; c += 64) {
-    const int bb = c + lane;
-    tot += bb < B ? seq_groups(p, p.lens[bb]) : 0;
+  // Prologue, one memory round trip for B <= 64*kRegChunks: every lane loads
+  // the lengths of sequences c*64 + lane, and the group counts and their
+  // running sums stay in registers.
+  constexpr int kRegChunks = 4;
+  int n_r[kRegChunks];
+  int64_t incl_r[kRegChunks];
+#pragma unroll
+  for (int c = 0; c < kRegChunks; ++c) {
+    const int bb = c * 64 + lane;
+    n_r[c] = bb < B ? seq_groups(p, p.lens[bb]) : 0;
   }
-  const int64_t G = wave_sum_i64(tot);
+  int64_t carry = 0;
+#pragma unroll
+  for (int c = 0; c < kRegChunks; ++c) {
+    incl_r[c] = carry + wave_incl_scan_i64(n_r[c], lane);
+    carry = __shfl(incl_r[c], 63);
+  }
+  for (int c = 64 * kRegChunks; c < B; c += 64) {  // larger batches: re-read
+    const int bb = c + lane;
+    carry += wave_sum_i64(bb < B ? seq_groups(p, p.lens[bb]) : 0);
+  }
+  const int64_t G = carry;
 
-  // Zero rows of empty sequences (no workgroup holds them).
-  for (int bb = w; bb < B; bb += W) {
-    if (seq_groups(p, p.lens[bb]) == 0) {
+  // Empty sequences (no workgroup holds them): workgroup b % W writes their
+  // zero rows and a meta entry that tells merge_sk_kernel to skip them.
+  auto zero_fill = [&](uint64_t mask, int c0) {
+    while (mask) {
+      const int bb = c0 + __builtin_ctzll(mask);
+      mask &= mask - 1;
       S* o = static_cast<S*>(p.out) + static_cast<int64_t>(bb) * p.Hq * p.D;
       for (int i = threadIdx.x; i < p.Hq * p.D; i += 64 * nw) o[i] = Elem<DT>::from_f(0.f);
+      if (threadIdx.x == 0) {
+        p.meta[2 * bb] = 0;
+        p.meta[2 * bb + 1] = 0;
+      }
     }
+  };
+#pragma unroll
+  for (int c = 0; c < kRegChunks; ++c) {
+    const int bb = c * 64 + lane;
+    zero_fill(__ballot(bb < B && n_r[c] == 0 && bb % W == w), c * 64);
+  }
+  for (int c = 64 * kRegChunks; c < B; c += 64) {
+    const int bb = c + lane;
+    zero_fill(__ballot(bb < B && bb % W == w && seq_groups(p, p.lens[bb]) == 0), c);
   }
 
   const int64_t g0 = static_cast<int64_t>(w) * G / W;
   const int64_t g1 = static_cast<int64_t>(w + 1) * G / W;
   if (g0 >= g1) return;  // uniform across the workgroup
 
-  // Pass 2: the sequence holding group g0 and its first group gs.
+  // The sequence holding group g0 (the first whose running group end exceeds
+  // g0) and its first group gs.
   int b = B;
   int64_t gs = 0;
-  int64_t carry = 0;
-  for (int c = 0; c < B; c += 64) {
-    const int bb = c + lane;
-    const int64_t n = bb < B ? static_cast<int64_t>(seq_groups(p, p.lens[bb])) : 0;
-    const int64_t incl = carry + wave_incl_scan_i64(n, lane);
-    const uint64_t before = __ballot(bb < B && incl <= g0);  // sequences ending at or before g0
-    const int cnt = __popcll(before);
-    if (cnt < min(64, B - c)) {
-      b = c + cnt;
-      gs = __shfl(incl - n, cnt);
-      break;
+#pragma unroll
+  for (int c = 0; c < kRegChunks; ++c) {
+    if (b == B) {
+      const int bb = c * 64 + lane;
+      const int cnt = __popcll(__ballot(bb < B && incl_r[c] <= g0));
+      if (cnt < min(64, B - c * 64)) {
+        b = c * 64 + cnt;
+        gs = __shfl(incl_r[c] - n_r[c], cnt);
+      }
     }
-    carry = __shfl(incl, 63);
+  }
+  if (b == B) {
+    carry = __shfl(incl_r[kRegChunks - 1], 63);
+    for (int c = 64 * kRegChunks; c < B; c += 64) {
+      const int bb = c + lane;
+      const int64_t n = bb < B ? static_cast<int64_t>(seq_groups(p, p.lens[bb])) : 0;
+      const int64_t incl = carry + wave_incl_scan_i64(n, lane);
+      const int cnt = __popcll(__ballot(bb < B && incl <= g0));
+      if (cnt < min(64, B - c)) {
+        b = c + cnt;
+        gs = __shfl(incl - n, cnt);
+        break;
+      }
+      carry = __shfl(incl, 63);
+    }
   }
   if (b >= B) return;  // unreachable when G is consistent
 
   // Workgroup holding flattened group x.
   auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * W - 1) / G); };
 
-  MfmaWave<D, DT, PF> wv;
+  MfmaWave<D, DT, PF, NKV> wv;
   wv.init_lane();
   int len = clamp_len(p, p.lens[b]);
   int nb = (len + 15) >> 4;
@@ -890,14 +955,18 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) void decode_mfma_sk_kernel(Decode
     const int seg = static_cast<int>(min(static_cast<int64_t>(nb - gi), remaining));
     const bool whole = gi == 0 && gi + seg == nb;
     float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
-    for (int kvh = wid; kvh < p.Hkv; kvh += nw) {
-      wv.begin_item(p, b, kvh, len);
+    for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
+      wv.begin_item(p, b, kvh0, len);
       wv.run(p, gi, gi + seg, ktile[wid]);
-      const float l_tot = wv.total_l();
-      if (whole)
-        wv.store_direct(p, b, kvh, l_tot);
-      else
-        wv.template store_partial<false>(p, slot + static_cast<int64_t>(kvh) * p.g * (D + 2), D + 2, l_tot);
+#pragma unroll
+      for (int j = 0; j < NKV; ++j) {
+        const float l_tot = wv.total_l(j);
+        if (whole)
+          wv.store_direct(p, b, kvh0, j, l_tot);
+        else
+          wv.template store_partial<false>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2), D + 2,
+                                           l_tot);
+      }
     }
     // The workgroup holding a sequence's first group records which
     // workgroups span it, for merge_sk_kernel (also for a whole sequence, so
@@ -921,19 +990,19 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) void decode_mfma_sk_kernel(Decode
 }
 
 // Stream-K merge: grid (Hkv, B), block 64; one wave merges the g heads of
-// one kv-head of one sequence from slots first+b .. first+b+nwg-1.
+// one kv-head of one sequence from slots first+b .. first+b+nwg-1.  Two
+// dependent memory round trips: the meta entry, then the partial rows.
 template <int D, int DT>
 __global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
   const int kvh = blockIdx.x;
   const int b = blockIdx.y;
-  if (clamp_len(p, p.lens[b]) == 0) return;  // zero-filled by the decode kernel
   const int first = p.meta[2 * b];
   const int nwg = p.meta[2 * b + 1];
-  if (nwg <= 1) return;  // written directly
+  if (nwg <= 1) return;  // written directly, or an empty sequence (zero-filled)
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
   const int64_t h0 = static_cast<int64_t>(kvh) * p.g;
-  merge_kv_group<D, DT>(p.ws + static_cast<int64_t>(first + b) * slot_floats + h0 * (D + 2), slot_floats, nwg,
+  merge_kv_group<D, DT, 16>(p.ws + static_cast<int64_t>(first + b) * slot_floats + h0 * (D + 2), slot_floats, nwg,
                         p.g, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h0) * D);
 }
 
@@ -1101,17 +1170,30 @@ KernelFn pick_mfma(int D) {
   }
 }
 
+#ifndef QD_PREFETCH_DUAL
+#define QD_PREFETCH_DUAL 2
+#endif
+// Groups in flight per wave when a wave serves two kv-heads (twice the
+// bytes per group).
+constexpr int kPrefetchDual = QD_PREFETCH_DUAL;
+
 template <int DT>
-KernelFn pick_mfma_sk(int D) {
+KernelFn pick_mfma_sk(int D, int nkv) {
+  if (nkv == 2) {
+    switch (D) {
+      case 64: return decode_mfma_sk_kernel<64, DT, kPrefetchDual, 2>;
+      default: return decode_mfma_sk_kernel<128, DT, kPrefetchDual, 2>;
+    }
+  }
   switch (D) {
-    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch>;
-    case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch>;
-    default: return decode_mfma_sk_kernel<256, DT, 2>;
+    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch, 1>;
+    case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch, 1>;
+    default: return decode_mfma_sk_kernel<256, DT, 2, 1>;
   }
 }
 
-KernelFn pick_mfma_sk_dt(int dtype, int D) {
-  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D) : pick_mfma_sk<QD_DTYPE_BF16>(D);
+KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv) {
+  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D, nkv) : pick_mfma_sk<QD_DTYPE_BF16>(D, nkv);
 }
 
 template <int DT>
@@ -1177,11 +1259,23 @@ int resident_blocks(KernelFn fn, int threads) {
   return blocks;
 }
 
-// Waves per stream-K workgroup: the largest divisor of kv_heads <= 8, so
-// every wave serves the same number of kv-heads.
-int sk_wg_waves(int kv_heads) {
-  for (int n = kMaxWgWaves; n > 1; --n)
-    if (kv_heads % n == 0) return n;
+#ifndef QD_SK_DUAL_MIN_KV
+#define QD_SK_DUAL_MIN_KV 8
+#endif
+// Kv-heads per wave on the stream-K path: two when there are at least
+// QD_SK_DUAL_MIN_KV (an even number of) kv-heads and head_dim <= 128, so a
+// workgroup of one wave per SIMD still covers whole rows; else one.
+int sk_kv_per_wave(int kv_heads, int head_dim) {
+  return (head_dim <= 128 && kv_heads % 2 == 0 && kv_heads >= QD_SK_DUAL_MIN_KV) ? 2 : 1;
+}
+
+// Waves per stream-K workgroup: the largest divisor of kv_heads / nkv that
+// fits the kernel's bound, so every wave serves the same number of
+// kv-heads.
+int sk_wg_waves(int kv_heads, int nkv, int head_dim) {
+  const int units = kv_heads / nkv;
+  for (int n = (nkv == 1 && head_dim <= 128) ? kMaxWgWaves : kMaxWgWaves / 2; n > 1; --n)
+    if (units % n == 0) return n;
   return 1;
 }
 
@@ -1193,6 +1287,7 @@ struct AutoPlan {
   bool stream_k;
   int wgs;          // stream-K grid (workgroups)
   int wg_waves;     // stream-K waves per workgroup
+  int kv_per_wave;  // stream-K kv-heads per wave
   int splits;       // explicit-split path
   int chunk_pages;
   size_t ws_bytes;  // control region + scratch
@@ -1203,15 +1298,16 @@ struct AutoPlan {
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
               int dtype, bool aligned, AutoPlan* ap) {
-  *ap = AutoPlan{false, 0, 1, 1, 0, 0, 0};
+  *ap = AutoPlan{false, 0, 1, 1, 1, 0, 0, 0};
   if (batch <= 0) return QD_OK;
   const size_t ctrl = control_bytes(batch);
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
-    const int nw = sk_wg_waves(kv_heads);
+    const int nkv = sk_kv_per_wave(kv_heads, head_dim);
+    const int nw = sk_wg_waves(kv_heads, nkv, head_dim);
     const int64_t gmax = static_cast<int64_t>(batch) *
                          ((static_cast<int64_t>(max_pages) * block_size + 15) / 16);
-    int64_t w = static_cast<int64_t>(resident_blocks(pick_mfma_sk_dt(dtype, head_dim), 64 * nw)) *
+    int64_t w = static_cast<int64_t>(resident_blocks(pick_mfma_sk_dt(dtype, head_dim, nkv), 64 * nw)) *
                 kSkOversubscribe;
     const int64_t by_work = (gmax + kSkMinGroups - 1) / kSkMinGroups;
     if (w > by_work) w = by_work;
@@ -1219,6 +1315,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     ap->stream_k = true;
     ap->wgs = static_cast<int>(w);
     ap->wg_waves = nw;
+    ap->kv_per_wave = nkv;
     ap->meta_offset = static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
     ap->ws_bytes = ctrl + ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
     return QD_OK;
@@ -1509,7 +1606,8 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (stages & QD_STAGE_DECODE)
-    hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
+    hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0,
+                       stm, prm);
   if (stages & QD_STAGE_MERGE)
     hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim), dim3(kv_heads, batch), dim3(64), 0, stm, prm);
   return launch_error();

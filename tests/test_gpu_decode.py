@@ -392,8 +392,14 @@ def test_auto_workspace_reuse_across_length_mixes(gpu):
         assert torch.count_nonzero(ws[:ctrl]) == 0, "control region not left zero" 
 
 
-@pytest.mark.parametrize("lengths", [[1] * 300, [0] * 5 + [33], [16] * 64, [1, 0, 2, 0, 15, 16, 17]],
-                         ids=["ones", "zeros-then-one", "one-group-each", "tiny-mix"])
+_BIG_MIX = [int(x) for x in np.random.default_rng(5).integers(0, 120, 520)]
+for _i in range(0, 520, 37):
+    _BIG_MIX[_i] = 0
+
+
+@pytest.mark.parametrize("lengths", [[1] * 300, [0] * 5 + [33], [16] * 64, [1, 0, 2, 0, 15, 16, 17],
+                                     _BIG_MIX],
+                         ids=["ones", "zeros-then-one", "one-group-each", "tiny-mix", "b520-with-zeros"])
 def test_auto_tiny_items(gpu, lengths):
     say(f"auto tiny items {lengths[:8]}... (B={len(lengths)})")
     case = to_dev(make_decode_case(lengths=lengths, q_heads=16, kv_heads=2, head_dim=64, block_size=16,
