@@ -84,6 +84,11 @@ def lib():
         L.qd_gqa_decode_auto_stages.argtypes = (
             [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
             + [ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_void_p])
+        L.qd_kv_append_validate.restype = ctypes.c_int
+        L.qd_kv_append_validate.argtypes = [P] * 6 + [ctypes.c_char_p, ctypes.c_size_t]
+        L.qd_kv_append_launch.restype = ctypes.c_int
+        L.qd_kv_append_launch.argtypes = ([ctypes.c_void_p] * 6 + [ctypes.c_int] * 5 + [ctypes.c_int64]
+                                          + [ctypes.c_int, ctypes.c_void_p])
         L.qd_gqa_decode_auto_info.restype = ctypes.c_int
         L.qd_gqa_decode_auto_info.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int)] * 3
         _lib = L
@@ -165,3 +170,19 @@ def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None
         q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), lens.data_ptr(), out.data_ptr(),
         ws_ptr, ws_bytes, B, Hq, Hkv, D, P, table.shape[1], k.shape[0], DTYPE[q.dtype], float(scale),
         stages, stream)
+
+
+def validate_kv_append(key, value, kc, vc, table, pos):
+    buf = ctypes.create_string_buffer(256)
+    rc = lib().qd_kv_append_validate(*(ctypes.byref(d) for d in (key, value, kc, vc, table, pos)), buf, 256)
+    return rc, buf.value.decode()
+
+
+def kv_append_launch(key, value, kc, vc, table, pos, stream=None):
+    """Calls qd_kv_append_launch on torch device tensors (no validation)."""
+    B, Hkv, D = key.shape
+    if stream is None:
+        stream = torch.cuda.current_stream(key.device).cuda_stream if key.is_cuda else 0
+    return lib().qd_kv_append_launch(key.data_ptr(), value.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                     table.data_ptr(), pos.data_ptr(), B, Hkv, D, kc.shape[1],
+                                     table.shape[1], kc.shape[0], DTYPE[key.dtype], stream)

@@ -110,3 +110,14 @@ def gqa_decode_auto(q, k_cache, v_cache, block_table, context_lens, *, scale=Non
     if q.ndim != 3 or k_cache.ndim != 4 or block_table.ndim != 2:
         raise ValueError('invalid decode input dimensions')
     return gqa_decode(q, k_cache, v_cache, block_table, context_lens, scale=scale)
+
+
+def kv_append(key, value, k_cache, v_cache, block_table, positions):
+    """Writes one token per sequence into the paged caches (reference
+    ``core.py:59-63``): ``key``/``value`` ``[B, Hkv, D]`` go to row
+    ``(block_table[b, pos // P], pos % P)``.  Destinations are caller-owned
+    and must be distinct; a position or page id outside the table or the
+    pool is skipped rather than written."""
+    if _LOAD_ERROR is not None:
+        raise RuntimeError("qd_attention HIP extension was not loaded") from _LOAD_ERROR
+    torch.ops.qd_attention.kv_append(key, value, k_cache, v_cache, block_table, positions)

@@ -1102,9 +1102,18 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeParams p) {
 thread_local std::string g_last_error;
 thread_local int g_last_status = 0;
 
-int fail(int status, const std::string& msg) {
+}  // namespace
+
+// Shared with the other entry points of the library (kv_append.hip).
+void qd_set_last_error(int status, const std::string& msg) {
   g_last_status = status;
   g_last_error = msg;
+}
+
+namespace {
+
+int fail(int status, const std::string& msg) {
+  qd_set_last_error(status, msg);
   return status;
 }
 

@@ -1,7 +1,7 @@
 // Thin PyTorch-ROCm binding: registers the reference's `qd_attention` op
 // schemas and forwards to the C ABI of libqd_attention.so.
 //
-// Schemas   csrc/binding/torch_ops.cpp:53-56 (reference tree)
+// Schemas   csrc/binding/torch_ops.cpp:52-56 (reference tree)
 // Impl key  CUDA (PyTorch-ROCm's key for HIP devices), as torch_ops.cpp:59-77
 // Host path csrc/cuda/dense/gqa_decode.cu:96-183: validation in the
 //           reference's order and words, device guard, empty_like output,
@@ -157,9 +157,32 @@ at::Tensor gqa_decode_split_workspace_hip(const at::Tensor& q, const at::Tensor&
   return decode_impl(q, k, v, table, lens, scale, splits, workspace);
 }
 
+// kv_append (reference kv_append.cu:29-56): validation in the reference's
+// order and words, device guard, B == 0 no-op, launch on the current stream.
+void kv_append_hip(const at::Tensor& key, const at::Tensor& value, at::Tensor k_cache, at::Tensor v_cache,
+                   const at::Tensor& table, const at::Tensor& positions) {
+  const qd_tensor_desc dk = describe(key), dv = describe(value), dkc = describe(k_cache),
+                       dvc = describe(v_cache), dt = describe(table), dp = describe(positions);
+  char msg[256];
+  int st = qd_kv_append_validate(&dk, &dv, &dkc, &dvc, &dt, &dp, msg, sizeof(msg));
+  TORCH_CHECK(st == QD_OK, msg);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
+  if (key.size(0) == 0) return;
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
+  st = qd_kv_append_launch(key.data_ptr(), value.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                           table.data_ptr<int32_t>(), positions.data_ptr<int32_t>(),
+                           static_cast<int>(key.size(0)), static_cast<int>(key.size(1)),
+                           static_cast<int>(key.size(2)), static_cast<int>(k_cache.size(1)),
+                           static_cast<int>(table.size(1)), k_cache.size(0), dk.dtype, stream);
+  TORCH_CHECK(st == QD_OK, qd_error_string(st));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(qd_attention, m) {
+  m.def(
+      "kv_append(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor block_table, "
+      "Tensor positions) -> ()");
   m.def(
       "gqa_decode_split_workspace(Tensor q, Tensor k, Tensor v, Tensor table, Tensor lengths, "
       "float scale, int splits, Tensor(a!) workspace) -> Tensor");
@@ -172,6 +195,7 @@ TORCH_LIBRARY(qd_attention, m) {
 }
 
 TORCH_LIBRARY_IMPL(qd_attention, CUDA, m) {
+  m.impl("kv_append", TORCH_FN(kv_append_hip));
   m.impl("gqa_decode_split_workspace", TORCH_FN(gqa_decode_split_workspace_hip));
   m.impl("gqa_decode_split", TORCH_FN(gqa_decode_split_hip));
   m.impl("gqa_decode", TORCH_FN(gqa_decode_hip));

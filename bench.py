@@ -56,6 +56,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=5)
     ap.add_argument("--mode", choices=["decode", "copy"], default="decode")
+    ap.add_argument("--op", choices=["decode", "kv_append"], default="decode",
+                    help="kv_append: time the paged cache append on the config's shapes instead")
     ap.add_argument("--device-gen", action="store_true", help="draw inputs on the GPU")
     return ap.parse_args()
 
@@ -146,6 +148,62 @@ def profiled_traffic(kernel: str, config: str):
     return None
 
 
+def kv_append_mode(args) -> None:
+    """One step = one attention_amd.kv_append call writing one token per
+    sequence of the config (positions = length - 1, rotating over cache
+    pools above the Infinity Cache size).  Bytes = key+value read and the
+    two cache rows written per sequence, plus the table entry and position."""
+    import attention_amd
+    from attention_amd.cases import CONFIGS
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    lengths = cfg.lengths()
+    _, k, v, table, lens = cfg.make(device=dev, device_gen=True, lengths=lengths)
+    B, Hkv, D = cfg.batch, cfg.kv_heads, cfg.head_dim
+    gen = torch.Generator(device=dev).manual_seed(7)
+    key = torch.randn(B, Hkv, D, device=dev, generator=gen).to(cfg.dtype)
+    value = torch.randn(B, Hkv, D, device=dev, generator=gen).to(cfg.dtype)
+    pos = (lens - 1).clamp(min=0).to(torch.int32)
+    kv_bytes = 2 * k.numel() * k.element_size()
+    pools = max(2, math.ceil(768e6 / kv_bytes))
+    ks, vs = [k], [v]
+    for _ in range(1, pools):
+        ks.append(torch.empty_like(k))
+        vs.append(torch.empty_like(v))
+    stream = torch.cuda.current_stream(dev)
+    ms = time_loop(lambda i: attention_amd.kv_append(key, value, ks[i % pools], vs[i % pools], table, pos),
+                   args.steps, args.warmup, stream)
+    s = key.element_size()
+    nbytes = 4 * B * Hkv * D * s + 8 * B
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    # CPU baseline: the reference's comparator, torch indexed assignment
+    # (benchmarks/bench_all_operators.py:100-102), on the host copies.
+    kc, vc, tc, pc, kk, vv = (x.cpu() for x in (k, v, table, pos, key, value))
+    idx = torch.arange(B)
+    page, slot = tc[idx, (pc // cfg.block_size).long()].long(), (pc % cfg.block_size).long()
+    times = []
+    for _ in range(max(5, args.cpu_repeats)):
+        t0 = time.perf_counter()
+        kc[page, slot] = kk
+        vc[page, slot] = vv
+        times.append(time.perf_counter() - t0)
+    t_cpu = statistics.median(times)
+    print(json.dumps({
+        "metric": "paged KV append µs/call and achieved HBM GB/s, 1 MI355X",
+        "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 3),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+        "higher_is_better": True, "dtype": DT_NAME[cfg.dtype], "data": "synthetic",
+        "config": {"workload": f"kv_append on {cfg.name} shapes", "batch": B, "kv_heads": Hkv,
+                   "head_dim": D, "block_size": cfg.block_size, "bytes_per_call": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 5), "traffic": None,
+                     "note": "launch-bound: one token per sequence is a few hundred KB"},
+        "cpu_baseline": {"value": round(nbytes / t_cpu / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+                         "kind": "port", "sample": f"torch indexed assignment on CPU, median {t_cpu * 1e6:.1f} us"},
+    }), flush=True)
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -168,6 +226,9 @@ def main() -> None:
         sys.exit(2)
     if args.mode == "copy":
         copy_mode(args)
+        return
+    if args.op == "kv_append":
+        kv_append_mode(args)
         return
 
     import attention_amd

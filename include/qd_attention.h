@@ -186,6 +186,29 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
 int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, int block_size,
                             int max_pages, int dtype, int* waves, int* splits, int* chunk_pages);
 
+/* ---- Paged KV-cache append ------------------------------------------
+ * Replaces csrc/cuda/cache/kv_append.cu:29-56 (kv_append_cuda) behind the
+ * op kv_append (csrc/binding/torch_ops.cpp:52; attention/core.py:59-63).
+ *   key, value   [batch, kv_heads, head_dim]                   dtype
+ *   k/v cache    [num_blocks, block_size, kv_heads, head_dim]  dtype (written)
+ *   block_table  [batch, max_pages] int32, positions [batch] int32
+ * Sequence b's token goes to row (block_table[b][pos/block_size],
+ * pos % block_size) of both caches.  Destinations are caller-owned and
+ * must be distinct; a position outside [0, max_pages*block_size) or a page
+ * id outside [0, num_blocks) is skipped (never written). */
+
+/* The reference's checks in order (kv_append.cu:32-43), messages included. */
+int qd_kv_append_validate(const qd_tensor_desc* key, const qd_tensor_desc* value,
+                          const qd_tensor_desc* k_cache, const qd_tensor_desc* v_cache,
+                          const qd_tensor_desc* block_table, const qd_tensor_desc* positions, char* msg,
+                          size_t msg_cap);
+
+/* Enqueues the append on `stream`; no allocation, no synchronization. */
+int qd_kv_append_launch(const void* key, const void* value, void* k_cache, void* v_cache,
+                        const int32_t* block_table, const int32_t* positions, int batch, int kv_heads,
+                        int head_dim, int block_size, int max_pages, int64_t num_blocks, int dtype,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

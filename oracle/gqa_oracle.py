@@ -256,6 +256,36 @@ def merge_partials(part, out_dtype="f32"):
 
 
 # ----------------------------------------------------------------------------
+# KV-cache append: reference csrc/cuda/cache/kv_append.cu:11-19
+# ----------------------------------------------------------------------------
+
+
+def oracle_kv_append(key, value, k_cache, v_cache, table, positions):
+    """Returns copies of the caches after writing sequence b's [Hkv, D] key and
+    value row to (table[b, pos // P], pos % P) (kv_append.cu:12-18).  The
+    reference leaves out-of-range metadata to the caller; here, as in the
+    HIP kernel, a position outside [0, maxP*P) or a page id outside [0, N)
+    writes nothing.  Sequences are applied in order (the reference requires
+    distinct destinations, so order does not matter for valid input)."""
+    kc = np.array(k_cache, copy=True)
+    vc = np.array(v_cache, copy=True)
+    table = np.asarray(table)
+    positions = np.asarray(positions)
+    nblocks, block_size = kc.shape[0], kc.shape[1]
+    max_pages = table.shape[1]
+    for b in range(positions.shape[0]):
+        t = int(positions[b])
+        if t < 0 or t >= max_pages * block_size:
+            continue
+        phys = int(table[b, t // block_size])
+        if phys < 0 or phys >= nblocks:
+            continue
+        kc[phys, t % block_size] = key[b]
+        vc[phys, t % block_size] = value[b]
+    return kc, vc
+
+
+# ----------------------------------------------------------------------------
 # C restatement (oracle/gqa_oracle.c) through ctypes
 # ----------------------------------------------------------------------------
 

@@ -275,6 +275,62 @@ def test_auto_batch_zero_is_a_no_op():
 
 
 # ----------------------------------------------------------------------------
+# kv_append boundary (reference csrc/cuda/cache/kv_append.cu:32-45)
+# ----------------------------------------------------------------------------
+
+def kv_good():
+    return [cabi.desc([4, 2, 64], BF16), cabi.desc([4, 2, 64], BF16), cabi.desc([57, 16, 2, 64], BF16),
+            cabi.desc([57, 16, 2, 64], BF16), cabi.desc([4, 32], I32), cabi.desc([4], I32)]
+
+
+def _kv(mutate):
+    d = kv_good()
+    mutate(d)
+    return cabi.validate_kv_append(*d)
+
+
+KV_ORDER = [
+    (lambda d: None, ""),
+    (_set(0, is_device=0), "all tensors must be contiguous CUDA tensors"),
+    (_set(3, contiguous=0), "all tensors must be contiguous CUDA tensors"),
+    (_set(5, device_index=1), "all tensors must share a device"),
+    (_set(0, sizes=[4, 2]), "key/value must be [B, Hkv, D]"),
+    (_set(1, sizes=[4, 2, 32]), "key/value must be [B, Hkv, D]"),
+    (_set(2, sizes=[57, 16, 2]), "cache must be [Nblocks, P, Hkv, D]"),
+    (_set(3, sizes=[57, 16, 2, 32]), "cache must be [Nblocks, P, Hkv, D]"),
+    (lambda d: (_set(2, sizes=[57, 16, 4, 64])(d), _set(3, sizes=[57, 16, 4, 64])(d)), "cache head shape mismatch"),
+    (lambda d: (_set(2, sizes=[0, 16, 2, 64])(d), _set(3, sizes=[0, 16, 2, 64])(d)), "invalid dimensions"),
+    (_set(4, sizes=[3, 32]), "invalid metadata shape"),
+    (_set(4, sizes=[4, 0]), "invalid metadata shape"),
+    (_set(5, sizes=[4, 1]), "invalid metadata shape"),
+    (_set(4, dtype=5), "metadata must be int32"),
+    (_set(2, dtype=F16), "dtype mismatch"),
+    (lambda d: [setattr(x, "dtype", 5) for x in d[:4]], "unsupported dtype"),
+]
+
+
+@pytest.mark.parametrize("i", range(len(KV_ORDER)))
+def test_kv_append_validation_in_reference_order(i):
+    mutate, msg = KV_ORDER[i]
+    rc, got = _kv(mutate)
+    assert (rc == 0) == (msg == "")
+    assert got == msg
+
+
+def test_kv_append_launch_argument_errors():
+    L = cabi.lib()
+    args = [1, 1, 1, 1, 1, 1, 4, 2, 64, 16, 32, 57, BF16, None]
+    assert L.qd_kv_append_launch(*args[:12], 5, None) == 1
+    assert cabi.error_string(1) == "unsupported dtype"
+    bad = list(args)
+    bad[10] = 0
+    assert L.qd_kv_append_launch(*bad) == 1 and cabi.error_string(1) == "invalid dimensions"
+    zero = list(args)
+    zero[6] = 0
+    assert L.qd_kv_append_launch(*zero) == 0                     # batch 0: nothing enqueued
+
+
+# ----------------------------------------------------------------------------
 # Torch op surface and Python API
 # ----------------------------------------------------------------------------
 
@@ -289,6 +345,9 @@ def test_op_schemas_match_reference():
     assert str(ops.gqa_decode_split_workspace.default._schema) == (
         "qd_attention::gqa_decode_split_workspace(Tensor q, Tensor k, Tensor v, Tensor table, "
         "Tensor lengths, float scale, int splits, Tensor(a!) workspace) -> Tensor")
+    assert str(ops.kv_append.default._schema) == (
+        "qd_attention::kv_append(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+        "Tensor block_table, Tensor positions) -> ()")
 
 
 def test_cpu_tensors_have_no_kernel():
@@ -301,7 +360,7 @@ def test_cpu_tensors_have_no_kernel():
 
 def test_public_api_surface():
     assert attention_amd.is_cuda_extension_loaded()
-    for name in ["gqa_decode", "gqa_decode_split", "gqa_decode_auto", "is_cuda_extension_loaded"]:
+    for name in ["gqa_decode", "gqa_decode_split", "gqa_decode_auto", "kv_append", "is_cuda_extension_loaded"]:
         assert name in attention_amd.__all__
 
 

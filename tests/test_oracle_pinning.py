@@ -344,3 +344,46 @@ def test_planted_mutants_are_caught(kind):
     np.testing.assert_allclose(O.brute_force_f64(q, k, v, t, l), ref, rtol=1e-10, atol=1e-12)
     got = _mutant(kind)(q, k, v, t, l)
     assert not np.allclose(got, ref, rtol=1e-3, atol=1e-4), f"mutant {kind} not detected"
+
+
+# ----------------------------------------------------------------------------
+# kv_append oracle (reference csrc/cuda/cache/kv_append.cu:11-19)
+# ----------------------------------------------------------------------------
+
+def test_kv_append_oracle_matches_torch_indexed_assignment():
+    """The reference's own check (benchmarks/bench_all_operators.py:100-104):
+    k[page, slot] = key with page = table[b, pos // P], slot = pos % P."""
+    gen = torch.Generator().manual_seed(3)
+    B, Hkv, D, P, maxP, N = 6, 3, 5, 4, 4, 40
+    kc = torch.randn(N, P, Hkv, D, generator=gen)
+    vc = torch.randn(N, P, Hkv, D, generator=gen)
+    table = torch.randperm(N, generator=gen)[:B * maxP].view(B, maxP).int()
+    pos = torch.tensor([0, 3, 4, 15, 7, 9], dtype=torch.int32)
+    key = torch.randn(B, Hkv, D, generator=gen)
+    value = torch.randn(B, Hkv, D, generator=gen)
+    got_k, got_v = O.oracle_kv_append(key.numpy(), value.numpy(), kc.numpy(), vc.numpy(), table.numpy(),
+                                      pos.numpy())
+    idx = torch.arange(B)
+    page = table[idx, (pos // P).long()].long()
+    slot = (pos % P).long()
+    ref_k, ref_v = kc.clone(), vc.clone()
+    ref_k[page, slot] = key
+    ref_v[page, slot] = value
+    assert np.array_equal(got_k, ref_k.numpy()) and np.array_equal(got_v, ref_v.numpy())
+
+
+def test_kv_append_oracle_touches_only_destinations_and_skips_invalid():
+    rng = np.random.default_rng(0)
+    kc = rng.standard_normal((10, 4, 2, 3)).astype(np.float32)
+    vc = rng.standard_normal((10, 4, 2, 3)).astype(np.float32)
+    table = np.array([[1, 2], [3, -1], [9, 10]], dtype=np.int32)   # 10 is out of the pool
+    pos = np.array([5, 4, 4], dtype=np.int32)                      # b1 -> page -1, b2 -> page 10
+    key = np.full((3, 2, 3), 7.0, np.float32)
+    val = np.full((3, 2, 3), 8.0, np.float32)
+    nk, nv = O.oracle_kv_append(key, val, kc, vc, table, pos)
+    changed = np.argwhere(np.any(nk != kc, axis=(2, 3)))
+    assert changed.tolist() == [[2, 1]]                             # only (table[0][1], 5 % 4)
+    assert np.all(nk[2, 1] == 7.0) and np.all(nv[2, 1] == 8.0)
+    for bad in ([-1, 8, 100], [8, -5, 9]):                          # all outside [0, maxP*P)
+        k2, v2 = O.oracle_kv_append(key, val, kc, vc, table, np.array(bad, np.int32))
+        assert np.array_equal(k2, kc) and np.array_equal(v2, vc)
