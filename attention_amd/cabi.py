@@ -89,6 +89,9 @@ def lib():
         L.qd_kv_append_launch.restype = ctypes.c_int
         L.qd_kv_append_launch.argtypes = ([ctypes.c_void_p] * 6 + [ctypes.c_int] * 5 + [ctypes.c_int64]
                                           + [ctypes.c_int, ctypes.c_void_p])
+        L.qd_validate_paged_metadata.restype = ctypes.c_int
+        L.qd_validate_paged_metadata.argtypes = ([ctypes.c_void_p] * 3 + [ctypes.c_int] * 3
+                                                 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p])
         L.qd_gqa_decode_auto_info.restype = ctypes.c_int
         L.qd_gqa_decode_auto_info.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int)] * 3
         _lib = L

@@ -209,6 +209,31 @@ int qd_kv_append_launch(const void* key, const void* value, void* k_cache, void*
                         int head_dim, int block_size, int max_pages, int64_t num_blocks, int dtype,
                         void* stream);
 
+/* ---- Paged metadata validation --------------------------------------
+ * Device-side body of attention.validation.validate_paged_metadata
+ * (attention/validation.py:5-39).  Checks, per sequence b in order: the
+ * length is in [0, max_pages*block_size]; every used page id
+ * (ceil(len/block_size) of them) is in [0, num_blocks); and, when
+ * `positions` is not NULL, the append position is in
+ * [0, max_pages*block_size), its page id is in [0, num_blocks) and its
+ * (page, slot) destination is not taken by an earlier sequence.
+ * Writes to device memory `*result` the first failure in the reference's
+ * order as (b << 35) | (check << 32) | page, or all ones when the metadata
+ * is valid; `page` is the failing page index for QD_META_BAD_PAGE.
+ * Enqueues two kernels on `stream`; the caller reads *result after them.
+ * Requires batch < 2^28, max_pages > 0, block_size > 0, num_blocks > 0. */
+enum {
+  QD_META_BAD_LENGTH = 1,      /* "invalid length at batch {b}"          */
+  QD_META_BAD_PAGE = 2,        /* "invalid block at batch {b}, page {p}" */
+  QD_META_BAD_POSITION = 3,    /* "invalid append position at batch {b}" */
+  QD_META_BAD_APPEND_PAGE = 4, /* "invalid append page at batch {b}"     */
+  QD_META_CONFLICT = 5         /* "conflicting append destinations"      */
+};
+
+int qd_validate_paged_metadata(const int32_t* block_table, const int32_t* context_lens,
+                               const int32_t* positions, int batch, int max_pages, int block_size,
+                               int64_t num_blocks, unsigned long long* result, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

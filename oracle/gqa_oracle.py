@@ -286,6 +286,41 @@ def oracle_kv_append(key, value, k_cache, v_cache, table, positions):
 
 
 # ----------------------------------------------------------------------------
+# Metadata validation: reference attention/validation.py:23-38
+# ----------------------------------------------------------------------------
+
+
+def oracle_validate_metadata(table, lens, block_size, num_blocks, positions=None):
+    """First failure message of the reference's host loop, or None.
+
+    Per sequence b in order (validation.py:23-38): length in
+    [0, maxP*P]; each used page id in [0, num_blocks); then, when appending,
+    position in [0, maxP*P), its page id in [0, num_blocks), and a
+    (page, slot) destination not seen for an earlier sequence."""
+    table = np.asarray(table)
+    max_pages = table.shape[1]
+    seen = set()
+    for b, length in enumerate(np.asarray(lens).tolist()):
+        if not 0 <= length <= max_pages * block_size:
+            return f'invalid length at batch {b}'
+        for p in range((length + block_size - 1) // block_size):
+            if not 0 <= int(table[b, p]) < num_blocks:
+                return f'invalid block at batch {b}, page {p}'
+        if positions is not None:
+            t = int(positions[b])
+            if not 0 <= t < max_pages * block_size:
+                return f'invalid append position at batch {b}'
+            page = int(table[b, t // block_size])
+            if not 0 <= page < num_blocks:
+                return f'invalid append page at batch {b}'
+            dest = (page, t % block_size)
+            if dest in seen:
+                return 'conflicting append destinations'
+            seen.add(dest)
+    return None
+
+
+# ----------------------------------------------------------------------------
 # C restatement (oracle/gqa_oracle.c) through ctypes
 # ----------------------------------------------------------------------------
 

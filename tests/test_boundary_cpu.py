@@ -382,3 +382,17 @@ def test_backend_and_dimension_errors():
         attention_amd.gqa_decode_split(q, q, q, q, q, backend="cpu")
     with pytest.raises(ValueError, match="invalid decode input dimensions"):
         attention_amd.gqa_decode_auto(q, q, q, q, q)
+
+
+def test_validate_paged_metadata_argument_errors():
+    from attention_amd.validation import validate_paged_metadata as vpm
+    t = torch.zeros(2, 3, dtype=torch.int32)
+    l = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="block_size and num_blocks must be positive"):
+        vpm(t, l, block_size=0, num_blocks=4)
+    with pytest.raises(ValueError, match=r"metadata shapes must be \[B,MaxPages\] and \[B\]"):
+        vpm(t, l[:1], block_size=16, num_blocks=4)
+    with pytest.raises(ValueError, match="metadata must be int32"):
+        vpm(t.long(), l, block_size=16, num_blocks=4)
+    with pytest.raises(ValueError, match=r"positions must be int32 \[B\]"):
+        vpm(t, l, block_size=16, num_blocks=4, positions=l.long())

@@ -387,3 +387,61 @@ def test_kv_append_oracle_touches_only_destinations_and_skips_invalid():
     for bad in ([-1, 8, 100], [8, -5, 9]):                          # all outside [0, maxP*P)
         k2, v2 = O.oracle_kv_append(key, val, kc, vc, table, np.array(bad, np.int32))
         assert np.array_equal(k2, kc) and np.array_equal(v2, vc)
+
+
+# ----------------------------------------------------------------------------
+# Metadata validation oracle (reference attention/validation.py:5-39): each
+# failure kind built by hand, and the order between them.
+# ----------------------------------------------------------------------------
+
+def _meta():
+    table = np.array([[0, 1, -1], [2, 3, 4], [5, -1, -1]], dtype=np.int32)
+    lens = np.array([20, 33, 1], dtype=np.int32)   # P = 16: 2, 3 and 1 used pages
+    return table, lens
+
+
+def test_validation_oracle_accepts_valid_metadata():
+    table, lens = _meta()
+    assert O.oracle_validate_metadata(table, lens, 16, 6) is None
+    assert O.oracle_validate_metadata(table, lens, 16, 6, positions=np.array([20, 33, 1])) is None
+
+
+@pytest.mark.parametrize("edit,expected", [
+    (lambda t, l, p: l.__setitem__(1, 49), "invalid length at batch 1"),          # 49 > 3*16
+    (lambda t, l, p: l.__setitem__(0, -1), "invalid length at batch 0"),
+    (lambda t, l, p: t.__setitem__((1, 2), 6), "invalid block at batch 1, page 2"),
+    (lambda t, l, p: t.__setitem__((0, 1), -1), "invalid block at batch 0, page 1"),
+    (lambda t, l, p: t.__setitem__((0, 2), 99), None),                              # unused page never read
+    (lambda t, l, p: p.__setitem__(2, 48), "invalid append position at batch 2"),  # 48 = 3*16
+    (lambda t, l, p: p.__setitem__(2, 16), "invalid append page at batch 2"),      # row 2, page 1 is -1
+])
+def test_validation_oracle_failure_kinds(edit, expected):
+    table, lens = _meta()
+    pos = np.array([20, 33, 1], dtype=np.int32)
+    edit(table, lens, pos)
+    assert O.oracle_validate_metadata(table, lens, 16, 6, positions=pos) == expected
+
+
+def test_validation_oracle_conflict_is_reported_at_the_later_sequence():
+    table = np.array([[0, 1, -1], [2, 3, 4], [5, 3, -1]], dtype=np.int32)
+    lens = np.array([20, 33, 17], dtype=np.int32)
+    # b1 writes (page 3, slot 1) at position 17; b2 at position 17 writes the same slot.
+    assert O.oracle_validate_metadata(table, lens, 16, 6, positions=np.array([20, 17, 17])) == \
+        "conflicting append destinations"
+    # Same page, different slot: no conflict.
+    assert O.oracle_validate_metadata(table, lens, 16, 6, positions=np.array([20, 17, 18])) is None
+    # An earlier failure wins over the conflict.
+    assert O.oracle_validate_metadata(table, np.array([20, 99, 17]), 16, 6,
+                                      positions=np.array([20, 17, 17])) == "invalid length at batch 1"
+
+
+def test_validation_oracle_reports_first_sequence_and_check_order():
+    table, lens = _meta()
+    pos = np.array([20, 33, 1], dtype=np.int32)
+    table[2, 0] = 9                    # b2: bad block
+    lens[1] = 100                      # b1: bad length (earlier sequence wins)
+    assert O.oracle_validate_metadata(table, lens, 16, 6, positions=pos) == "invalid length at batch 1"
+    lens[1] = 33
+    pos[1] = 99                        # b1: bad position, but b1's pages are checked first
+    table[1, 0] = -3
+    assert O.oracle_validate_metadata(table, lens, 16, 6, positions=pos) == "invalid block at batch 1, page 0"
