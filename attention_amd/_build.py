@@ -56,7 +56,7 @@ def _run(cmd: list[str], verbose: bool) -> None:
 def hip_library_cmd() -> list[str]:
     return [_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
             os.path.join(CSRC, "gqa_decode.hip"), os.path.join(CSRC, "kv_append.hip"),
-            os.path.join(CSRC, "validate.hip"),
+            os.path.join(CSRC, "validate.hip"), os.path.join(CSRC, "mla.hip"),
             "-o", HIP_LIB + ".tmp", f"-Wl,-rpath,{ROCM}/lib"]
 
 

@@ -17,7 +17,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 HEADER = os.path.join(os.path.dirname(PKG), "include", "qd_attention.h")
 LIB_PATH = os.path.join(PKG, "lib", "libqd_attention.so")
 
-DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.int32: 3}
+DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.int32: 3, torch.int64: 4}
 QD_FLAG_FORCE_GENERIC = 1
 QD_STAGE_DECODE, QD_STAGE_MERGE, QD_STAGE_ALL = 1, 2, 3
 
@@ -94,6 +94,32 @@ def lib():
                                                  + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p])
         L.qd_gqa_decode_auto_info.restype = ctypes.c_int
         L.qd_gqa_decode_auto_info.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int)] * 3
+        V, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+        MSG = [ctypes.c_char_p, ctypes.c_size_t]
+        L.qd_latent_kv_write_validate.restype = I
+        L.qd_latent_kv_write_validate.argtypes = [P] * 4 + MSG
+        L.qd_latent_kv_write.restype = I
+        L.qd_latent_kv_write.argtypes = [V] * 4 + [I64, I, I, I64, I, V]
+        L.qd_mla_project_validate.restype = I
+        L.qd_mla_project_validate.argtypes = [P, P, I] + MSG
+        L.qd_mla_project.restype = I
+        L.qd_mla_project.argtypes = [V] * 3 + [I64] + [I] * 6 + [V]
+        L.qd_mla_attend_validate.restype = I
+        L.qd_mla_attend_validate.argtypes = [P] * 7 + [ctypes.c_double] + MSG
+        L.qd_mla_attend_workspace_bytes.restype = ctypes.c_size_t
+        L.qd_mla_attend_workspace_bytes.argtypes = [I] * 11
+        L.qd_mla_attend_info.restype = I
+        L.qd_mla_attend_info.argtypes = [I] * 11 + [ctypes.POINTER(I)] * 2
+        L.qd_mla_attend.restype = I
+        L.qd_mla_attend.argtypes = ([V] * 9 + [ctypes.c_size_t] + [I] * 7 + [I64] + [I] * 3 + [F]
+                                    + [I, I, V])
+        L.qd_mla_decode_validate.restype = I
+        L.qd_mla_decode_validate.argtypes = [P] * 9 + [ctypes.c_double] + MSG
+        L.qd_mla_decode_workspace_bytes.restype = ctypes.c_size_t
+        L.qd_mla_decode_workspace_bytes.argtypes = [I] * 11
+        L.qd_mla_decode.restype = I
+        L.qd_mla_decode.argtypes = ([V] * 11 + [ctypes.c_size_t] + [I] * 9 + [I64] + [I] * 3 + [F]
+                                    + [I, I, V])
         _lib = L
     return _lib
 
@@ -189,3 +215,98 @@ def kv_append_launch(key, value, kc, vc, table, pos, stream=None):
     return lib().qd_kv_append_launch(key.data_ptr(), value.data_ptr(), kc.data_ptr(), vc.data_ptr(),
                                      table.data_ptr(), pos.data_ptr(), B, Hkv, D, kc.shape[1],
                                      table.shape[1], kc.shape[0], DTYPE[key.dtype], stream)
+
+
+# ---- Paged MLA decode ------------------------------------------------------
+
+
+def _stream(t, stream):
+    if stream is None:
+        return torch.cuda.current_stream(t.device).cuda_stream if t.is_cuda else 0
+    return stream
+
+
+def _msg_call(fn, *args):
+    buf = ctypes.create_string_buffer(256)
+    rc = fn(*args, buf, 256)
+    return rc, buf.value.decode()
+
+
+def _ref(d):
+    return None if d is None else ctypes.byref(d)
+
+
+def validate_latent_kv_write(latent, rope, cache, slots):
+    return _msg_call(lib().qd_latent_kv_write_validate, *(ctypes.byref(d) for d in (latent, rope, cache, slots)))
+
+
+def validate_mla_project(x, w, absorb):
+    return _msg_call(lib().qd_mla_project_validate, ctypes.byref(x), ctypes.byref(w), int(absorb))
+
+
+def validate_mla_attend(q, qr, cache, table, lens, pos, indices=None, scale=0.1):
+    return _msg_call(lib().qd_mla_attend_validate, *(ctypes.byref(d) for d in (q, qr, cache, table, lens, pos)),
+                     _ref(indices), scale)
+
+
+def validate_mla_decode(q, qr, cache, table, lens, pos, wk, wv, indices=None, scale=0.1):
+    return _msg_call(lib().qd_mla_decode_validate,
+                     *(ctypes.byref(d) for d in (q, qr, cache, table, lens, pos, wk, wv)), _ref(indices), scale)
+
+
+def mla_attend_info(B, T, H, Dc, Dr, P, maxP, nk=-1, dtype=2, splits=0, flags=0):
+    """(kind, splits, head_groups); kind 1 = MFMA kernel, 0 = VALU kernel."""
+    s, g = ctypes.c_int(), ctypes.c_int()
+    kind = lib().qd_mla_attend_info(B, T, H, Dc, Dr, P, maxP, nk, dtype, splits, flags, ctypes.byref(s),
+                                    ctypes.byref(g))
+    return kind, s.value, g.value
+
+
+def latent_kv_write(latent, rope, cache, slots, stream=None):
+    return lib().qd_latent_kv_write(latent.data_ptr(), rope.data_ptr(), cache.data_ptr(), slots.data_ptr(),
+                                    latent.shape[0], latent.shape[1], rope.shape[1],
+                                    cache.shape[0] * cache.shape[1], DTYPE[latent.dtype], _stream(latent, stream))
+
+
+def mla_project(x, w, out, absorb, flags=0, stream=None):
+    B, T, H, di = x.shape
+    dout = out.shape[-1]
+    return lib().qd_mla_project(x.data_ptr(), w.data_ptr(), out.data_ptr(), B * T, H, di, dout, int(absorb),
+                                DTYPE[x.dtype], flags, _stream(x, stream))
+
+
+def mla_attend(q, qr, cache, table, lens, pos, out, *, scale, indices=None, causal=True, splits=0, flags=0,
+               workspace=None, stream=None):
+    """Calls qd_mla_attend on torch device tensors (no validation); allocates
+    the split workspace when none is given."""
+    B, T, H, Dc = q.shape
+    Dr = qr.shape[-1]
+    nk = -1 if indices is None else indices.shape[-1]
+    need = lib().qd_mla_attend_workspace_bytes(B, T, H, Dc, Dr, cache.shape[1], table.shape[1], nk,
+                                               DTYPE[q.dtype], splits, flags)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    return lib().qd_mla_attend(q.data_ptr(), qr.data_ptr(), cache.data_ptr(), table.data_ptr(), lens.data_ptr(),
+                               pos.data_ptr(), None if indices is None else indices.data_ptr(), out.data_ptr(),
+                               ws_ptr, ws_bytes, B, T, H, Dc, Dr, cache.shape[1], table.shape[1], cache.shape[0],
+                               nk, int(causal), DTYPE[q.dtype], float(scale), splits, flags, _stream(q, stream))
+
+
+def mla_decode(q, qr, cache, table, lens, pos, wk, wv, out, *, scale, indices=None, causal=True, splits=0,
+               flags=0, stream=None):
+    """Calls qd_mla_decode on torch device tensors (no validation)."""
+    B, T, H, Dn = q.shape
+    Dr = qr.shape[-1]
+    Dc = wk.shape[-1]
+    Dv = wv.shape[1]
+    nk = -1 if indices is None else indices.shape[-1]
+    need = lib().qd_mla_decode_workspace_bytes(B, T, H, Dc, Dr, cache.shape[1], table.shape[1], nk,
+                                               DTYPE[q.dtype], splits, flags)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    return lib().qd_mla_decode(q.data_ptr(), qr.data_ptr(), cache.data_ptr(), table.data_ptr(), lens.data_ptr(),
+                               pos.data_ptr(), wk.data_ptr(), wv.data_ptr(),
+                               None if indices is None else indices.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                               ws.numel(), B, T, H, Dn, Dc, Dr, Dv, cache.shape[1], table.shape[1], cache.shape[0],
+                               nk, int(causal), DTYPE[q.dtype], float(scale), splits, flags, _stream(q, stream))

@@ -133,3 +133,124 @@ def algorithmic_bytes(lengths, batch, q_heads, kv_heads, head_dim, block_size, e
 
 def algorithmic_flops(lengths, q_heads, head_dim) -> int:
     return 4 * q_heads * head_dim * sum(max(0, int(x)) for x in lengths)
+
+
+# ----------------------------------------------------------------------------
+# Paged MLA decode inputs
+# ----------------------------------------------------------------------------
+
+
+def make_mla_case(*, lengths, q_len=1, heads=16, nope_dim=128, latent_dim=512, rope_dim=64, value_dim=128,
+                  block_size=64, dtype=torch.bfloat16, device="cpu", seed=7, num_indices=None,
+                  device_gen=False):
+    """Seeded paged-MLA decode inputs, the recipe of the reference's MLA
+    benchmarks (``benchmarks/bench_attention_primitives.py:47-51``): fp32
+    ``randn`` q_nope, q_rope, latent and rope keys; ``w_uk`` scaled by
+    ``1/sqrt(Dn)`` and ``w_uv`` by ``1/sqrt(Dc)``; cast to dtype last.
+
+    The cache ``[N, P, Dc+Dr]`` holds exactly the needed pages in a random
+    physical order, table entries past each sequence's pages are -1, and
+    query t of sequence b sits at absolute position ``len - q_len + t``.
+    With ``num_indices`` an index list ``[B, T, K]`` of distinct visible
+    tokens per query (padded with -1) is returned as well.
+
+    Returns a dict with q_nope, q_rope, cache, table, lens, positions, w_uk,
+    w_uv, indices (or None).
+    """
+    bsz = len(lengths)
+    P = block_size
+    max_pages = max(1, math.ceil(max(lengths) / P))
+    used = [math.ceil(x / P) for x in lengths]
+    nblocks = max(1, sum(used))
+    W = latent_dim + rope_dim
+    gen_dev = device if device_gen else "cpu"
+    gen = torch.Generator(device=gen_dev).manual_seed(seed)
+    f32 = dict(generator=gen, dtype=torch.float32, device=gen_dev)
+    q_nope = torch.randn(bsz, q_len, heads, nope_dim, **f32)
+    q_rope = torch.randn(bsz, q_len, heads, rope_dim, **f32)
+    cache = _randn_cast((nblocks, P, W), gen, gen_dev, dtype, 1.0)
+    w_uk = torch.randn(heads, nope_dim, latent_dim, **f32) / math.sqrt(nope_dim)
+    w_uv = torch.randn(heads, value_dim, latent_dim, **f32) / math.sqrt(latent_dim)
+    cpu_gen = torch.Generator(device="cpu").manual_seed(seed + 1)
+    order = torch.randperm(nblocks, generator=cpu_gen, dtype=torch.int64)
+    table = torch.full((bsz, max_pages), -1, dtype=torch.int32)
+    offset = 0
+    for b, n in enumerate(used):
+        table[b, :n] = order[offset:offset + n].to(torch.int32)
+        offset += n
+    lens = torch.tensor(lengths, dtype=torch.int32)
+    positions = torch.tensor([[max(0, x - q_len + t) for t in range(q_len)] for x in lengths],
+                             dtype=torch.int32).view(bsz, q_len)
+    indices = None
+    if num_indices is not None:
+        indices = torch.full((bsz, q_len, num_indices), -1, dtype=torch.int32)
+        for b in range(bsz):
+            for t in range(q_len):
+                visible = min(lengths[b], int(positions[b, t]) + 1)
+                if visible > 0:
+                    pick = torch.randperm(visible, generator=cpu_gen)[:num_indices]
+                    indices[b, t, :pick.numel()] = pick.to(torch.int32)
+    out = dict(q_nope=q_nope, q_rope=q_rope, cache=cache, table=table, lens=lens, positions=positions,
+               w_uk=w_uk, w_uv=w_uv, indices=indices)
+    for key, val in out.items():
+        if val is None:
+            continue
+        if val.is_floating_point():
+            val = val.to(dtype)
+        out[key] = val.to(device).contiguous()
+    return out
+
+
+def mla_attend_bytes(lengths, q_len, heads, latent_dim, rope_dim, block_size, elem_bytes, num_indices=None) -> int:
+    """Algorithmic HBM bytes of one latent-attention call: every visible
+    cache row once per query row (or each listed row once), the absorbed
+    query and rope query, the output, lengths, positions and used table
+    entries.  Assumes queries at the last q_len positions (causal)."""
+    W = latent_dim + rope_dim
+    rows = 0
+    for x in lengths:
+        for t in range(q_len):
+            vis = max(0, x - q_len + t + 1) if x >= q_len else x
+            rows += min(vis, num_indices) if num_indices is not None else vis
+    bsz = len(lengths)
+    per_row_q = heads * (latent_dim + rope_dim + latent_dim) * elem_bytes
+    table = sum(math.ceil(x / block_size) for x in lengths) * 4
+    idx = bsz * q_len * num_indices * 4 if num_indices is not None else 0
+    return rows * W * elem_bytes + bsz * q_len * per_row_q + 4 * bsz + 4 * bsz * q_len + table + idx
+
+
+@dataclass(frozen=True)
+class MlaConfig:
+    """A paged-MLA decode workload (DeepSeek-V3 attention shapes: 128 heads,
+    Dn 128, Dc 512, Dr 64, Dv 128)."""
+    name: str
+    description: str
+    batch: int
+    heads: int
+    len_range: tuple
+    seed: int
+    block_size: int = 64
+    nope_dim: int = 128
+    latent_dim: int = 512
+    rope_dim: int = 64
+    value_dim: int = 128
+    dtype: torch.dtype = torch.bfloat16
+
+    def lengths(self):
+        gen = torch.Generator().manual_seed(20_000 + self.seed)
+        lo, hi = self.len_range
+        return torch.randint(lo, hi + 1, (self.batch,), generator=gen).tolist()
+
+    def make(self, device="cpu", device_gen=False):
+        return make_mla_case(lengths=self.lengths(), q_len=1, heads=self.heads, nope_dim=self.nope_dim,
+                             latent_dim=self.latent_dim, rope_dim=self.rope_dim, value_dim=self.value_dim,
+                             block_size=self.block_size, dtype=self.dtype, device=device, seed=self.seed,
+                             device_gen=device_gen)
+
+
+MLA_CONFIGS = {
+    "mla-h128": MlaConfig("mla-h128", "DeepSeek-V3 MLA decode, all 128 heads on one GPU, B32, len U[1024,4096], P64",
+                          batch=32, heads=128, len_range=(1024, 4096), seed=11),
+    "mla-h16": MlaConfig("mla-h16", "DeepSeek-V3 MLA decode, 16-head share (TP8), B128, len U[1024,4096], P64",
+                         batch=128, heads=16, len_range=(1024, 4096), seed=12),
+}

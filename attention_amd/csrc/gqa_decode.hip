@@ -52,47 +52,9 @@
 #include <string>
 
 #include "qd_attention.h"
+#include "qd_device.h"
 
 namespace {
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-
-// ----------------------------------------------------------------------------
-// Element types
-// ----------------------------------------------------------------------------
-
-template <int DT>
-struct Elem;
-template <>
-struct Elem<QD_DTYPE_F32> {
-  using S = float;
-  __device__ static float to_f(S x) { return x; }
-  __device__ static S from_f(float x) { return x; }
-};
-template <>
-struct Elem<QD_DTYPE_F16> {
-  using S = _Float16;
-  __device__ static float to_f(S x) { return static_cast<float>(x); }
-  __device__ static S from_f(float x) { return static_cast<_Float16>(x); }  // RNE
-};
-template <>
-struct Elem<QD_DTYPE_BF16> {
-  using S = __bf16;
-  __device__ static float to_f(S x) { return static_cast<float>(x); }
-  __device__ static S from_f(float x) { return static_cast<__bf16>(x); }  // RNE
-};
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 struct DecodeParams {
   const void* q;
@@ -112,8 +74,6 @@ struct DecodeParams {
   int* meta;      // stream-K path: per sequence {first workgroup, workgroups}
   int wg_waves;   // stream-K path: waves per workgroup
 };
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Valid tokens of a sequence: lengths are clamped to the table capacity
 // max_pages*block_size so that a length beyond the table never reads past
@@ -153,30 +113,6 @@ __device__ __forceinline__ int clamp_page(int32_t phys, int64_t num_blocks) {
   if (phys < 0) return 0;
   if (phys >= num_blocks) return static_cast<int>(num_blocks - 1);
   return phys;
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over each row of 16 lanes; every lane of the row gets the same bits.
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp_f<0xB1>(x);   // quad_perm [1,0,3,2]
-  x += dpp_f<0x4E>(x);   // quad_perm [2,3,0,1]
-  x += dpp_f<0x141>(x);  // row_half_mirror
-  x += dpp_f<0x140>(x);  // row_mirror
-  return x;
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-  return x;
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-  return x;
 }
 
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
@@ -372,41 +308,6 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
 // MFMA pipeline
 // ----------------------------------------------------------------------------
 
-template <int DT>
-struct MfmaOps;
-
-template <>
-struct MfmaOps<QD_DTYPE_BF16> {
-  __device__ static f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  __device__ static f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
-                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
-  }
-  __device__ static uint32_t pack2(float x, float y) {
-    const f32x2 v = {x, y};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-  }
-};
-
-template <>
-struct MfmaOps<QD_DTYPE_F16> {
-  __device__ static f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  __device__ static f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
-                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
-  }
-  __device__ static uint32_t pack2(float x, float y) {
-    const f32x2 v = {x, y};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
-  }
-};
-
 // V bytes one lane loads from one cache row: head_dim/16 elements.
 template <int D>
 struct VRow {
@@ -415,16 +316,6 @@ struct VRow {
   uint32_t w[kWords];
 };
 
-// K/V are streamed once per call: nontemporal loads (the NT cache policy)
-// keep them from displacing reusable lines and measure ~15% more read
-// bandwidth than plain loads on MI355X.
-__device__ __forceinline__ u32x4 stream_load16(const char* ptr) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
-}
-
-__device__ __forceinline__ u32x2 stream_load8(const char* ptr) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(ptr));
-}
 
 template <int D>
 __device__ __forceinline__ VRow<D> load_vrow(const char* ptr) {

@@ -1,0 +1,1261 @@
+// Paged MLA (multi-head latent attention) decode for MI355X (gfx950).
+// C ABI in include/qd_attention.h.
+//
+// Reference operators replaced (paths relative to the reference tree):
+//   latent_kv_write   csrc/cuda/mla/mla.cu:28-32 (write_cache), :151-160
+//   mla_project       csrc/cuda/mla/mla.cu:16-27 (projection), :138-150
+//   mla_attend        csrc/cuda/mla/mla.cu:34-82 (attend, attend_split,
+//                     attend_merge), :161-181
+//   mla_decode_fused  csrc/cuda/mla/mla.cu:86-134 (fused_decode, fused_split,
+//                     fused_split_merge), :184-198
+//
+// Layouts: cache [N, P, W] with W = Dc + Dr (latent | rope), q / out
+// [B, T, H, Dc], q_rope [B, T, H, Dr], table [B, maxP], lengths [B],
+// positions [B, T], indices [B, T, K] (logical token ids, -1 = none).
+//
+// Design.  All H heads of a query row read the same latent row, so the
+// attention is one shared K/V stream per row: a workgroup stages 32-token
+// tiles of whole cache rows in LDS (each row read from HBM once per
+// workgroup) and each of its waves runs 16 heads on the matrix cores:
+//   S^T[32 tok x 16 heads] = C[32 x W] . [q | q_rope]^T   v_mfma 16x16x32
+//   O^T[Dc x 16 heads]    += C[:, :Dc]^T . P^T            v_mfma 16x16x32
+// with the fp32 online softmax per lane (one head per lane column).  A
+// context can be split over workgroups; partials {m, l, acc[Dc]} are merged
+// with the reference's log-sum-exp rule.  The query absorption and value
+// projection are per-head GEMMs over all rows of the batch, so the weights
+// are read once per call rather than once per row as in the reference's
+// fused kernels; the rounding points (absorbed query, latent output, final
+// output, each rounded to the input dtype) are the reference's.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cmath>
+#include <mutex>
+#include <string>
+
+#include "qd_attention.h"
+#include "qd_device.h"
+
+// Records the calling thread's last failure for qd_error_string (defined
+// with the decode entry points).
+void qd_set_last_error(int status, const std::string& msg);
+
+namespace {
+
+constexpr int kTileTokens = 32;
+constexpr int kAttendThreads = 256;  // 4 waves: up to 64 heads, all load
+constexpr int kMaxSplits = 64;
+
+// ----------------------------------------------------------------------------
+// latent_kv_write
+// ----------------------------------------------------------------------------
+
+struct LatentWriteParams {
+  const char* latent;
+  const char* rope;
+  char* cache;
+  const int64_t* slots;
+  int64_t lat_bytes, rope_bytes, row_bytes;
+  int64_t rows;  // Nblocks * P
+};
+
+// grid n, block 64: row t -> cache row slots[t] (skipped when out of range).
+__global__ __launch_bounds__(64) void latent_write_vec16_kernel(LatentWriteParams p) {
+  const int64_t t = blockIdx.x;
+  const int64_t s = p.slots[t];
+  if (s < 0 || s >= p.rows) return;
+  char* dst = p.cache + s * p.row_bytes;
+  const char* la = p.latent + t * p.lat_bytes;
+  const char* ro = p.rope + t * p.rope_bytes;
+  const int64_t nl = p.lat_bytes >> 4, nr = p.rope_bytes >> 4;
+  for (int64_t i = threadIdx.x; i < nl + nr; i += 64) {
+    const u32x4 v = i < nl ? *reinterpret_cast<const u32x4*>(la + 16 * i)
+                           : *reinterpret_cast<const u32x4*>(ro + 16 * (i - nl));
+    *reinterpret_cast<u32x4*>(dst + 16 * i) = v;
+  }
+}
+
+template <typename E>
+__global__ __launch_bounds__(64) void latent_write_elem_kernel(LatentWriteParams p) {
+  const int64_t t = blockIdx.x;
+  const int64_t s = p.slots[t];
+  if (s < 0 || s >= p.rows) return;
+  const int64_t nl = p.lat_bytes / static_cast<int64_t>(sizeof(E));
+  const int64_t nr = p.rope_bytes / static_cast<int64_t>(sizeof(E));
+  E* dst = reinterpret_cast<E*>(p.cache + s * p.row_bytes);
+  const E* la = reinterpret_cast<const E*>(p.latent + t * p.lat_bytes);
+  const E* ro = reinterpret_cast<const E*>(p.rope + t * p.rope_bytes);
+  for (int64_t i = threadIdx.x; i < nl + nr; i += 64) dst[i] = i < nl ? la[i] : ro[i - nl];
+}
+
+// ----------------------------------------------------------------------------
+// Per-head projection (query absorption / value up-projection)
+// ----------------------------------------------------------------------------
+//
+// out[r, h, o] = sum_k x[r, h, k] * W_h(k, o) over rows r = (b, t), with
+//   absorb: W_h(k, o) = w[h, k, o]   (w [H, Dn, Dc], k = Dn, o = Dc)
+//   value:  W_h(k, o) = w[h, o, k]   (w [H, Dv, Dc], k = Dc, o = Dv)
+// fp32 accumulation, one rounding to the dtype (mla.cu:21-26).
+
+struct ProjParams {
+  const void* x;
+  const void* w;
+  void* out;
+  int64_t rows;
+  int H, di, dout;
+};
+
+// grid (ceil(dout/128), H), block 256.  The workgroup owns 128 output
+// columns of one head for all rows; its 4 waves split the k range (k chunks
+// of 32, chunk c on wave c % 4) and their partial tiles are summed in LDS.
+// A wave covers 64 rows x 128 columns: 4 row tiles x 8 column tiles of
+// v_mfma_f32_16x16x32, column tile e holding columns base + 8*(l%16) + e,
+// so the absorb layout (columns contiguous in memory) is turned into the B
+// operand by an 8x8 in-register transpose and the value layout (k
+// contiguous) is loaded as is.  Row groups of 64 are processed in turn, so
+// a head's weights come from HBM once and from cache afterwards.
+template <int DT, bool ABSORB>
+__global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
+  using E = Elem<DT>;
+  using Ops = MfmaOps<DT>;
+  using S = typename E::S;
+  __shared__ f32x4 red[4][8][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int r16 = lane & 15, q4 = lane >> 4;
+  const int h = blockIdx.y;
+  const int cbase = 128 * blockIdx.x;
+  const int col = min(cbase + 8 * r16, p.dout - 8);  // clamped load column
+  const int nch = p.di / 32;
+  const char* xb = static_cast<const char*>(p.x);
+  const char* wb = static_cast<const char*>(p.w);
+  S* out = static_cast<S*>(p.out);
+  for (int64_t r0 = 0; r0 < p.rows; r0 += 64) {
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[rt][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = wv; c < nch; c += 4) {
+      const int k0 = 32 * c + 8 * q4;
+      u32x4 bop[8];
+      if constexpr (ABSORB) {
+        u32x4 raw[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          raw[t] = *reinterpret_cast<const u32x4*>(
+              wb + ((static_cast<int64_t>(h) * p.di + k0 + t) * p.dout + col) * 2);
+        transpose8x8_b16(raw, bop);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          bop[e] = *reinterpret_cast<const u32x4*>(
+              wb + ((static_cast<int64_t>(h) * p.dout + col + e) * p.di + k0) * 2);
+      }
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        int64_t row = r0 + 16 * rt + r16;
+        if (row >= p.rows) row = p.rows - 1;
+        const u32x4 a =
+            *reinterpret_cast<const u32x4*>(xb + ((row * p.H + h) * p.di + k0) * 2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[rt][e] = Ops::mma32(a, bop[e], acc[rt][e]);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wv][e][lane] = acc[rt][e];
+      __syncthreads();
+#pragma unroll
+      for (int ee = 0; ee < 2; ++ee) {
+        const int e = 2 * wv + ee;
+        const f32x4 s = red[0][e][lane] + red[1][e][lane] + red[2][e][lane] + red[3][e][lane];
+        const int ocol = cbase + 8 * r16 + e;
+        if (ocol < p.dout) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int64_t row = r0 + 16 * rt + 4 * q4 + i;
+            if (row < p.rows) out[(row * p.H + h) * p.dout + ocol] = E::from_f(s[i]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Any dtype/shape: one thread per output element, k summed in order (the
+// reference's loop, mla.cu:18-26).
+template <int DT, bool ABSORB>
+__global__ __launch_bounds__(256) void mla_project_generic_kernel(ProjParams p) {
+  using E = Elem<DT>;
+  using S = typename E::S;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= p.rows * p.H * p.dout) return;
+  const int o = static_cast<int>(i % p.dout);
+  const int h = static_cast<int>((i / p.dout) % p.H);
+  const int64_t r = i / (static_cast<int64_t>(p.H) * p.dout);
+  const S* x = static_cast<const S*>(p.x) + (r * p.H + h) * p.di;
+  const S* w = static_cast<const S*>(p.w);
+  float sum = 0.f;
+  for (int k = 0; k < p.di; ++k) {
+    const int64_t wi = ABSORB ? (static_cast<int64_t>(h) * p.di + k) * p.dout + o
+                              : (static_cast<int64_t>(h) * p.dout + o) * p.di + k;
+    sum = fmaf(E::to_f(x[k]), E::to_f(w[wi]), sum);
+  }
+  static_cast<S*>(p.out)[i] = E::from_f(sum);
+}
+
+// ----------------------------------------------------------------------------
+// Paged latent attention
+// ----------------------------------------------------------------------------
+
+struct MlaParams {
+  const void* q;    // [R, H, Dc]
+  const void* qr;   // [R, H, Dr]
+  const void* cache;
+  const int32_t* table;
+  const int32_t* lens;
+  const int32_t* pos;  // [R]
+  const int32_t* idx;  // [R, nk] when nk >= 0
+  void* out;           // [R, H, Dc] (splits == 1)
+  float* part;         // [R, H, splits, Dc + 2] (splits > 1)
+  int B, T, H, Dc, Dr, W, P, maxP;
+  int nk;  // indices per row, -1 = all tokens (dense)
+  int causal, splits;
+  int head_groups;  // MFMA kernel: workgroups per (row, split)
+  int kch;          // MFMA kernel: ceil(W / 32)
+  int nt;           // MFMA kernel: nontemporal cache loads
+  int64_t num_blocks;
+  int64_t units;    // rows * splits
+  float sl2;        // scale * log2(e)
+};
+
+// Visible prefix of query row r (mla.cu:37), clamped to the table capacity
+// so that a length beyond the table never reads past the table row.
+__device__ __forceinline__ int row_end(const MlaParams& p, int b, int64_t r) {
+  const int64_t cap = static_cast<int64_t>(p.maxP) * p.P;
+  int64_t end = p.lens[b];
+  if (p.causal) {
+    const int64_t lim = static_cast<int64_t>(p.pos[r]) + 1;
+    end = min(end, max(static_cast<int64_t>(0), lim));
+  }
+  end = min(end, cap);
+  return end > 0 ? static_cast<int>(end) : 0;
+}
+
+// Token list positions [i0, i1) of split s over `count` entries (mla.cu:60).
+__device__ __forceinline__ void split_range(int count, int s, int splits, int& i0, int& i1) {
+  i0 = static_cast<int>(static_cast<int64_t>(count) * s / splits);
+  i1 = static_cast<int>(static_cast<int64_t>(count) * (s + 1) / splits);
+}
+
+// Element offset of logical token `tok` of sequence b (mla.cu:45-46);
+// out-of-range page ids are clamped so every access stays in the cache.
+__device__ __forceinline__ int64_t token_offset(const MlaParams& p, int b, int tok) {
+  int32_t phys = p.table[static_cast<int64_t>(b) * p.maxP + tok / p.P];
+  if (phys < 0) phys = 0;
+  if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
+  return (static_cast<int64_t>(phys) * p.P + tok % p.P) * p.W;
+}
+
+// Stores a row's result: the normalized output (splits == 1) or the
+// partial {m (natural-log units), l, acc[Dc]} (mla.cu:71-73).
+__device__ __forceinline__ float* partial_row(const MlaParams& p, int64_t r, int h, int s) {
+  return p.part + ((r * p.H + h) * p.splits + s) * static_cast<int64_t>(p.Dc + 2);
+}
+
+// Max over the 4 lanes l % 16 == const (lanes l, l^16, l^32, l^48) with
+// gfx950's v_permlane32_swap / v_permlane16_swap: swapping a register with
+// itself leaves the lane's value and its partner's (l^32, resp. l^16) in the
+// returned pair.  No LDS round trip, unlike ds_bpermute.
+__device__ __forceinline__ float max_over_lane_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// LDS-only workgroup barrier for the DMA pipeline: waits for this wave's LDS
+// operations and for all but `kVm` of its vector-memory loads (LDS DMA
+// included), then s_barrier.  __syncthreads() would wait for every
+// outstanding load (vmcnt(0)) and drain the DMA ring at each tile.  The
+// empty asm statements keep the compiler from moving memory accesses across.
+template <int kVm>
+__device__ __forceinline__ void dma_barrier() {
+  static_assert(kVm >= 0 && kVm < 64, "vmcnt is 6 bits");
+  constexpr int imm = (kVm & 0xF) | ((kVm >> 4) << 14) | (0x7 << 4) | (0x0 << 8);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(imm);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Tile ring depth for CPT DMA instructions per thread per tile (CPT * 4 KB
+// per tile buffer), within 160 KB of LDS.
+constexpr int ring_depth(int cpt) { return cpt <= 9 ? 4 : 3; }
+constexpr int kOffSlotsDma = 6;  // ring depth + 2
+constexpr int kWinPages = 256;    // page-table window (dense rows)
+
+__host__ __device__ constexpr size_t mla_mfma_lds_bytes(int cpt) {
+  return static_cast<size_t>(ring_depth(cpt)) * cpt * 4096 + kOffSlotsDma * kTileTokens * 8 + kOffSlotsDma * 4 +
+         kWinPages * 4 + 1024;
+}
+
+// MFMA kernel.  grid = ceil(units/8)*8*head_groups workgroups of 256
+// threads; workgroup L serves unit ((L/8)/hg)*8 + L%8 and head group
+// (L/8)%hg, so the head groups of one (row, split) - which read the same
+// cache rows - run on the same XCD and share its L2.
+//
+// Waves: wave w of head group g owns heads 16*(4g+w) .. +15; waves without
+// heads only help load.  Per 32-token tile:
+//   load     direct global->LDS DMA (global_load_lds_dwordx4, 1 KB per wave
+//            instruction, CPT per thread) into a ring of ring_depth(CPT)
+//            tile buffers, ring_depth - 1 tiles ahead; no registers hold the
+//            stream.  Rows are unpadded (2W bytes); when W/8 is a multiple
+//            of 8, 16-byte column c of row r is stored at c ^ (r & 7) so the
+//            MFMA operand reads spread over the banks.  Row offsets come
+//            from wave 0, ring_depth tiles ahead, through a page-table
+//            window in LDS (dense rows) or the index list (sparse rows).
+//            A token that is not visible is loaded as a duplicate of a
+//            visible row of its tile (finite data) and gets probability 0.
+//   QK       lane (r16, q4): A = row r16 (+16), 16-byte column 4c + q4 of
+//            the tile, B = [q | q_rope | 0] of head r16, elements
+//            32c + 8 q4 .. +7 -> S0/S1 lane values: tokens 4 q4 + i and
+//            16 + 4 q4 + i.
+//   softmax  per lane (one head per lane column), reduced over the 4 lane
+//            groups; per-lane partial sums l.
+//   PV       k index 8 q4 + e <-> token 4 q4 + e (e < 4) / 16 + 4 q4 + e - 4,
+//            so B = P^T is the lane's own 8 probabilities; A = C^T for
+//            latent columns 128 blk + 8 r16 + e of those 8 tokens (8 LDS
+//            reads + 8x8 transpose); C tile (blk, e) row r <-> column
+//            128 blk + 8 r + e, i.e. lane rows 4 q4 + i hold columns
+//            128 blk + 32 q4 + 8 i + e: 32 contiguous columns per lane.
+template <int DT, int NBLK, int CPT>
+__global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaParams p) {
+  using E = Elem<DT>;
+  using Ops = MfmaOps<DT>;
+  using S = typename E::S;
+  constexpr int KMAX = 2 * CPT;  // W <= 64 CPT  ->  ceil(W/32) <= 2 CPT
+  constexpr int kRing = ring_depth(CPT);
+  constexpr int kTileBytes = CPT * 4096;
+  extern __shared__ __align__(16) char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int r16 = lane & 15, q4 = lane >> 4;
+
+  const int64_t L = blockIdx.x;
+  const int64_t slot = L >> 3;
+  const int64_t unit = (slot / p.head_groups) * 8 + (L & 7);
+  const int hg = static_cast<int>(slot % p.head_groups);
+  if (unit >= p.units) return;  // whole workgroup: uniform
+  const int64_t r = unit / p.splits;
+  const int s = static_cast<int>(unit % p.splits);
+  const int b = static_cast<int>(r / p.T);
+
+  const int end = row_end(p, b, r);
+  const bool sparse = p.nk >= 0;
+  const int count = sparse ? p.nk : end;
+  int i0, i1;
+  split_range(count, s, p.splits, i0, i1);
+  const int ntiles = (i1 - i0 + kTileTokens - 1) / kTileTokens;
+
+  char* ring = smem;
+  int64_t* offs = reinterpret_cast<int64_t*>(smem + kRing * kTileBytes);  // [kOffSlotsDma][32]
+  uint32_t* masks = reinterpret_cast<uint32_t*>(offs + kOffSlotsDma * kTileTokens);
+  int32_t* win = reinterpret_cast<int32_t*>(masks + kOffSlotsDma);          // [kWinPages]
+
+  const int h0 = 16 * (4 * hg + wv);
+  const bool active = h0 < p.H;
+  const int h = h0 + r16;
+  const bool head_ok = h < p.H;
+  const int kch = p.kch;
+  const int w8 = p.W / 8;
+  const int swz = (w8 & 7) == 0 ? 7 : 0;
+
+  // Query operand [q | q_rope | 0] of head h, chunks of 32 elements.
+  u32x4 qv[KMAX];
+  {
+    const S* qrow = static_cast<const S*>(p.q) + (r * p.H + (head_ok ? h : 0)) * p.Dc;
+    const S* rrow = static_cast<const S*>(p.qr) + (r * p.H + (head_ok ? h : 0)) * p.Dr;
+#pragma unroll
+    for (int c = 0; c < KMAX; ++c) {
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      if (c < kch && head_ok && active) {
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const int k = 32 * c + 8 * q4 + e;
+          float x0 = 0.f, x1 = 0.f;
+          if (k < p.Dc) x0 = E::to_f(qrow[k]);
+          else if (k < p.W) x0 = E::to_f(rrow[k - p.Dc]);
+          if (k + 1 < p.Dc) x1 = E::to_f(qrow[k + 1]);
+          else if (k + 1 < p.W) x1 = E::to_f(rrow[k + 1 - p.Dc]);
+          w[e / 2] = Ops::pack2(x0, x1);
+        }
+      }
+      qv[c] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+  }
+
+  // This thread's DMA work: LDS chunk k*256 + tid of a tile is row-major
+  // (row, c) = divmod(., W/8) and holds global column c ^ (row & swz);
+  // chunks past the 32 rows are fillers that reread a chunk of row 0.
+  const int total_chunks = kTileTokens * w8;
+  const int row0 = static_cast<int>(threadIdx.x) / w8, col0 = static_cast<int>(threadIdx.x) % w8;
+  const int step_rows = kAttendThreads / w8, step_cols = kAttendThreads % w8;
+  const char* cache = static_cast<const char*>(p.cache);
+
+  int win_base = -kWinPages;  // wave 0 only: first page held in `win`
+  auto load_window = [&](int first) {
+    for (int i = lane; i < kWinPages; i += 64) {
+      const int pg = first + i;
+      win[i] = pg < p.maxP ? p.table[static_cast<int64_t>(b) * p.maxP + pg] : 0;
+    }
+    win_base = first;
+  };
+  // wave 0: offsets (elements) and visibility of tile t into slot t % kOffSlotsDma.
+  auto compute_offsets = [&](int t) {
+    const int i = i0 + kTileTokens * t + lane;
+    bool valid = lane < kTileTokens && i < i1;
+    int tok = i;
+    if (sparse) {
+      tok = valid ? p.idx[r * p.nk + i] : -1;
+      valid = valid && tok >= 0 && tok < end;
+    }
+    int32_t phys = 0;
+    if (sparse) {
+      if (valid) phys = p.table[static_cast<int64_t>(b) * p.maxP + tok / p.P];
+    } else {
+      const int first = (i0 + kTileTokens * t) / p.P;
+      const int last = (min(i0 + kTileTokens * t + kTileTokens, i1) - 1) / p.P;
+      if (last >= win_base + kWinPages) load_window(first);
+      if (valid) phys = win[tok / p.P - win_base];
+    }
+    if (phys < 0) phys = 0;
+    if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
+    const int64_t off = valid ? (static_cast<int64_t>(phys) * p.P + tok % p.P) * p.W : 0;
+    const uint32_t mask = static_cast<uint32_t>(__ballot(valid));
+    const int fv = mask ? __builtin_ctz(mask) : 0;
+    const int64_t dummy = __shfl(off, fv);
+    const int sl = t % kOffSlotsDma;
+    if (lane < kTileTokens) offs[sl * kTileTokens + lane] = valid ? off : dummy;
+    if (lane == 0) masks[sl] = mask;
+  };
+  auto issue_dma = [&](int t) {
+    char* buf = ring + (t % kRing) * kTileBytes;
+    const int64_t* o = offs + (t % kOffSlotsDma) * kTileTokens;
+    // All sources first (one LDS round trip), then the DMA instructions.
+    const char* src[CPT];
+    int row = row0, col = col0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const bool real = static_cast<int>(threadIdx.x) + k * kAttendThreads < total_chunks;
+      src[k] = cache + 2 * o[real ? row : 0] + (real ? 16 * (col ^ (row & swz)) : 0);
+      row += step_rows;
+      col += step_cols;
+      if (col >= w8) {
+        col -= w8;
+        ++row;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src[k]),
+                                       (__attribute__((address_space(3))) void*)(buf + (4 * k + wv) * 1024), 16,
+                                       0, 0);
+  };
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 acc[NBLK][8];
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[blk][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (ntiles > 0) {
+    if (wv == 0) {
+      if (!sparse) load_window(i0 / p.P);
+      for (int t = 0; t < kRing && t < ntiles; ++t) compute_offsets(t);
+    }
+    __syncthreads();
+    for (int t = 0; t < kRing - 1 && t < ntiles; ++t) issue_dma(t);
+  }
+  for (int j = 0; j < ntiles; ++j) {
+    // Tile j's DMA done in every wave (tiles j+1 .. j+kRing-2 may fly on),
+    // and every wave is past tile j-1's compute.
+    if (ntiles - 1 - j >= kRing - 2)
+      dma_barrier<(kRing - 2) * CPT>();
+    else
+      dma_barrier<0>();
+    if (j + kRing - 1 < ntiles) issue_dma(j + kRing - 1);  // into tile j-1's buffer
+    if (active) {
+      const char* buf = ring + (j % kRing) * kTileBytes;
+      const uint32_t mask = masks[j % kOffSlotsDma];
+      if (mask != 0u) {
+        // S^T = C . Qcat^T for tokens 0-15 (s0) and 16-31 (s1), over all
+        // 2*CPT chunks: the query is zero past W, and a chunk past W reads
+        // the next row or the tile's filler chunks (finite cache data,
+        // inside the tile buffer since W/8 <= 8*CPT).  A fixed chunk count
+        // lets the LDS reads run ahead of the MFMAs.
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        const int ra = r16, rb = 16 + r16;
+#pragma unroll
+        for (int c = 0; c < KMAX; ++c) {
+          const int c4 = 4 * c + q4;
+          const u32x4 a0 = *reinterpret_cast<const u32x4*>(buf + 16 * (ra * w8 + (c4 ^ (ra & swz))));
+          const u32x4 a1 = *reinterpret_cast<const u32x4*>(buf + 16 * (rb * w8 + (c4 ^ (rb & swz))));
+          s0 = Ops::mma32(a0, qv[c], s0);
+          s1 = Ops::mma32(a1, qv[c], s1);
+        }
+
+        // Online softmax in log2 units.  The accumulator is rescaled only on
+        // tiles that raise some head's running max (a wave-uniform branch;
+        // rare once the max has been seen), so every probability is <= 1 and
+        // the largest score's is exactly 1 in the 16-bit PV operand.
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[i] = (mask >> (4 * q4 + i)) & 1u ? s0[i] * p.sl2 : -INFINITY;
+          x[4 + i] = (mask >> (16 + 4 * q4 + i)) & 1u ? s1[i] * p.sl2 : -INFINITY;
+        }
+        float mx = x[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
+        mx = max_over_lane_groups(mx);
+        const bool move = mx > m_run;
+        if (__ballot(move)) {
+          const float alpha = move ? fast_exp2(m_run - mx) : 1.f;
+          m_run = move ? mx : m_run;
+          l_run *= alpha;
+#pragma unroll
+          for (int blk = 0; blk < NBLK; ++blk)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[blk][e] *= alpha;
+        }
+        // The denominator sums the same 16-bit probabilities the PV product
+        // uses, so the output is an exactly normalized average of values.
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float pr[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pr[e] = fast_exp2(x[e] - m_use);
+        const u32x4 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3]), Ops::pack2(pr[4], pr[5]),
+                          Ops::pack2(pr[6], pr[7])};
+        l_run += (Ops::sum2(pb[0]) + Ops::sum2(pb[1])) + (Ops::sum2(pb[2]) + Ops::sum2(pb[3]));
+
+        // O^T += C[:, :Dc]^T . P^T
+#pragma unroll
+        for (int blk = 0; blk < NBLK; ++blk) {
+          const int cc = min(16 * blk + r16, p.Dc / 8 - 1);
+          u32x4 raw[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int tok = t < 4 ? 4 * q4 + t : 16 + 4 * q4 + (t - 4);
+            raw[t] = *reinterpret_cast<const u32x4*>(buf + 16 * (tok * w8 + (cc ^ (tok & swz))));
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            acc[blk][e] = Ops::mma32(transpose8x8_col_b16(raw, e), pb, acc[blk][e]);
+        }
+      }
+    }
+    if (wv == 0 && j + kRing < ntiles) compute_offsets(j + kRing);
+  }
+  if (!active || !head_ok) return;
+
+  float l = l_run + __shfl_xor(l_run, 16);
+  l += __shfl_xor(l, 32);
+  if (p.splits == 1) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    S* orow = static_cast<S*>(p.out) + (r * p.H + h) * p.Dc;
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int dc0 = 128 * blk + 32 * q4 + 8 * i;
+        if (dc0 < p.Dc) {
+          uint32_t w[4];
+#pragma unroll
+          for (int e = 0; e < 8; e += 2)
+            w[e / 2] = Ops::pack2(acc[blk][e][i] * inv, acc[blk][e + 1][i] * inv);
+          *reinterpret_cast<u32x4*>(orow + dc0) = u32x4{w[0], w[1], w[2], w[3]};
+        }
+      }
+  } else {
+    float* pr = partial_row(p, r, h, s);
+    if (q4 == 0) {
+      pr[0] = m_run == -INFINITY ? -INFINITY : m_run * kLn2;
+      pr[1] = l;
+    }
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int dc0 = 128 * blk + 32 * q4 + 8 * i;
+        if (dc0 < p.Dc) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pr[2 + dc0 + e] = acc[blk][e][i];
+        }
+      }
+  }
+}
+
+// Any dtype/shape (mla.cu:34-82 on the VALU): one wave per (row, head,
+// split), one token per step, lanes over the W columns of the cache row.
+template <int DT>
+__global__ __launch_bounds__(256) void mla_attend_generic_kernel(MlaParams p) {
+  using E = Elem<DT>;
+  using S = typename E::S;
+  constexpr int kAcc = 8;  // Dc <= 512 = 8 * 64
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t per_row = static_cast<int64_t>(p.H) * p.splits;
+  if (wid >= static_cast<int64_t>(p.B) * p.T * per_row) return;
+  const int64_t r = wid / per_row;
+  const int h = static_cast<int>((wid / p.splits) % p.H);
+  const int s = static_cast<int>(wid % p.splits);
+  const int b = static_cast<int>(r / p.T);
+  const int end = row_end(p, b, r);
+  const int count = p.nk >= 0 ? p.nk : end;
+  int i0, i1;
+  split_range(count, s, p.splits, i0, i1);
+
+  const S* qrow = static_cast<const S*>(p.q) + (r * p.H + h) * p.Dc;
+  const S* rrow = static_cast<const S*>(p.qr) + (r * p.H + h) * p.Dr;
+  const S* cache = static_cast<const S*>(p.cache);
+  float m_run = -INFINITY, l_run = 0.f;
+  float acc[kAcc];
+#pragma unroll
+  for (int j = 0; j < kAcc; ++j) acc[j] = 0.f;
+  for (int i = i0; i < i1; ++i) {
+    const int tok = p.nk >= 0 ? p.idx[r * p.nk + i] : i;
+    if (tok < 0 || tok >= end) continue;
+    const S* row = cache + token_offset(p, b, tok);
+    float cv[kAcc];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < kAcc; ++j) {
+      const int d = lane + 64 * j;
+      cv[j] = d < p.Dc ? E::to_f(row[d]) : 0.f;
+      if (d < p.Dc) dot = fmaf(E::to_f(qrow[d]), cv[j], dot);
+    }
+    for (int d = lane; d < p.Dr; d += 64) dot = fmaf(E::to_f(rrow[d]), E::to_f(row[p.Dc + d]), dot);
+    const float x = wave_sum(dot) * p.sl2;
+    const float m_new = fmaxf(m_run, x);
+    const float alpha = l_run == 0.f ? 0.f : fast_exp2(m_run - m_new);
+    const float pw = fast_exp2(x - m_new);
+    l_run = alpha * l_run + pw;
+    m_run = m_new;
+#pragma unroll
+    for (int j = 0; j < kAcc; ++j) acc[j] = alpha * acc[j] + pw * cv[j];
+  }
+  if (p.splits == 1) {
+    S* orow = static_cast<S*>(p.out) + (r * p.H + h) * p.Dc;
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+    for (int j = 0; j < kAcc; ++j) {
+      const int d = lane + 64 * j;
+      if (d < p.Dc) orow[d] = E::from_f(acc[j] * inv);
+    }
+  } else {
+    float* pr = partial_row(p, r, h, s);
+    if (lane == 0) {
+      pr[0] = m_run == -INFINITY ? -INFINITY : m_run * kLn2;
+      pr[1] = l_run;
+    }
+#pragma unroll
+    for (int j = 0; j < kAcc; ++j) {
+      const int d = lane + 64 * j;
+      if (d < p.Dc) pr[2 + d] = acc[j];
+    }
+  }
+}
+
+// Log-sum-exp merge of [R, H, splits, Dc+2] partials (mla.cu:75-82, rule
+// of online_softmax.cuh:17-24): one wave per (row, head), splits folded in
+// order, empty partials skipped, an all-empty row gives zeros.
+template <int DT>
+__global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
+  using E = Elem<DT>;
+  using S = typename E::S;
+  constexpr int kAcc = 8;
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t nrows = static_cast<int64_t>(p.B) * p.T * p.H;
+  if (wid >= nrows) return;
+  const float* base = p.part + wid * p.splits * static_cast<int64_t>(p.Dc + 2);
+  float M = -INFINITY, Lsum = 0.f;
+  float acc[kAcc];
+#pragma unroll
+  for (int j = 0; j < kAcc; ++j) acc[j] = 0.f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float* pr = base + s * static_cast<int64_t>(p.Dc + 2);
+    const float ms = pr[0], ls = pr[1];
+    if (ls == 0.f) continue;
+    const float mn = fmaxf(M, ms);
+    const float a = Lsum == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
+    const float bb = fast_exp2((ms - mn) * kLog2e);
+    Lsum = a * Lsum + bb * ls;
+    M = mn;
+#pragma unroll
+    for (int j = 0; j < kAcc; ++j) {
+      const int d = lane + 64 * j;
+      if (d < p.Dc) acc[j] = a * acc[j] + bb * pr[2 + d];
+    }
+  }
+  S* orow = static_cast<S*>(p.out) + wid * p.Dc;
+  const float inv = Lsum > 0.f ? 1.f / Lsum : 0.f;
+#pragma unroll
+  for (int j = 0; j < kAcc; ++j) {
+    const int d = lane + 64 * j;
+    if (d < p.Dc) orow[d] = E::from_f(acc[j] * inv);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Host side
+// ----------------------------------------------------------------------------
+
+int mla_fail(char* msg, size_t cap, const char* text) {
+  qd_set_last_error(QD_ERR_INVALID_VALUE, text);
+  if (msg && cap) {
+    size_t n = strlen(text);
+    if (n >= cap) n = cap - 1;
+    memcpy(msg, text, n);
+    msg[n] = '\0';
+  }
+  return QD_ERR_INVALID_VALUE;
+}
+
+int mla_ok(char* msg, size_t cap) {
+  if (msg && cap) msg[0] = '\0';
+  return QD_OK;
+}
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    qd_set_last_error(static_cast<int>(e), std::string(what) + " kernel launch failed: " + hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  return QD_OK;
+}
+
+// The reference's check(): contiguous CUDA tensor on `base`'s device.
+bool placed(const qd_tensor_desc* x, const qd_tensor_desc* base) {
+  return x->defined && x->is_device && x->contiguous && x->device_index == base->device_index;
+}
+
+bool float_dtype(int dt) { return dt == QD_DTYPE_F32 || dt == QD_DTYPE_F16 || dt == QD_DTYPE_BF16; }
+
+int elem_size(int dt) {
+  switch (dt) {
+    case QD_DTYPE_F32: return 4;
+    case QD_DTYPE_F16:
+    case QD_DTYPE_BF16: return 2;
+    default: return 0;
+  }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+int device_max_lds() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+  if (cached[dev] == 0) {
+    int bytes = 0;
+    if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        bytes <= 0)
+      bytes = 65536;
+    cached[dev] = bytes;
+  }
+  return cached[dev];
+}
+
+// Shape of one attention call.
+struct AttendShape {
+  int B, T, H, Dc, Dr, P, maxP, nk, dtype;
+};
+
+// Launch plan of the attention: kernel, splits, and the MFMA kernel's
+// instance (latent blocks of 128 columns, DMA chunks per thread per tile).
+// Depends on static shapes and the device only.
+struct AttendPlan {
+  bool mfma;
+  int nblk, cpt, kch, head_groups;
+  size_t lds;
+  int splits;
+};
+
+// Smallest instantiated DMA-chunk count covering ceil(W/64), 0 if none.
+int cpt_for(int W) {
+  const int need = (W + 63) / 64;
+  for (int c : {2, 5, 9, 10})
+    if (need <= c) return c;
+  return 0;
+}
+
+AttendPlan plan_attend(const AttendShape& a, int forced_splits, int flags) {
+  AttendPlan pl{};
+  const int W = a.Dc + a.Dr;
+  pl.nblk = (a.Dc + 127) / 128;
+  pl.kch = (W + 31) / 32;
+  pl.cpt = cpt_for(W);
+  if (pl.cpt == 5 && pl.nblk > 3) pl.cpt = 9;  // (4, 5) is not instantiated
+  if (pl.cpt == 2 && pl.nblk > 1) pl.cpt = 5;
+  pl.lds = pl.cpt ? mla_mfma_lds_bytes(pl.cpt) : 0;
+  const int ht = (a.H + 15) / 16;
+  pl.head_groups = (ht + 3) / 4;
+  pl.mfma = (flags & QD_FLAG_FORCE_GENERIC) == 0 && (a.dtype == QD_DTYPE_F16 || a.dtype == QD_DTYPE_BF16) &&
+            a.Dc % 8 == 0 && a.Dr % 8 == 0 && a.Dc <= 512 && pl.nblk >= 1 && pl.nblk <= 4 && pl.cpt > 0 &&
+            pl.lds <= static_cast<size_t>(device_max_lds());
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T;
+  if (forced_splits > 0) {
+    pl.splits = forced_splits;
+  } else {
+    // One resident workgroup per CU (the MFMA kernel's LDS ring) or two
+    // (VALU kernel), at least 256 listed tokens per split, at most
+    // kMaxSplits.
+    const int64_t cap = a.nk >= 0 ? a.nk : static_cast<int64_t>(a.maxP) * a.P;
+    const int64_t per_row = pl.mfma ? pl.head_groups : (static_cast<int64_t>(a.H) + 3) / 4;
+    const int64_t target = (pl.mfma ? 1 : 2) * static_cast<int64_t>(device_cus());
+    const int64_t want = (target + rows * per_row - 1) / (rows * per_row);
+    int64_t sp = std::min<int64_t>(want, std::max<int64_t>(1, cap / 256));
+    pl.splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(sp, kMaxSplits)));
+  }
+  return pl;
+}
+
+size_t attend_partial_bytes(const AttendShape& a, int splits) {
+  if (splits <= 1) return 0;
+  return static_cast<size_t>(a.B) * a.T * a.H * splits * (a.Dc + 2) * sizeof(float);
+}
+
+template <int DT, int NBLK, int CPT>
+hipError_t launch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
+  auto fn = mla_attend_mfma_kernel<DT, NBLK, CPT>;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [&] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(mla_mfma_lds_bytes(CPT)));
+  });
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kAttendThreads), pl.lds, st, prm);
+  return hipSuccess;
+}
+
+template <int DT>
+hipError_t dispatch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
+  switch (pl.cpt * 8 + pl.nblk) {
+    case 2 * 8 + 1: return launch_attend_mfma<DT, 1, 2>(prm, pl, grid, st);
+    case 5 * 8 + 1: return launch_attend_mfma<DT, 1, 5>(prm, pl, grid, st);
+    case 5 * 8 + 2: return launch_attend_mfma<DT, 2, 5>(prm, pl, grid, st);
+    case 5 * 8 + 3: return launch_attend_mfma<DT, 3, 5>(prm, pl, grid, st);
+    case 9 * 8 + 1: return launch_attend_mfma<DT, 1, 9>(prm, pl, grid, st);
+    case 9 * 8 + 2: return launch_attend_mfma<DT, 2, 9>(prm, pl, grid, st);
+    case 9 * 8 + 3: return launch_attend_mfma<DT, 3, 9>(prm, pl, grid, st);
+    case 9 * 8 + 4: return launch_attend_mfma<DT, 4, 9>(prm, pl, grid, st);
+    case 10 * 8 + 1: return launch_attend_mfma<DT, 1, 10>(prm, pl, grid, st);
+    case 10 * 8 + 2: return launch_attend_mfma<DT, 2, 10>(prm, pl, grid, st);
+    case 10 * 8 + 3: return launch_attend_mfma<DT, 3, 10>(prm, pl, grid, st);
+    case 10 * 8 + 4: return launch_attend_mfma<DT, 4, 10>(prm, pl, grid, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Enqueues attention (+ merge) writing [R, H, Dc] of the dtype to `out`.
+int run_attend(const AttendShape& a, const void* q, const void* qr, const void* cache, const int32_t* table,
+               const int32_t* lens, const int32_t* pos, const int32_t* idx, int causal, int64_t num_blocks,
+               float scale, void* out, void* part_ws, size_t part_bytes, const AttendPlan& pl, hipStream_t st) {
+  MlaParams prm{};
+  prm.q = q;
+  prm.qr = qr;
+  prm.cache = cache;
+  prm.table = table;
+  prm.lens = lens;
+  prm.pos = pos;
+  prm.idx = idx;
+  prm.out = out;
+  prm.part = static_cast<float*>(part_ws);
+  prm.B = a.B;
+  prm.T = a.T;
+  prm.H = a.H;
+  prm.Dc = a.Dc;
+  prm.Dr = a.Dr;
+  prm.W = a.Dc + a.Dr;
+  prm.P = a.P;
+  prm.maxP = a.maxP;
+  prm.nk = a.nk;
+  prm.causal = causal ? 1 : 0;
+  prm.splits = pl.splits;
+  prm.head_groups = pl.head_groups;
+  prm.kch = pl.kch;
+  prm.nt = pl.head_groups == 1 ? 1 : 0;
+  prm.num_blocks = num_blocks;
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T;
+  prm.units = rows * pl.splits;
+  prm.sl2 = scale * kLog2e;
+  if (pl.splits > 1 && part_bytes < attend_partial_bytes(a, pl.splits))
+    return mla_fail(nullptr, 0, "workspace too small for the split partials");
+  (void)hipGetLastError();
+  hipError_t err = hipSuccess;
+  if (pl.mfma) {
+    const int64_t grid = (prm.units + 7) / 8 * 8 * pl.head_groups;
+    if (grid > 2147483647LL) return mla_fail(nullptr, 0, "mla_attend grid exceeds launch limits");
+    err = a.dtype == QD_DTYPE_BF16 ? dispatch_attend_mfma<QD_DTYPE_BF16>(prm, pl, grid, st)
+                                   : dispatch_attend_mfma<QD_DTYPE_F16>(prm, pl, grid, st);
+  } else {
+    const int64_t waves = rows * a.H * pl.splits;
+    const int64_t grid = (waves + 3) / 4;
+    if (grid > 2147483647LL) return mla_fail(nullptr, 0, "mla_attend grid exceeds launch limits");
+    switch (a.dtype) {
+      case QD_DTYPE_F32:
+        hipLaunchKernelGGL(mla_attend_generic_kernel<QD_DTYPE_F32>, dim3(grid), dim3(256), 0, st, prm);
+        break;
+      case QD_DTYPE_F16:
+        hipLaunchKernelGGL(mla_attend_generic_kernel<QD_DTYPE_F16>, dim3(grid), dim3(256), 0, st, prm);
+        break;
+      default:
+        hipLaunchKernelGGL(mla_attend_generic_kernel<QD_DTYPE_BF16>, dim3(grid), dim3(256), 0, st, prm);
+        break;
+    }
+  }
+  if (err != hipSuccess) {
+    qd_set_last_error(static_cast<int>(err), std::string("mla_attend launch setup failed: ") + hipGetErrorString(err));
+    return static_cast<int>(err);
+  }
+  int rc = launch_status("mla_attend");
+  if (rc != QD_OK || pl.splits == 1) return rc;
+  const int64_t mgrid = (rows * a.H + 3) / 4;
+  switch (a.dtype) {
+    case QD_DTYPE_F32: hipLaunchKernelGGL(mla_merge_kernel<QD_DTYPE_F32>, dim3(mgrid), dim3(256), 0, st, prm); break;
+    case QD_DTYPE_F16: hipLaunchKernelGGL(mla_merge_kernel<QD_DTYPE_F16>, dim3(mgrid), dim3(256), 0, st, prm); break;
+    default: hipLaunchKernelGGL(mla_merge_kernel<QD_DTYPE_BF16>, dim3(mgrid), dim3(256), 0, st, prm); break;
+  }
+  return launch_status("mla_attend merge");
+}
+
+bool project_mfma_applies(int di, int dout, int dtype, const void* x, const void* w, const void* out) {
+  return (dtype == QD_DTYPE_F16 || dtype == QD_DTYPE_BF16) && di % 32 == 0 && dout % 8 == 0 && dout >= 8 &&
+         aligned16(x) && aligned16(w) && aligned16(out);
+}
+
+template <int DT>
+void launch_project(const ProjParams& prm, bool absorb, bool mfma, hipStream_t st) {
+  if constexpr (DT != QD_DTYPE_F32) {
+    if (mfma) {
+      const dim3 grid((prm.dout + 127) / 128, prm.H);
+      if (absorb)
+        hipLaunchKernelGGL((mla_project_mfma_kernel<DT, true>), grid, dim3(256), 0, st, prm);
+      else
+        hipLaunchKernelGGL((mla_project_mfma_kernel<DT, false>), grid, dim3(256), 0, st, prm);
+      return;
+    }
+  }
+  {
+    const int64_t n = prm.rows * prm.H * prm.dout;
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    if (absorb)
+      hipLaunchKernelGGL((mla_project_generic_kernel<DT, true>), grid, dim3(256), 0, st, prm);
+    else
+      hipLaunchKernelGGL((mla_project_generic_kernel<DT, false>), grid, dim3(256), 0, st, prm);
+  }
+}
+
+int run_project(const void* x, const void* w, void* out, int64_t rows, int H, int di, int dout, bool absorb,
+                int dtype, int flags, hipStream_t st) {
+  if (rows < 0 || H <= 0 || di <= 0 || dout <= 0) return mla_fail(nullptr, 0, "invalid projection shape");
+  if (!float_dtype(dtype)) return mla_fail(nullptr, 0, "dtype must be float32/float16/bfloat16");
+  if (rows == 0) return QD_OK;
+  if (!x || !w || !out) return mla_fail(nullptr, 0, "null tensor pointer");
+  ProjParams prm{x, w, out, rows, H, di, dout};
+  const bool mfma = (flags & QD_FLAG_FORCE_GENERIC) == 0 && project_mfma_applies(di, dout, dtype, x, w, out);
+  if (!mfma && (rows * H * static_cast<int64_t>(dout) + 255) / 256 > 2147483647LL)
+    return mla_fail(nullptr, 0, "mla_project grid exceeds launch limits");
+  (void)hipGetLastError();
+  switch (dtype) {
+    case QD_DTYPE_F32: launch_project<QD_DTYPE_F32>(prm, absorb, false, st); break;
+    case QD_DTYPE_F16: launch_project<QD_DTYPE_F16>(prm, absorb, mfma, st); break;
+    default: launch_project<QD_DTYPE_BF16>(prm, absorb, mfma, st); break;
+  }
+  return launch_status("mla_project");
+}
+
+size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Workspace of the fused decode: absorbed query and latent output
+// ([R, H, Dc] of the dtype each), then the split partials.
+struct DecodeLayout {
+  size_t qa, latent, part, total;
+};
+
+DecodeLayout decode_layout(const AttendShape& a, int splits) {
+  DecodeLayout d{};
+  const size_t n = static_cast<size_t>(a.B) * a.T * a.H * a.Dc * elem_size(a.dtype);
+  d.qa = 0;
+  d.latent = round_up256(n);
+  d.part = d.latent + round_up256(n);
+  d.total = d.part + attend_partial_bytes(a, splits);
+  return d;
+}
+
+bool attend_shape_ok(const AttendShape& a) {
+  return a.B >= 0 && a.T >= 0 && a.H > 0 && a.Dc > 0 && a.Dc <= 512 && a.Dr > 0 && a.P > 0 && a.maxP > 0 &&
+         a.nk >= -1 && float_dtype(a.dtype) && a.B <= 65535 && a.T <= 65535;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qd_latent_kv_write_validate(const qd_tensor_desc* latent, const qd_tensor_desc* rope,
+                                const qd_tensor_desc* cache, const qd_tensor_desc* slots, char* msg,
+                                size_t msg_cap) {
+  if (!latent || !rope || !cache || !slots) return mla_fail(msg, msg_cap, "null tensor descriptor");
+  if (!placed(latent, latent)) return mla_fail(msg, msg_cap, "latent must be contiguous and on the same CUDA device");
+  if (!placed(rope, latent)) return mla_fail(msg, msg_cap, "rope must be contiguous and on the same CUDA device");
+  if (!placed(cache, latent)) return mla_fail(msg, msg_cap, "cache must be contiguous and on the same CUDA device");
+  if (!placed(slots, latent)) return mla_fail(msg, msg_cap, "slots must be contiguous and on the same CUDA device");
+  if (!float_dtype(latent->dtype)) return mla_fail(msg, msg_cap, "dtype must be float32/float16/bfloat16");
+  if (!(latent->ndim == 2 && rope->ndim == 2 && cache->ndim == 3 && slots->ndim == 1 &&
+        latent->sizes[0] == rope->sizes[0] && slots->sizes[0] == latent->sizes[0]))
+    return mla_fail(msg, msg_cap, "invalid latent/rope/cache/slots shape");
+  if (!(latent->sizes[1] > 0 && rope->sizes[1] > 0 && cache->sizes[1] > 0 &&
+        cache->sizes[2] == latent->sizes[1] + rope->sizes[1]))
+    return mla_fail(msg, msg_cap, "invalid cache width");
+  if (!(slots->dtype == QD_DTYPE_I64 && latent->dtype == rope->dtype && latent->dtype == cache->dtype))
+    return mla_fail(msg, msg_cap, "slots must be int64 and tensors must share dtype");
+  return mla_ok(msg, msg_cap);
+}
+
+int qd_latent_kv_write(const void* latent, const void* rope, void* cache, const int64_t* slots, int64_t tokens,
+                       int latent_dim, int rope_dim, int64_t cache_rows, int dtype, void* stream) {
+  const int es = elem_size(dtype);
+  if (es == 0) return mla_fail(nullptr, 0, "dtype must be float32/float16/bfloat16");
+  if (tokens < 0 || latent_dim <= 0 || rope_dim <= 0 || cache_rows < 0)
+    return mla_fail(nullptr, 0, "invalid latent/rope/cache/slots shape");
+  if (tokens > 2147483647LL) return mla_fail(nullptr, 0, "too many tokens for one launch");
+  if (tokens == 0) return QD_OK;
+  if (!latent || !rope || !cache || !slots) return mla_fail(nullptr, 0, "null tensor pointer");
+  LatentWriteParams prm;
+  prm.latent = static_cast<const char*>(latent);
+  prm.rope = static_cast<const char*>(rope);
+  prm.cache = static_cast<char*>(cache);
+  prm.slots = slots;
+  prm.lat_bytes = static_cast<int64_t>(latent_dim) * es;
+  prm.rope_bytes = static_cast<int64_t>(rope_dim) * es;
+  prm.row_bytes = prm.lat_bytes + prm.rope_bytes;
+  prm.rows = cache_rows;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  const dim3 grid(static_cast<unsigned>(tokens));
+  if (prm.lat_bytes % 16 == 0 && prm.rope_bytes % 16 == 0 && aligned16(latent) && aligned16(rope) &&
+      aligned16(cache))
+    hipLaunchKernelGGL(latent_write_vec16_kernel, grid, dim3(64), 0, st, prm);
+  else if (es == 4)
+    hipLaunchKernelGGL(latent_write_elem_kernel<uint32_t>, grid, dim3(64), 0, st, prm);
+  else
+    hipLaunchKernelGGL(latent_write_elem_kernel<uint16_t>, grid, dim3(64), 0, st, prm);
+  return launch_status("latent_kv_write");
+}
+
+int qd_mla_project_validate(const qd_tensor_desc* x, const qd_tensor_desc* w, int absorb, char* msg,
+                            size_t msg_cap) {
+  if (!x || !w) return mla_fail(msg, msg_cap, "null tensor descriptor");
+  if (!placed(x, x)) return mla_fail(msg, msg_cap, "x must be contiguous and on the same CUDA device");
+  if (!placed(w, x)) return mla_fail(msg, msg_cap, "w must be contiguous and on the same CUDA device");
+  if (!float_dtype(x->dtype)) return mla_fail(msg, msg_cap, "dtype must be float32/float16/bfloat16");
+  if (x->dtype != w->dtype) return mla_fail(msg, msg_cap, "dtype mismatch");
+  if (!(x->ndim == 4 && w->ndim == 3 && x->sizes[2] == w->sizes[0]))
+    return mla_fail(msg, msg_cap, "x [B,T,H,D], weight [H,Dn,Dc] or [H,Dv,Dc]");
+  const int64_t di = x->sizes[3], dout = absorb ? w->sizes[2] : w->sizes[1];
+  if (!(di > 0 && dout > 0 && (absorb ? w->sizes[1] == di : w->sizes[2] == di)))
+    return mla_fail(msg, msg_cap, "projection dimension mismatch");
+  return mla_ok(msg, msg_cap);
+}
+
+int qd_mla_project(const void* x, const void* w, void* out, int64_t rows, int heads, int in_dim, int out_dim,
+                   int absorb, int dtype, int flags, void* stream) {
+  return run_project(x, w, out, rows, heads, in_dim, out_dim, absorb != 0, dtype, flags,
+                     static_cast<hipStream_t>(stream));
+}
+
+int qd_mla_attend_validate(const qd_tensor_desc* q, const qd_tensor_desc* q_rope, const qd_tensor_desc* cache,
+                           const qd_tensor_desc* table, const qd_tensor_desc* lengths,
+                           const qd_tensor_desc* positions, const qd_tensor_desc* indices, double scale,
+                           char* msg, size_t msg_cap) {
+  if (!q || !q_rope || !cache || !table || !lengths || !positions)
+    return mla_fail(msg, msg_cap, "null tensor descriptor");
+  if (!placed(q, q)) return mla_fail(msg, msg_cap, "q must be contiguous and on the same CUDA device");
+  if (!placed(q_rope, q)) return mla_fail(msg, msg_cap, "q_rope must be contiguous and on the same CUDA device");
+  if (!placed(cache, q)) return mla_fail(msg, msg_cap, "cache must be contiguous and on the same CUDA device");
+  if (!placed(table, q)) return mla_fail(msg, msg_cap, "table must be contiguous and on the same CUDA device");
+  if (!placed(lengths, q)) return mla_fail(msg, msg_cap, "lengths must be contiguous and on the same CUDA device");
+  if (!placed(positions, q))
+    return mla_fail(msg, msg_cap, "positions must be contiguous and on the same CUDA device");
+  if (!float_dtype(q->dtype)) return mla_fail(msg, msg_cap, "dtype must be float32/float16/bfloat16");
+  if (!(q->ndim == 4 && q_rope->ndim == 4 && cache->ndim == 3 && table->ndim == 2 && lengths->ndim == 1 &&
+        positions->ndim == 2))
+    return mla_fail(msg, msg_cap, "invalid tensor ranks");
+  const int64_t* qs = q->sizes;
+  if (!(qs[0] == q_rope->sizes[0] && qs[1] == q_rope->sizes[1] && qs[2] == q_rope->sizes[2] &&
+        qs[0] == table->sizes[0] && qs[0] == lengths->sizes[0] && positions->sizes[0] == qs[0] &&
+        positions->sizes[1] == qs[1]))
+    return mla_fail(msg, msg_cap, "shape mismatch");
+  if (!(qs[3] > 0 && qs[3] <= 512 && q_rope->sizes[3] > 0 && cache->sizes[2] == qs[3] + q_rope->sizes[3] &&
+        cache->sizes[0] > 0 && cache->sizes[1] > 0 && table->sizes[1] > 0 && qs[2] > 0))
+    return mla_fail(msg, msg_cap, "invalid dimensions");
+  if (!(qs[0] <= 65535 && qs[1] <= 65535)) return mla_fail(msg, msg_cap, "CUDA grid limit");
+  if (!(q->dtype == q_rope->dtype && q->dtype == cache->dtype)) return mla_fail(msg, msg_cap, "dtype mismatch");
+  if (!(table->dtype == QD_DTYPE_I32 && lengths->dtype == QD_DTYPE_I32 && positions->dtype == QD_DTYPE_I32))
+    return mla_fail(msg, msg_cap, "metadata must be int32");
+  if (!(std::isfinite(scale) && scale > 0)) return mla_fail(msg, msg_cap, "scale must be positive and finite");
+  if (indices && indices->defined) {
+    if (!placed(indices, q))
+      return mla_fail(msg, msg_cap, "indices must be contiguous and on the same CUDA device");
+    if (!(indices->ndim == 3 && indices->sizes[0] == qs[0] && indices->sizes[1] == qs[1] &&
+          indices->dtype == QD_DTYPE_I32))
+      return mla_fail(msg, msg_cap, "indices must be int32 [B,T,K]");
+  }
+  return mla_ok(msg, msg_cap);
+}
+
+size_t qd_mla_attend_workspace_bytes(int batch, int q_len, int heads, int latent_dim, int rope_dim,
+                                     int block_size, int max_pages, int num_indices, int dtype, int splits,
+                                     int flags) {
+  const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
+  if (!attend_shape_ok(a)) return 0;
+  return attend_partial_bytes(a, plan_attend(a, splits, flags).splits);
+}
+
+int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope_dim, int block_size,
+                       int max_pages, int num_indices, int dtype, int splits, int flags, int* out_splits,
+                       int* head_groups) {
+  const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
+  if (!attend_shape_ok(a)) return -1;
+  const AttendPlan pl = plan_attend(a, splits, flags);
+  if (out_splits) *out_splits = pl.splits;
+  if (head_groups) *head_groups = pl.mfma ? pl.head_groups : 0;
+  return pl.mfma ? 1 : 0;
+}
+
+int qd_mla_attend(const void* q, const void* q_rope, const void* cache, const int32_t* block_table,
+                  const int32_t* lengths, const int32_t* positions, const int32_t* indices, void* out,
+                  void* workspace, size_t workspace_bytes, int batch, int q_len, int heads, int latent_dim,
+                  int rope_dim, int block_size, int max_pages, int64_t num_blocks, int num_indices, int causal,
+                  int dtype, float scale, int splits, int flags, void* stream) {
+  const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
+  if (!attend_shape_ok(a) || num_blocks <= 0) return mla_fail(nullptr, 0, "invalid dimensions");
+  if (num_indices > 0 && !indices) return mla_fail(nullptr, 0, "null indices with num_indices > 0");
+  if (splits < 0 || splits > 65535) return mla_fail(nullptr, 0, "splits must be in [0, 65535]");
+  if (!(std::isfinite(scale) && scale > 0.f)) return mla_fail(nullptr, 0, "scale must be positive and finite");
+  if (static_cast<int64_t>(batch) * q_len == 0) return QD_OK;
+  if (!q || !q_rope || !cache || !block_table || !lengths || !positions || !out)
+    return mla_fail(nullptr, 0, "null tensor pointer");
+  AttendPlan pl = plan_attend(a, splits, flags);
+  if (pl.mfma && !(aligned16(cache) && aligned16(out))) pl.mfma = false;
+  return run_attend(a, q, q_rope, cache, block_table, lengths, positions, indices, causal, num_blocks, scale, out,
+                    workspace, workspace_bytes, pl, static_cast<hipStream_t>(stream));
+}
+
+int qd_mla_decode_validate(const qd_tensor_desc* q_nope, const qd_tensor_desc* q_rope, const qd_tensor_desc* cache,
+                           const qd_tensor_desc* table, const qd_tensor_desc* lengths,
+                           const qd_tensor_desc* positions, const qd_tensor_desc* w_uk, const qd_tensor_desc* w_uv,
+                           const qd_tensor_desc* indices, double scale, char* msg, size_t msg_cap) {
+  const qd_tensor_desc* all[8] = {q_nope, q_rope, cache, table, lengths, positions, w_uk, w_uv};
+  for (int i = 0; i < 8; ++i)
+    if (!all[i]) return mla_fail(msg, msg_cap, "null tensor descriptor");
+  for (int i = 0; i < 8; ++i)
+    if (!placed(all[i], q_nope)) return mla_fail(msg, msg_cap, "input must be contiguous and on the same CUDA device");
+  if (!float_dtype(q_nope->dtype)) return mla_fail(msg, msg_cap, "dtype must be float32/float16/bfloat16");
+  if (!(q_nope->ndim == 4 && q_rope->ndim == 4 && cache->ndim == 3 && table->ndim == 2 && lengths->ndim == 1 &&
+        positions->ndim == 2 && w_uk->ndim == 3 && w_uv->ndim == 3))
+    return mla_fail(msg, msg_cap, "invalid tensor ranks");
+  const int64_t* qs = q_nope->sizes;
+  if (!(qs[0] == q_rope->sizes[0] && qs[1] == q_rope->sizes[1] && qs[2] == q_rope->sizes[2] &&
+        qs[0] == table->sizes[0] && qs[0] == lengths->sizes[0] && positions->sizes[0] == qs[0] &&
+        positions->sizes[1] == qs[1]))
+    return mla_fail(msg, msg_cap, "shape mismatch");
+  const int64_t dc = w_uk->sizes[2];
+  if (!(qs[2] > 0 && qs[3] > 0 && q_rope->sizes[3] > 0 && dc > 0 && dc <= 512 && w_uv->sizes[1] > 0 &&
+        w_uk->sizes[0] == qs[2] && w_uk->sizes[1] == qs[3] && w_uv->sizes[0] == qs[2] && w_uv->sizes[2] == dc &&
+        cache->sizes[2] == dc + q_rope->sizes[3] && cache->sizes[0] > 0 && cache->sizes[1] > 0 &&
+        table->sizes[1] > 0 && qs[0] <= 65535 && qs[1] <= 65535))
+    return mla_fail(msg, msg_cap, "invalid dimensions");
+  if (!(q_nope->dtype == q_rope->dtype && q_nope->dtype == cache->dtype && q_nope->dtype == w_uk->dtype &&
+        q_nope->dtype == w_uv->dtype))
+    return mla_fail(msg, msg_cap, "dtype mismatch");
+  if (!(table->dtype == QD_DTYPE_I32 && lengths->dtype == QD_DTYPE_I32 && positions->dtype == QD_DTYPE_I32 &&
+        std::isfinite(scale) && scale > 0))
+    return mla_fail(msg, msg_cap, "invalid metadata or scale");
+  if (indices && indices->defined) {
+    if (!placed(indices, q_nope))
+      return mla_fail(msg, msg_cap, "indices must be contiguous and on the same CUDA device");
+    if (!(indices->ndim == 3 && indices->sizes[0] == qs[0] && indices->sizes[1] == qs[1] &&
+          indices->dtype == QD_DTYPE_I32))
+      return mla_fail(msg, msg_cap, "invalid indices");
+  }
+  return mla_ok(msg, msg_cap);
+}
+
+size_t qd_mla_decode_workspace_bytes(int batch, int q_len, int heads, int latent_dim, int rope_dim,
+                                     int block_size, int max_pages, int num_indices, int dtype, int splits,
+                                     int flags) {
+  const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
+  if (!attend_shape_ok(a)) return 0;
+  return decode_layout(a, plan_attend(a, splits, flags).splits).total;
+}
+
+int qd_mla_decode(const void* q_nope, const void* q_rope, const void* cache, const int32_t* block_table,
+                  const int32_t* lengths, const int32_t* positions, const void* w_uk, const void* w_uv,
+                  const int32_t* indices, void* out, void* workspace, size_t workspace_bytes, int batch, int q_len,
+                  int heads, int nope_dim, int latent_dim, int rope_dim, int value_dim, int block_size,
+                  int max_pages, int64_t num_blocks, int num_indices, int causal, int dtype, float scale,
+                  int splits, int flags, void* stream) {
+  const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
+  if (!attend_shape_ok(a) || nope_dim <= 0 || value_dim <= 0 || num_blocks <= 0)
+    return mla_fail(nullptr, 0, "invalid dimensions");
+  if (num_indices > 0 && !indices) return mla_fail(nullptr, 0, "null indices with num_indices > 0");
+  if (splits < 0 || splits > 65535) return mla_fail(nullptr, 0, "splits must be in [0, 65535]");
+  if (!(std::isfinite(scale) && scale > 0.f)) return mla_fail(nullptr, 0, "scale must be positive and finite");
+  const int64_t rows = static_cast<int64_t>(batch) * q_len;
+  if (rows == 0) return QD_OK;
+  if (!q_nope || !q_rope || !cache || !block_table || !lengths || !positions || !w_uk || !w_uv || !out)
+    return mla_fail(nullptr, 0, "null tensor pointer");
+  AttendPlan pl = plan_attend(a, splits, flags);
+  const DecodeLayout lay = decode_layout(a, pl.splits);
+  if (!workspace || workspace_bytes < lay.total || !aligned16(workspace))
+    return mla_fail(nullptr, 0, "workspace must hold qd_mla_decode_workspace_bytes() bytes, 16-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  void* qa = ws + lay.qa;
+  void* latent = ws + lay.latent;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = run_project(q_nope, w_uk, qa, rows, heads, nope_dim, latent_dim, true, dtype, flags, st);
+  if (rc != QD_OK) return rc;
+  if (pl.mfma && !aligned16(cache)) pl.mfma = false;
+  rc = run_attend(a, qa, q_rope, cache, block_table, lengths, positions, indices, causal, num_blocks, scale, latent,
+                  ws + lay.part, workspace_bytes - lay.part, pl, st);
+  if (rc != QD_OK) return rc;
+  return run_project(latent, w_uv, out, rows, heads, latent_dim, value_dim, false, dtype, flags, st);
+}
+
+}  // extern "C"

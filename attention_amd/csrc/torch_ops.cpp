@@ -1,7 +1,7 @@
 // Thin PyTorch-ROCm binding: registers the reference's `qd_attention` op
 // schemas and forwards to the C ABI of libqd_attention.so.
 //
-// Schemas   csrc/binding/torch_ops.cpp:52-56 (reference tree)
+// Schemas   csrc/binding/torch_ops.cpp:47-56 (reference tree)
 // Impl key  CUDA (PyTorch-ROCm's key for HIP devices), as torch_ops.cpp:59-77
 // Host path csrc/cuda/dense/gqa_decode.cu:96-183: validation in the
 //           reference's order and words, device guard, empty_like output,
@@ -29,6 +29,7 @@ int dtype_code(const at::Tensor& t) {
     case at::kHalf: return QD_DTYPE_F16;
     case at::kBFloat16: return QD_DTYPE_BF16;
     case at::kInt: return QD_DTYPE_I32;
+    case at::kLong: return QD_DTYPE_I64;
     default: return QD_DTYPE_OTHER;
   }
 }
@@ -177,9 +178,122 @@ void kv_append_hip(const at::Tensor& key, const at::Tensor& value, at::Tensor k_
   TORCH_CHECK(st == QD_OK, qd_error_string(st));
 }
 
+// ---- Paged MLA decode (reference csrc/cuda/mla/mla.cu:138-198) ----------
+
+at::Tensor byte_workspace(const at::Tensor& like, size_t bytes) {
+  return at::empty({static_cast<int64_t>(std::max<size_t>(bytes, 16))}, like.options().dtype(at::kByte));
+}
+
+const int32_t* optional_indices(const c10::optional<at::Tensor>& indices) {
+  return indices.has_value() ? indices->data_ptr<int32_t>() : nullptr;
+}
+
+// mla_project (mla.cu:138-150).
+at::Tensor mla_project_hip(const at::Tensor& x, const at::Tensor& w, bool absorb) {
+  const qd_tensor_desc dx = describe(x), dw = describe(w);
+  char msg[256];
+  int st = qd_mla_project_validate(&dx, &dw, absorb ? 1 : 0, msg, sizeof(msg));
+  TORCH_CHECK(st == QD_OK, msg);
+  const int64_t dout = absorb ? w.size(2) : w.size(1);
+  auto out = at::empty({x.size(0), x.size(1), x.size(2), dout}, x.options());
+  if (out.numel() == 0) return out;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(x.get_device()).stream();
+  st = qd_mla_project(x.data_ptr(), w.data_ptr(), out.data_ptr(), x.size(0) * x.size(1),
+                      static_cast<int>(x.size(2)), static_cast<int>(x.size(3)), static_cast<int>(dout),
+                      absorb ? 1 : 0, dx.dtype, 0, stream);
+  TORCH_CHECK(st == QD_OK, qd_error_string(st));
+  return out;
+}
+
+// latent_kv_write (mla.cu:151-160).
+void latent_kv_write_hip(const at::Tensor& latent, const at::Tensor& rope, at::Tensor cache,
+                         const at::Tensor& slots) {
+  const qd_tensor_desc dl = describe(latent), dr = describe(rope), dc = describe(cache), ds = describe(slots);
+  char msg[256];
+  int st = qd_latent_kv_write_validate(&dl, &dr, &dc, &ds, msg, sizeof(msg));
+  TORCH_CHECK(st == QD_OK, msg);
+  if (!latent.size(0)) return;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(latent.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(latent.get_device()).stream();
+  st = qd_latent_kv_write(latent.data_ptr(), rope.data_ptr(), cache.data_ptr(), slots.data_ptr<int64_t>(),
+                          latent.size(0), static_cast<int>(latent.size(1)), static_cast<int>(rope.size(1)),
+                          cache.size(0) * cache.size(1), dl.dtype, stream);
+  TORCH_CHECK(st == QD_OK, qd_error_string(st));
+}
+
+// mla_attend (mla.cu:161-181).
+at::Tensor mla_attend_hip(const at::Tensor& q, const at::Tensor& qr, const at::Tensor& cache,
+                          const at::Tensor& table, const at::Tensor& lens, const at::Tensor& positions,
+                          const c10::optional<at::Tensor>& indices, double scale, bool causal) {
+  const qd_tensor_desc dq = describe(q), dr = describe(qr), dc = describe(cache), dt = describe(table),
+                       dl = describe(lens), dp = describe(positions);
+  const qd_tensor_desc di = indices.has_value() ? describe(*indices) : qd_tensor_desc{};
+  char msg[256];
+  int st = qd_mla_attend_validate(&dq, &dr, &dc, &dt, &dl, &dp, &di, scale, msg, sizeof(msg));
+  TORCH_CHECK(st == QD_OK, msg);
+  auto out = at::empty_like(q);
+  if (q.numel() == 0) return out;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int B = static_cast<int>(q.size(0)), T = static_cast<int>(q.size(1)), H = static_cast<int>(q.size(2));
+  const int Dc = static_cast<int>(q.size(3)), Dr = static_cast<int>(qr.size(3));
+  const int P = static_cast<int>(cache.size(1)), maxP = static_cast<int>(table.size(1));
+  const int nk = indices.has_value() ? static_cast<int>(indices->size(2)) : -1;
+  const size_t bytes = qd_mla_attend_workspace_bytes(B, T, H, Dc, Dr, P, maxP, nk, dq.dtype, 0, 0);
+  at::Tensor ws;
+  if (bytes > 0) ws = byte_workspace(q, bytes);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  st = qd_mla_attend(q.data_ptr(), qr.data_ptr(), cache.data_ptr(), table.data_ptr<int32_t>(),
+                     lens.data_ptr<int32_t>(), positions.data_ptr<int32_t>(), optional_indices(indices),
+                     out.data_ptr(), ws.defined() ? ws.data_ptr() : nullptr, bytes, B, T, H, Dc, Dr, P, maxP,
+                     cache.size(0), nk, causal ? 1 : 0, dq.dtype, static_cast<float>(scale), 0, 0, stream);
+  TORCH_CHECK(st == QD_OK, qd_error_string(st));
+  return out;
+}
+
+// mla_decode_fused (mla.cu:184-198): absorption, paged latent attention
+// and value projection.
+at::Tensor mla_decode_fused_hip(const at::Tensor& q, const at::Tensor& qr, const at::Tensor& cache,
+                                const at::Tensor& table, const at::Tensor& lens, const at::Tensor& positions,
+                                const at::Tensor& wk, const at::Tensor& wv,
+                                const c10::optional<at::Tensor>& indices, double scale, bool causal) {
+  const qd_tensor_desc dq = describe(q), dr = describe(qr), dc = describe(cache), dt = describe(table),
+                       dl = describe(lens), dp = describe(positions), dk = describe(wk), dv = describe(wv);
+  const qd_tensor_desc di = indices.has_value() ? describe(*indices) : qd_tensor_desc{};
+  char msg[256];
+  int st = qd_mla_decode_validate(&dq, &dr, &dc, &dt, &dl, &dp, &dk, &dv, &di, scale, msg, sizeof(msg));
+  TORCH_CHECK(st == QD_OK, msg);
+  auto out = at::empty({q.size(0), q.size(1), q.size(2), wv.size(1)}, q.options());
+  if (!out.numel()) return out;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int B = static_cast<int>(q.size(0)), T = static_cast<int>(q.size(1)), H = static_cast<int>(q.size(2));
+  const int Dn = static_cast<int>(q.size(3)), Dc = static_cast<int>(wk.size(2)), Dr = static_cast<int>(qr.size(3));
+  const int Dv = static_cast<int>(wv.size(1));
+  const int P = static_cast<int>(cache.size(1)), maxP = static_cast<int>(table.size(1));
+  const int nk = indices.has_value() ? static_cast<int>(indices->size(2)) : -1;
+  const size_t bytes = qd_mla_decode_workspace_bytes(B, T, H, Dc, Dr, P, maxP, nk, dq.dtype, 0, 0);
+  const at::Tensor ws = byte_workspace(q, bytes);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  st = qd_mla_decode(q.data_ptr(), qr.data_ptr(), cache.data_ptr(), table.data_ptr<int32_t>(),
+                     lens.data_ptr<int32_t>(), positions.data_ptr<int32_t>(), wk.data_ptr(), wv.data_ptr(),
+                     optional_indices(indices), out.data_ptr(), ws.data_ptr(), bytes, B, T, H, Dn, Dc, Dr, Dv,
+                     P, maxP, cache.size(0), nk, causal ? 1 : 0, dq.dtype, static_cast<float>(scale), 0, 0,
+                     stream);
+  TORCH_CHECK(st == QD_OK, qd_error_string(st));
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(qd_attention, m) {
+  m.def(
+      "mla_decode_fused(Tensor q, Tensor qr, Tensor cache, Tensor table, Tensor lens, Tensor positions, "
+      "Tensor wk, Tensor wv, Tensor? indices, float scale, bool causal) -> Tensor");
+  m.def("mla_project(Tensor x, Tensor weight, bool absorb) -> Tensor");
+  m.def("latent_kv_write(Tensor latent, Tensor rope, Tensor(a!) cache, Tensor slots) -> ()");
+  m.def(
+      "mla_attend(Tensor q, Tensor q_rope, Tensor cache, Tensor table, Tensor lens, Tensor positions, "
+      "Tensor? indices, float scale, bool causal) -> Tensor");
   m.def(
       "kv_append(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor block_table, "
       "Tensor positions) -> ()");
@@ -195,6 +309,10 @@ TORCH_LIBRARY(qd_attention, m) {
 }
 
 TORCH_LIBRARY_IMPL(qd_attention, CUDA, m) {
+  m.impl("mla_decode_fused", TORCH_FN(mla_decode_fused_hip));
+  m.impl("mla_project", TORCH_FN(mla_project_hip));
+  m.impl("latent_kv_write", TORCH_FN(latent_kv_write_hip));
+  m.impl("mla_attend", TORCH_FN(mla_attend_hip));
   m.impl("kv_append", TORCH_FN(kv_append_hip));
   m.impl("gqa_decode_split_workspace", TORCH_FN(gqa_decode_split_workspace_hip));
   m.impl("gqa_decode_split", TORCH_FN(gqa_decode_split_hip));

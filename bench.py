@@ -56,8 +56,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=5)
     ap.add_argument("--mode", choices=["decode", "copy"], default="decode")
-    ap.add_argument("--op", choices=["decode", "kv_append"], default="decode",
-                    help="kv_append: time the paged cache append on the config's shapes instead")
+    ap.add_argument("--op", choices=["decode", "kv_append", "mla"], default="decode",
+                    help="kv_append: time the paged cache append on the config's shapes instead; "
+                         "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config")
+    ap.add_argument("--mla-config", default="mla-h128")
     ap.add_argument("--device-gen", action="store_true", help="draw inputs on the GPU")
     return ap.parse_args()
 
@@ -204,6 +206,140 @@ def kv_append_mode(args) -> None:
     }), flush=True)
 
 
+PEAK_MFMA_BF16_TFLOPS = 2500.0
+
+
+def mla_mode(args) -> None:
+    """One step = one attention_amd.mla_decode call (query absorption, paged
+    latent attention, value projection) over the batch of --mla-config, with
+    caches and weights rotated over pools above the Infinity Cache size.
+    value = algorithmic HBM bytes of the call / time: visible cache rows
+    once, q_nope and q_rope, both weight tensors, the output, lengths,
+    positions and used table entries.  The roofline is the latent-attention
+    stage alone (qd_mla_attend: attention kernel, plus the split merge when
+    the plan splits), on the absorbed query."""
+    import attention_amd
+    from attention_amd import cabi
+    from attention_amd.cases import MLA_CONFIGS, mla_attend_bytes
+
+    cfg = MLA_CONFIGS[args.mla_config]
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    lengths = cfg.lengths()
+    c_cpu = cfg.make(device="cpu")
+    c = {k: (v.to(dev) if v is not None else None) for k, v in c_cpu.items()}
+    B, H = cfg.batch, cfg.heads
+    Dn, Dc, Dr, Dv, P = cfg.nope_dim, cfg.latent_dim, cfg.rope_dim, cfg.value_dim, cfg.block_size
+    s = c["cache"].element_size()
+    per_pool = (c["cache"].numel() + c["w_uk"].numel() + c["w_uv"].numel()) * s
+    pools = args.pools or max(2, math.ceil(768e6 / per_pool))
+    caches, wks, wvs = [c["cache"]], [c["w_uk"]], [c["w_uv"]]
+    for i in range(1, pools):
+        caches.append(c["cache"].roll(i, dims=0).contiguous())
+        wks.append(c["w_uk"].roll(i, dims=0).contiguous())
+        wvs.append(c["w_uv"].roll(i, dims=0).contiguous())
+    table, lens, pos = c["table"], c["lens"], c["positions"]
+    scale = 1.0 / math.sqrt(Dn + Dr)
+    torch.cuda.synchronize()
+    log(f"{cfg.name}: {B} seqs, sum len {sum(lengths)}, cache {c['cache'].numel() * s / 1e6:.1f} MB, "
+        f"weights {(c['w_uk'].numel() + c['w_uv'].numel()) * s / 1e6:.1f} MB x {pools} pools, "
+        f"setup {time.perf_counter() - t0:.1f}s")
+    stream = torch.cuda.current_stream(dev)
+
+    if args.splits:
+        out = torch.empty(B, 1, H, Dv, dtype=cfg.dtype, device=dev)
+
+        def step(i):
+            rc = cabi.mla_decode(c["q_nope"], c["q_rope"], caches[i % pools], table, lens, pos, wks[i % pools],
+                                 wvs[i % pools], out, scale=scale, splits=args.splits)
+            if rc:
+                raise RuntimeError(cabi.error_string(rc))
+        path = f"C ABI qd_mla_decode splits={args.splits}"
+    else:
+        def step(i):
+            attention_amd.mla_decode(c["q_nope"], c["q_rope"], caches[i % pools], table, lens, pos,
+                                     wks[i % pools], wvs[i % pools])
+        path = "attention_amd.mla_decode (torch.ops.qd_attention.mla_decode_fused)"
+    ms = time_loop(step, args.steps, args.warmup, stream)
+    rows = sum(lengths)
+    meta = 4 * B + 4 * B + 4 * sum(math.ceil(x / P) for x in lengths)
+    call_bytes = (rows * (Dc + Dr) * s + B * H * (Dn + Dr) * s + H * Dn * Dc * s + H * Dv * Dc * s
+                  + B * H * Dv * s + meta)
+    gbs = call_bytes / (ms * 1e-3) / 1e9
+    log(f"mla_decode: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s algorithmic")
+
+    # Latent attention alone, on the absorbed query.
+    kind, splits, groups = cabi.mla_attend_info(B, 1, H, Dc, Dr, P, table.shape[1], -1, cabi.DTYPE[cfg.dtype],
+                                                args.splits)
+    qa = attention_amd.mla_query_absorb(c["q_nope"], c["w_uk"])
+    lat = torch.empty(B, 1, H, Dc, dtype=cfg.dtype, device=dev)
+    need = cabi.lib().qd_mla_attend_workspace_bytes(B, 1, H, Dc, Dr, P, table.shape[1], -1,
+                                                    cabi.DTYPE[cfg.dtype], args.splits, 0)
+    ws = torch.empty(max(16, need), dtype=torch.uint8, device=dev)
+
+    def attend(i):
+        rc = cabi.mla_attend(qa, c["q_rope"], caches[i % pools], table, lens,
+                             pos, lat, scale=scale, splits=args.splits, workspace=ws, stream=stream.cuda_stream)
+        if rc:
+            raise RuntimeError(cabi.error_string(rc))
+    a_ms = time_loop(attend, args.steps, args.warmup, stream)
+    a_bytes = mla_attend_bytes(lengths, 1, H, Dc, Dr, P, s)
+    a_gbs = a_bytes / (a_ms * 1e-3) / 1e9
+    a_flops = 2 * rows * H * (Dc + Dr + Dc)
+    a_tflops = a_flops / (a_ms * 1e-3) / 1e12
+    kname = "mla_attend_mfma_kernel" if kind == 1 else "mla_attend_generic_kernel"
+    kernels = kname + ("+mla_merge_kernel" if splits > 1 else "")
+    log(f"{kernels}: {a_ms * 1e3:.2f} us, {a_gbs:.1f} GB/s ({100 * a_gbs / PEAK_HBM_GBS:.1f}% of HBM peak), "
+        f"{a_tflops:.1f} TFLOP/s ({100 * a_tflops / PEAK_MFMA_BF16_TFLOPS:.1f}% of bf16 MFMA peak); "
+        f"splits={splits} head_groups={groups}")
+    result = {
+        "metric": "paged MLA decode µs/call and achieved HBM GB/s, 1 MI355X",
+        "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 3),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": DT_NAME[cfg.dtype],
+        "data": "synthetic: seeded N(0,1) latent cache and queries, scaled N(0,1) weights, shuffled exact pool",
+        "config": {"workload": f"{cfg.name}: {cfg.description}", "batch": B, "heads": H, "nope_dim": Dn,
+                   "latent_dim": Dc, "rope_dim": Dr, "value_dim": Dv, "block_size": P,
+                   "context_lens": f"U{list(cfg.len_range)}: sum {rows}, min {min(lengths)}, max {max(lengths)}",
+                   "pools_rotated": pools, "path": path, "algorithmic_bytes_per_call": call_bytes},
+        "roofline": {"bound": "hbm", "kernel": kernels, "achieved": round(a_gbs, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(a_gbs / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic(kname, cfg.name), "duration_us": round(a_ms * 1e3, 3),
+                     "algorithmic_bytes": a_bytes, "mfma_tflops": round(a_tflops, 2),
+                     "mfma_frac": round(a_tflops / PEAK_MFMA_BF16_TFLOPS, 4), "splits": splits,
+                     "head_groups": groups,
+                     "note": "latent attention on the absorbed query (qd_mla_attend), HIP events on its stream; "
+                             f"{a_flops / a_bytes:.0f} flop/byte against a bf16 ridge of "
+                             f"{PEAK_MFMA_BF16_TFLOPS / PEAK_HBM_GBS * 1e3:.0f}"},
+    }
+    if not args.no_cpu_baseline:
+        from oracle.cpu_path import reference_mla_cpu_path
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        torch.set_num_threads(threads)
+        nb = 2
+        sample = [c_cpu[k][:nb] for k in ("q_nope", "q_rope")] + [c_cpu["cache"], c_cpu["table"][:nb],
+                                                                  c_cpu["lens"][:nb], c_cpu["positions"][:nb],
+                                                                  c_cpu["w_uk"], c_cpu["w_uv"]]
+        reference_mla_cpu_path(*sample, scale=scale)
+        times, t_start = [], time.perf_counter()
+        while True:
+            t1 = time.perf_counter()
+            reference_mla_cpu_path(*sample, scale=scale)
+            times.append(time.perf_counter() - t1)
+            if (len(times) >= 3 and time.perf_counter() - t_start >= 10.0) or time.perf_counter() - t_start >= 30.0:
+                break
+        t = statistics.median(times)
+        sb = (sum(lengths[:nb]) * (Dc + Dr) * s + nb * H * (Dn + Dr + Dv) * s + H * Dn * Dc * s
+              + H * Dv * Dc * s)
+        result["cpu_baseline"] = {
+            "value": round(sb / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle/cpu_path.reference_mla_cpu_path (torch CPU ops of reference "
+                       f"attention/reference/mla.py:6-34, absorbed) on the first {nb} of {B} sequences "
+                       f"({sum(lengths[:nb])} tokens), median of {len(times)} calls: {t * 1e3:.1f} ms"),
+            "cpu": _cpu_model()}
+    print(json.dumps(result), flush=True)
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -229,6 +365,9 @@ def main() -> None:
         return
     if args.op == "kv_append":
         kv_append_mode(args)
+        return
+    if args.op == "mla":
+        mla_mode(args)
         return
 
     import attention_amd

@@ -50,6 +50,7 @@ enum {
   QD_DTYPE_F16 = 1,
   QD_DTYPE_BF16 = 2,
   QD_DTYPE_I32 = 3,
+  QD_DTYPE_I64 = 4,
   QD_DTYPE_OTHER = -1
 };
 
@@ -233,6 +234,100 @@ enum {
 int qd_validate_paged_metadata(const int32_t* block_table, const int32_t* context_lens,
                                const int32_t* positions, int batch, int max_pages, int block_size,
                                int64_t num_blocks, unsigned long long* result, void* stream);
+
+/* ---- Paged MLA (multi-head latent attention) decode -----------------
+ * Replaces the reference's MLA decode operators (csrc/cuda/mla/mla.cu,
+ * ops mla_project / latent_kv_write / mla_attend / mla_decode_fused,
+ * csrc/binding/torch_ops.cpp:47-50; Python attention/mla.py:16-53).
+ * Layouts (row-major, contiguous, one device, one dtype unless noted):
+ *   cache        [num_blocks, block_size, latent_dim + rope_dim]
+ *                (latent | rope key per token)
+ *   block_table  [batch, max_pages] int32; lengths [batch] int32
+ *   positions    [batch, q_len] int32 (absolute position of each query)
+ *   indices      [batch, q_len, num_indices] int32 logical token ids;
+ *                num_indices = -1 (indices unused, may be NULL) attends to
+ *                all visible tokens; ids outside [0, end) are skipped
+ *   q / q_nope   [batch, q_len, heads, latent_dim / nope_dim]
+ *   q_rope       [batch, q_len, heads, rope_dim]
+ *   w_uk [heads, nope_dim, latent_dim]; w_uv [heads, value_dim, latent_dim]
+ * Query row (b, t) sees tokens [0, end) with end = min(len, max(0, pos+1))
+ * when `causal`, else len (clamped to max_pages*block_size); a row with no
+ * visible token is zero.  `splits` 0 picks the context split from static
+ * shapes and the device; > 0 forces it.  flags: QD_FLAG_FORCE_GENERIC
+ * selects the VALU kernels.  Nothing here allocates or synchronizes. */
+
+/* Reference checks in order, messages included (mla.cu:152-155). */
+int qd_latent_kv_write_validate(const qd_tensor_desc* latent, const qd_tensor_desc* rope,
+                                const qd_tensor_desc* cache, const qd_tensor_desc* slots, char* msg,
+                                size_t msg_cap);
+
+/* Writes [latent | rope] of token t to flat cache row slots[t] (int64) of
+ * the [num_blocks*block_size, latent_dim+rope_dim] view (mla.cu:28-32,
+ * :151-160).  Rows outside [0, cache_rows) are skipped. */
+int qd_latent_kv_write(const void* latent, const void* rope, void* cache, const int64_t* slots, int64_t tokens,
+                       int latent_dim, int rope_dim, int64_t cache_rows, int dtype, void* stream);
+
+/* Reference checks in order, messages included (mla.cu:139-142). */
+int qd_mla_project_validate(const qd_tensor_desc* x, const qd_tensor_desc* w, int absorb, char* msg,
+                            size_t msg_cap);
+
+/* Per-head projection over rows = batch*q_len (mla.cu:16-27, :138-150):
+ *   absorb != 0: out[r,h,o] = sum_k x[r,h,k] * w[h,k,o]  (w [H, in, out])
+ *   absorb == 0: out[r,h,o] = sum_k x[r,h,k] * w[h,o,k]  (w [H, out, in])
+ * fp32 accumulation, output rounded to the dtype. */
+int qd_mla_project(const void* x, const void* w, void* out, int64_t rows, int heads, int in_dim, int out_dim,
+                   int absorb, int dtype, int flags, void* stream);
+
+/* Reference checks of mla_attend in order, messages included
+ * (mla.cu:162-171); `indices` may be NULL or undefined. */
+int qd_mla_attend_validate(const qd_tensor_desc* q, const qd_tensor_desc* q_rope, const qd_tensor_desc* cache,
+                           const qd_tensor_desc* table, const qd_tensor_desc* lengths,
+                           const qd_tensor_desc* positions, const qd_tensor_desc* indices, double scale,
+                           char* msg, size_t msg_cap);
+
+/* Bytes of float32 split partials qd_mla_attend needs (0 for one split). */
+size_t qd_mla_attend_workspace_bytes(int batch, int q_len, int heads, int latent_dim, int rope_dim,
+                                     int block_size, int max_pages, int num_indices, int dtype, int splits,
+                                     int flags);
+
+/* The plan qd_mla_attend would use: returns 1 for the MFMA kernel (with
+ * *head_groups workgroups per query row and split), 0 for the VALU kernel,
+ * -1 for invalid shapes; *out_splits gets the split count. */
+int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope_dim, int block_size,
+                       int max_pages, int num_indices, int dtype, int splits, int flags, int* out_splits,
+                       int* head_groups);
+
+/* Paged latent attention (mla.cu:34-82, :161-181): out [batch, q_len,
+ * heads, latent_dim] = softmax((q . c + q_rope . k_rope) * scale) . c. */
+int qd_mla_attend(const void* q, const void* q_rope, const void* cache, const int32_t* block_table,
+                  const int32_t* lengths, const int32_t* positions, const int32_t* indices, void* out,
+                  void* workspace, size_t workspace_bytes, int batch, int q_len, int heads, int latent_dim,
+                  int rope_dim, int block_size, int max_pages, int64_t num_blocks, int num_indices, int causal,
+                  int dtype, float scale, int splits, int flags, void* stream);
+
+/* Reference checks of mla_decode_fused in order, messages included
+ * (mla.cu:185-191). */
+int qd_mla_decode_validate(const qd_tensor_desc* q_nope, const qd_tensor_desc* q_rope, const qd_tensor_desc* cache,
+                           const qd_tensor_desc* table, const qd_tensor_desc* lengths,
+                           const qd_tensor_desc* positions, const qd_tensor_desc* w_uk, const qd_tensor_desc* w_uv,
+                           const qd_tensor_desc* indices, double scale, char* msg, size_t msg_cap);
+
+/* Workspace bytes of qd_mla_decode (absorbed query, latent output and
+ * split partials); 16-byte aligned device memory, no zeroing needed. */
+size_t qd_mla_decode_workspace_bytes(int batch, int q_len, int heads, int latent_dim, int rope_dim,
+                                     int block_size, int max_pages, int num_indices, int dtype, int splits,
+                                     int flags);
+
+/* Absorbed paged MLA decode (mla.cu:86-134, :184-198): query absorption,
+ * latent attention and value projection, with the reference's rounding
+ * points (absorbed query and latent output rounded to the dtype).
+ * out [batch, q_len, heads, value_dim]. */
+int qd_mla_decode(const void* q_nope, const void* q_rope, const void* cache, const int32_t* block_table,
+                  const int32_t* lengths, const int32_t* positions, const void* w_uk, const void* w_uv,
+                  const int32_t* indices, void* out, void* workspace, size_t workspace_bytes, int batch, int q_len,
+                  int heads, int nope_dim, int latent_dim, int rope_dim, int value_dim, int block_size,
+                  int max_pages, int64_t num_blocks, int num_indices, int causal, int dtype, float scale,
+                  int splits, int flags, void* stream);
 
 #ifdef __cplusplus
 }
