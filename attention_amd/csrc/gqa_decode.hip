@@ -115,10 +115,6 @@ __device__ __forceinline__ int clamp_page(int32_t phys, int64_t num_blocks) {
   return phys;
 }
 
-__device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-  return x;
-}
 
 // Partials exchanged between workgroups inside one kernel are written and
 // read with agent-scope relaxed atomic accesses (the sc1 cache policy):
@@ -145,14 +141,6 @@ __device__ __forceinline__ f32x2 load_agent2(const float* p) {  // p 8-byte alig
 }
 
 // Inclusive prefix sum over the 64 lanes.
-__device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t x, int lane) {
-  for (int off = 1; off < 64; off <<= 1) {
-    const int64_t t = __shfl_up(x, off);
-    if (lane >= off) x += t;
-  }
-  return x;
-}
-
 // ----------------------------------------------------------------------------
 // Portable VALU kernel
 // ----------------------------------------------------------------------------

@@ -110,82 +110,93 @@ struct ProjParams {
   int H, di, dout;
 };
 
-// grid (ceil(dout/128), H), block 256.  The workgroup owns 128 output
-// columns of one head for all rows; its 4 waves split the k range (k chunks
-// of 32, chunk c on wave c % 4) and their partial tiles are summed in LDS.
-// A wave covers 64 rows x 128 columns: 4 row tiles x 8 column tiles of
-// v_mfma_f32_16x16x32, column tile e holding columns base + 8*(l%16) + e,
+// grid (ceil(dout/128), H, ceil(rows/64)), block 256.  The workgroup owns
+// 128 output columns of one head for 64 rows; its 4 waves split the k range
+// (pairs of 32-wide chunks: wave v takes chunks 2v, 2v+1, 2v+8, 2v+9, ...,
+// all loads of a pair in flight together) and their partial tiles are summed
+// in LDS.  A wave covers 64 rows x 128 columns: 4 row tiles x 8 column tiles
+// of v_mfma_f32_16x16x32, column tile e holding columns base + 8*(l%16) + e,
 // so the absorb layout (columns contiguous in memory) is turned into the B
 // operand by an 8x8 in-register transpose and the value layout (k
-// contiguous) is loaded as is.  Row groups of 64 are processed in turn, so
-// a head's weights come from HBM once and from cache afterwards.
+// contiguous) is loaded as is.
 template <int DT, bool ABSORB>
 __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   using E = Elem<DT>;
   using Ops = MfmaOps<DT>;
   using S = typename E::S;
+  constexpr int kPair = 2;
   __shared__ f32x4 red[4][8][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r16 = lane & 15, q4 = lane >> 4;
   const int h = blockIdx.y;
   const int cbase = 128 * blockIdx.x;
+  const int64_t r0 = 64 * static_cast<int64_t>(blockIdx.z);
   const int col = min(cbase + 8 * r16, p.dout - 8);  // clamped load column
   const int nch = p.di / 32;
   const char* xb = static_cast<const char*>(p.x);
   const char* wb = static_cast<const char*>(p.w);
   S* out = static_cast<S*>(p.out);
-  for (int64_t r0 = 0; r0 < p.rows; r0 += 64) {
-    f32x4 acc[4][8];
+  f32x4 acc[4][8];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+  for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[rt][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int c = wv; c < nch; c += 4) {
+    for (int e = 0; e < 8; ++e) acc[rt][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = kPair * wv; c0 < nch; c0 += 4 * kPair) {
+    u32x4 bop[kPair][8], a[kPair][4];
+#pragma unroll
+    for (int u = 0; u < kPair; ++u) {
+      const int c = min(c0 + u, nch - 1);  // a missing second chunk repeats the first, weight 0 below
       const int k0 = 32 * c + 8 * q4;
-      u32x4 bop[8];
       if constexpr (ABSORB) {
         u32x4 raw[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t)
           raw[t] = *reinterpret_cast<const u32x4*>(
               wb + ((static_cast<int64_t>(h) * p.di + k0 + t) * p.dout + col) * 2);
-        transpose8x8_b16(raw, bop);
+        transpose8x8_b16(raw, bop[u]);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          bop[e] = *reinterpret_cast<const u32x4*>(
+          bop[u][e] = *reinterpret_cast<const u32x4*>(
               wb + ((static_cast<int64_t>(h) * p.dout + col + e) * p.di + k0) * 2);
       }
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
         int64_t row = r0 + 16 * rt + r16;
         if (row >= p.rows) row = p.rows - 1;
-        const u32x4 a =
-            *reinterpret_cast<const u32x4*>(xb + ((row * p.H + h) * p.di + k0) * 2);
+        a[u][rt] = *reinterpret_cast<const u32x4*>(xb + ((row * p.H + h) * p.di + k0) * 2);
+      }
+      if (c0 + u >= nch) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[rt][e] = Ops::mma32(a, bop[e], acc[rt][e]);
+        for (int rt = 0; rt < 4; ++rt) a[u][rt] = u32x4{0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
+    for (int u = 0; u < kPair; ++u)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red[wv][e][lane] = acc[rt][e];
-      __syncthreads();
+      for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int ee = 0; ee < 2; ++ee) {
-        const int e = 2 * wv + ee;
-        const f32x4 s = red[0][e][lane] + red[1][e][lane] + red[2][e][lane] + red[3][e][lane];
-        const int ocol = cbase + 8 * r16 + e;
-        if (ocol < p.dout) {
+        for (int e = 0; e < 8; ++e) acc[rt][e] = Ops::mma32(a[u][rt], bop[u][e], acc[rt][e]);
+  }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int64_t row = r0 + 16 * rt + 4 * q4 + i;
-            if (row < p.rows) out[(row * p.H + h) * p.dout + ocol] = E::from_f(s[i]);
-          }
+  for (int rt = 0; rt < 4; ++rt) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[wv][e][lane] = acc[rt][e];
+    __syncthreads();
+#pragma unroll
+    for (int ee = 0; ee < 2; ++ee) {
+      const int e = 2 * wv + ee;
+      const f32x4 s = red[0][e][lane] + red[1][e][lane] + red[2][e][lane] + red[3][e][lane];
+      const int ocol = cbase + 8 * r16 + e;
+      if (ocol < p.dout) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t row = r0 + 16 * rt + 4 * q4 + i;
+          if (row < p.rows) out[(row * p.H + h) * p.dout + ocol] = E::from_f(s[i]);
         }
       }
-      __syncthreads();
     }
+    __syncthreads();
   }
 }
 
@@ -223,16 +234,19 @@ struct MlaParams {
   const int32_t* lens;
   const int32_t* pos;  // [R]
   const int32_t* idx;  // [R, nk] when nk >= 0
-  void* out;           // [R, H, Dc] (splits == 1)
-  float* part;         // [R, H, splits, Dc + 2] (splits > 1)
+  void* out;           // [R, H, Dc]
+  float* part;         // VALU kernel: [R, H, splits, Dc + 2] (splits > 1);
+                       // MFMA kernel: [wgs + R, H, Dc + 2] stream-K partials
   int B, T, H, Dc, Dr, W, P, maxP;
   int nk;  // indices per row, -1 = all tokens (dense)
   int causal, splits;
-  int head_groups;  // MFMA kernel: workgroups per (row, split)
+  int head_groups;  // MFMA kernel: head groups (workgroups per tile range)
   int kch;          // MFMA kernel: ceil(W / 32)
-  int nt;           // MFMA kernel: nontemporal cache loads
+  int nht, ds;      // MFMA kernel: head tiles per workgroup, latent slices per head tile
+  int wgs;          // MFMA kernel: workgroups per head group (stream-K ranges)
+  int* meta;        // MFMA kernel: [rows][2] {first workgroup, workgroups} per row
+  int64_t* gtotal;  // MFMA kernel: tiles G of the batch (merge: skips empty ranges)
   int64_t num_blocks;
-  int64_t units;    // rows * splits
   float sl2;        // scale * log2(e)
 };
 
@@ -281,6 +295,15 @@ __device__ __forceinline__ float max_over_lane_groups(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Sum over the same 4 lanes; every lane gets the same bits (each step adds
+// a pair, and the pair's order does not change a sum).
+__device__ __forceinline__ float sum_over_lane_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // LDS-only workgroup barrier for the DMA pipeline: waits for this wave's LDS
 // operations and for all but `kVm` of its vector-memory loads (LDS DMA
 // included), then s_barrier.  __syncthreads() would wait for every
@@ -296,52 +319,89 @@ __device__ __forceinline__ void dma_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its outstanding loads (the DMA ring keeps flowing).
+__device__ __forceinline__ void lds_barrier() {
+  constexpr int imm = 0x3F | (0x3 << 14) | (0x7 << 4) | (0x0 << 8);  // vmcnt max, lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(imm);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Tile ring depth for CPT DMA instructions per thread per tile (CPT * 4 KB
 // per tile buffer), within 160 KB of LDS.
 constexpr int ring_depth(int cpt) { return cpt <= 9 ? 4 : 3; }
-constexpr int kOffSlotsDma = 6;  // ring depth + 2
+constexpr int kOffSlotsDma = 6;  // per-tile metadata slots (ring depth + 2)
 constexpr int kWinPages = 256;    // page-table window (dense rows)
+constexpr int kDmaWaves = 4;      // waves 0..3 issue the tile DMA
+constexpr int kFlagFirst = 1;     // first tile of a row segment in this workgroup
+constexpr int kFlagLast = 2;      // last tile of a row segment in this workgroup
+constexpr int kFlagWhole = 4;     // (with kFlagLast) the segment is the whole row
 
 __host__ __device__ constexpr size_t mla_mfma_lds_bytes(int cpt) {
-  return static_cast<size_t>(ring_depth(cpt)) * cpt * 4096 + kOffSlotsDma * kTileTokens * 8 + kOffSlotsDma * 4 +
-         kWinPages * 4 + 1024;
+  return static_cast<size_t>(ring_depth(cpt)) * cpt * 4096  // tile ring
+         + kOffSlotsDma * kTileTokens * 8                      // row offsets
+         + kOffSlotsDma * 8                                    // tile rows
+         + kOffSlotsDma * 4 * 2                                // masks, flags
+         + kWinPages * 4                                       // page window
+         + 32                                                  // prologue results
+         + kAttendThreads * 32                                 // score exchange
+         + 1024;                                               // slack
 }
 
-// MFMA kernel.  grid = ceil(units/8)*8*head_groups workgroups of 256
-// threads; workgroup L serves unit ((L/8)/hg)*8 + L%8 and head group
-// (L/8)%hg, so the head groups of one (row, split) - which read the same
-// cache rows - run on the same XCD and share its L2.
+// Tiles of 32 listed tokens of query row r (dense: the visible prefix).
+__device__ __forceinline__ int row_tiles(const MlaParams& p, int64_t r) {
+  const int count = p.nk >= 0 ? p.nk : row_end(p, static_cast<int>(r / p.T), r);
+  return (count + kTileTokens - 1) / kTileTokens;
+}
+
+// MFMA kernel, stream-K.  The (query row, 32-token tile) space of the batch
+// (G tiles) is cut into p.wgs equal ranges; workgroup w of head group g
+// processes tiles [w*G/wgs, (w+1)*G/wgs) for heads 16*nht*g .. +16*nht.  A
+// row whose tiles all fall in one workgroup is written directly; a row split
+// across workgroups leaves {m, l, acc} partials in slot (w + row) and the
+// merge kernel folds them, guided by meta[row] = {first workgroup, count}
+// written by the workgroup holding the row's first tile.  Grid:
+// ceil(wgs/8)*8*head_groups; workgroup L serves w = ((L/8)/hg)*8 + L%8 and
+// head group (L/8)%hg, so the head groups of one tile range (same cache rows)
+// run on one XCD and share its L2.
 //
-// Waves: wave w of head group g owns heads 16*(4g+w) .. +15; waves without
-// heads only help load.  Per 32-token tile:
-//   load     direct global->LDS DMA (global_load_lds_dwordx4, 1 KB per wave
-//            instruction, CPT per thread) into a ring of ring_depth(CPT)
-//            tile buffers, ring_depth - 1 tiles ahead; no registers hold the
-//            stream.  Rows are unpadded (2W bytes); when W/8 is a multiple
-//            of 8, 16-byte column c of row r is stored at c ^ (r & 7) so the
-//            MFMA operand reads spread over the banks.  Row offsets come
-//            from wave 0, ring_depth tiles ahead, through a page-table
-//            window in LDS (dense rows) or the index list (sparse rows).
-//            A token that is not visible is loaded as a duplicate of a
-//            visible row of its tile (finite data) and gets probability 0.
-//   QK       lane (r16, q4): A = row r16 (+16), 16-byte column 4c + q4 of
-//            the tile, B = [q | q_rope | 0] of head r16, elements
-//            32c + 8 q4 .. +7 -> S0/S1 lane values: tokens 4 q4 + i and
-//            16 + 4 q4 + i.
-//   softmax  per lane (one head per lane column), reduced over the 4 lane
-//            groups; per-lane partial sums l.
+// Waves: wave v works on head tile v % nht (16 heads) and latent slice
+// v / nht (NBLKW blocks of 128 columns).  Every wave of a head tile computes
+// the same scores (the QK product is cheap next to the stream) and the PV
+// product for its own slice only.  Per 32-token tile:
+//   load     waves 0..3 move the tile's cache rows HBM -> LDS with direct
+//            DMA (global_load_lds_dwordx4, 1 KB per wave instruction, CPT
+//            per thread) into a ring of ring_depth(CPT) buffers, up to
+//            ring_depth - 1 tiles ahead.  Rows are unpadded (2W bytes); when
+//            W/8 is a multiple of 8, 16-byte column c of row r sits at
+//            c ^ (r & 7) so the operand reads spread over the banks.  Wave 0
+//            walks the rows ahead of the ring: per tile it writes the row
+//            offsets (from a page-table window in LDS for dense rows, from
+//            the index list for sparse rows), the visibility mask, the row
+//            and the segment flags.  A token that is not visible is loaded
+//            as a duplicate of a visible row of its tile and gets weight 0.
+//   QK       lane (r16, q4): A = row r16 (+16), 16-byte column 4c + q4,
+//            B = [q | q_rope | 0] of head r16, elements 32c + 8 q4 .. +7
+//            -> S0/S1: tokens 4 q4 + i and 16 + 4 q4 + i.
+//   softmax  per lane (one head per lane column), max over the 4 lane
+//            groups with permlane swaps; the accumulator is rescaled only
+//            when a head's running max rises (wave-uniform branch).
 //   PV       k index 8 q4 + e <-> token 4 q4 + e (e < 4) / 16 + 4 q4 + e - 4,
 //            so B = P^T is the lane's own 8 probabilities; A = C^T for
-//            latent columns 128 blk + 8 r16 + e of those 8 tokens (8 LDS
+//            latent columns 128 blk + 8 r16 + e of those tokens (8 LDS
 //            reads + 8x8 transpose); C tile (blk, e) row r <-> column
-//            128 blk + 8 r + e, i.e. lane rows 4 q4 + i hold columns
-//            128 blk + 32 q4 + 8 i + e: 32 contiguous columns per lane.
-template <int DT, int NBLK, int CPT>
+//            128 blk + 8 r + e: lane rows 4 q4 + i hold the 32 contiguous
+//            columns 128 blk + 32 q4 .. +31.
+template <int DT, int DS, int CPT>
 __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaParams p) {
   using E = Elem<DT>;
   using Ops = MfmaOps<DT>;
   using S = typename E::S;
-  constexpr int KMAX = 2 * CPT;  // W <= 64 CPT  ->  ceil(W/32) <= 2 CPT
+  constexpr int KMAX = 2 * CPT;            // W <= 64 CPT  ->  ceil(W/32) <= 2 CPT
+  constexpr int NBLKW = 4 / DS;            // latent blocks of 128 columns per wave
+  constexpr int QCH = (KMAX + DS - 1) / DS;  // query chunks per wave (c = slice + DS i)
   constexpr int kRing = ring_depth(CPT);
   constexpr int kTileBytes = CPT * 4096;
   extern __shared__ __align__(16) char smem[];
@@ -349,91 +409,143 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int r16 = lane & 15, q4 = lane >> 4;
 
-  const int64_t L = blockIdx.x;
-  const int64_t slot = L >> 3;
-  const int64_t unit = (slot / p.head_groups) * 8 + (L & 7);
-  const int hg = static_cast<int>(slot % p.head_groups);
-  if (unit >= p.units) return;  // whole workgroup: uniform
-  const int64_t r = unit / p.splits;
-  const int s = static_cast<int>(unit % p.splits);
-  const int b = static_cast<int>(r / p.T);
-
-  const int end = row_end(p, b, r);
-  const bool sparse = p.nk >= 0;
-  const int count = sparse ? p.nk : end;
-  int i0, i1;
-  split_range(count, s, p.splits, i0, i1);
-  const int ntiles = (i1 - i0 + kTileTokens - 1) / kTileTokens;
+  const int L = blockIdx.x;
+  const int hg = (L >> 3) % p.head_groups;
+  const int w = ((L >> 3) / p.head_groups) * 8 + (L & 7);
+  if (w >= p.wgs) return;  // whole workgroup: uniform
 
   char* ring = smem;
-  int64_t* offs = reinterpret_cast<int64_t*>(smem + kRing * kTileBytes);  // [kOffSlotsDma][32]
-  uint32_t* masks = reinterpret_cast<uint32_t*>(offs + kOffSlotsDma * kTileTokens);
-  int32_t* win = reinterpret_cast<int32_t*>(masks + kOffSlotsDma);          // [kWinPages]
+  int64_t* offs = reinterpret_cast<int64_t*>(smem + kRing * kTileBytes);  // [slots][32]
+  int64_t* tile_row = offs + kOffSlotsDma * kTileTokens;                   // [slots]
+  uint32_t* masks = reinterpret_cast<uint32_t*>(tile_row + kOffSlotsDma);  // [slots]
+  int* flags = reinterpret_cast<int*>(masks + kOffSlotsDma);               // [slots]
+  int32_t* win = flags + kOffSlotsDma;                                     // [kWinPages]
+  int64_t* scal = reinterpret_cast<int64_t*>(win + kWinPages);             // {G, row0, tir0}
+  f32x4* sx = reinterpret_cast<f32x4*>(scal + 4);                           // [waves][64][2] partial scores
 
-  const int h0 = 16 * (4 * hg + wv);
-  const bool active = h0 < p.H;
+  const int64_t rows = static_cast<int64_t>(p.B) * p.T;
+  const bool sparse = p.nk >= 0;
+  const int nblk = (p.Dc + 127) / 128;
+
+  // Wave roles.
+  const int ht = wv % p.nht, slice = wv / p.nht;
+  const int h0 = 16 * (p.nht * hg + ht);
+  const bool active = wv < p.nht * DS && h0 < p.H;
   const int h = h0 + r16;
   const bool head_ok = h < p.H;
-  const int kch = p.kch;
-  const int w8 = p.W / 8;
-  const int swz = (w8 & 7) == 0 ? 7 : 0;
+  const int blk0 = slice * NBLKW;
 
-  // Query operand [q | q_rope | 0] of head h, chunks of 32 elements.
-  u32x4 qv[KMAX];
-  {
-    const S* qrow = static_cast<const S*>(p.q) + (r * p.H + (head_ok ? h : 0)) * p.Dc;
-    const S* rrow = static_cast<const S*>(p.qr) + (r * p.H + (head_ok ? h : 0)) * p.Dr;
-#pragma unroll
-    for (int c = 0; c < KMAX; ++c) {
-      uint32_t w[4] = {0u, 0u, 0u, 0u};
-      if (c < kch && head_ok && active) {
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const int k = 32 * c + 8 * q4 + e;
-          float x0 = 0.f, x1 = 0.f;
-          if (k < p.Dc) x0 = E::to_f(qrow[k]);
-          else if (k < p.W) x0 = E::to_f(rrow[k - p.Dc]);
-          if (k + 1 < p.Dc) x1 = E::to_f(qrow[k + 1]);
-          else if (k + 1 < p.W) x1 = E::to_f(rrow[k + 1 - p.Dc]);
-          w[e / 2] = Ops::pack2(x0, x1);
-        }
+  // Prologue (wave 0): total tiles G and the (row, tile) where this
+  // workgroup's range starts.
+  if (wv == 0) {
+    int64_t G = 0;
+    for (int64_t base = 0; base < rows; base += 64) {
+      const int64_t r = base + lane;
+      G += wave_sum_i64(r < rows ? row_tiles(p, r) : 0);
+    }
+    const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
+    int64_t carry = 0, row0 = 0, tir0 = 0;
+    for (int64_t base = 0; base < rows; base += 64) {
+      const int64_t r = base + lane;
+      const int64_t n = r < rows ? row_tiles(p, r) : 0;
+      const int64_t incl = carry + wave_incl_scan_i64(n, lane);
+      const uint64_t hit = __ballot(r < rows && incl > g0);
+      if (hit) {
+        const int f = __builtin_ctzll(hit);
+        row0 = base + f;
+        tir0 = g0 - (__shfl(incl, f) - __shfl(n, f));
+        break;
       }
-      qv[c] = u32x4{w[0], w[1], w[2], w[3]};
+      carry = __shfl(incl, 63);
+    }
+    if (lane == 0) {
+      scal[0] = G;
+      scal[1] = row0;
+      scal[2] = tir0;
+      if (w == 0 && hg == 0) *p.gtotal = G;
+    }
+  }
+  __syncthreads();
+  const int64_t G = scal[0];
+  const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
+  const int ntiles = static_cast<int>(static_cast<int64_t>(w + 1) * G / p.wgs - g0);
+
+  // Rows with no tile: zeros from workgroup (row % wgs), meta {0, 0}.
+  for (int64_t r = w; r < rows; r += p.wgs) {
+    if (row_tiles(p, r) != 0) continue;
+    if (active && head_ok) {
+      S* orow = static_cast<S*>(p.out) + (r * p.H + h) * p.Dc;
+#pragma unroll
+      for (int bb = 0; bb < NBLKW; ++bb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int dc0 = 128 * (blk0 + bb) + 32 * q4 + 8 * i;
+          if (blk0 + bb < nblk && dc0 < p.Dc) *reinterpret_cast<u32x4*>(orow + dc0) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    if (hg == 0 && threadIdx.x == 0) {
+      p.meta[2 * r] = 0;
+      p.meta[2 * r + 1] = 0;
     }
   }
 
-  // This thread's DMA work: LDS chunk k*256 + tid of a tile is row-major
-  // (row, c) = divmod(., W/8) and holds global column c ^ (row & swz);
-  // chunks past the 32 rows are fillers that reread a chunk of row 0.
-  const int total_chunks = kTileTokens * w8;
-  const int row0 = static_cast<int>(threadIdx.x) / w8, col0 = static_cast<int>(threadIdx.x) % w8;
-  const int step_rows = kAttendThreads / w8, step_cols = kAttendThreads % w8;
+  const int kch = p.kch;
+  (void)kch;
+  const int w8 = p.W / 8;
+  const int swz = (w8 & 7) == 0 ? 7 : 0;
   const char* cache = static_cast<const char*>(p.cache);
 
-  int win_base = -kWinPages;  // wave 0 only: first page held in `win`
+  // This thread's DMA work (waves 0..3): LDS chunk k*256 + tid of a tile is
+  // row-major (row, c) = divmod(., W/8) and holds global column
+  // c ^ (row & swz); chunks past the 32 rows are fillers that reread row 0.
+  const int total_chunks = kTileTokens * w8;
+  const int dtid = static_cast<int>(threadIdx.x) & 255;
+  const int row0d = dtid / w8, col0d = dtid % w8;
+  const int step_rows = 256 / w8, step_cols = 256 % w8;
+
+  // Wave 0's cursor over the workgroup's tiles.
+  int64_t cur_row = scal[1];
+  int cur_tir = static_cast<int>(scal[2]);
+  int cur_n = 0, cur_end = 0, cur_b = 0, seg_tir = cur_tir;
+  int64_t g_cur = g0;
+  int win_base = -kWinPages;
+  auto enter_row = [&]() {
+    cur_b = static_cast<int>(cur_row / p.T);
+    cur_end = row_end(p, cur_b, cur_row);
+    cur_n = row_tiles(p, cur_row);
+    win_base = -kWinPages;  // window belongs to one sequence
+  };
   auto load_window = [&](int first) {
     for (int i = lane; i < kWinPages; i += 64) {
       const int pg = first + i;
-      win[i] = pg < p.maxP ? p.table[static_cast<int64_t>(b) * p.maxP + pg] : 0;
+      win[i] = pg < p.maxP ? p.table[static_cast<int64_t>(cur_b) * p.maxP + pg] : 0;
     }
     win_base = first;
   };
-  // wave 0: offsets (elements) and visibility of tile t into slot t % kOffSlotsDma.
+  // wave 0: metadata of the workgroup's tile t (called for t = 0, 1, ...).
   auto compute_offsets = [&](int t) {
-    const int i = i0 + kTileTokens * t + lane;
-    bool valid = lane < kTileTokens && i < i1;
-    int tok = i;
-    if (sparse) {
-      tok = valid ? p.idx[r * p.nk + i] : -1;
-      valid = valid && tok >= 0 && tok < end;
+    int fl = 0;
+    if (t == 0 || cur_tir == 0) {
+      fl |= kFlagFirst;
+      seg_tir = cur_tir;
     }
+    if (t == ntiles - 1 || cur_tir == cur_n - 1) {
+      fl |= kFlagLast;
+      if (seg_tir == 0 && cur_tir == cur_n - 1) fl |= kFlagWhole;
+    }
+    const int count = sparse ? p.nk : cur_end;
+    const int i = kTileTokens * cur_tir + lane;
+    bool valid = lane < kTileTokens && i < count;
+    int tok = i;
     int32_t phys = 0;
     if (sparse) {
-      if (valid) phys = p.table[static_cast<int64_t>(b) * p.maxP + tok / p.P];
+      tok = valid ? p.idx[cur_row * p.nk + i] : -1;
+      valid = valid && tok >= 0 && tok < cur_end;
+      if (valid) phys = p.table[static_cast<int64_t>(cur_b) * p.maxP + tok / p.P];
     } else {
-      const int first = (i0 + kTileTokens * t) / p.P;
-      const int last = (min(i0 + kTileTokens * t + kTileTokens, i1) - 1) / p.P;
-      if (last >= win_base + kWinPages) load_window(first);
+      const int first = (kTileTokens * cur_tir) / p.P;
+      const int last = (min(kTileTokens * cur_tir + kTileTokens, count) - 1) / p.P;
+      if (first < win_base || last >= win_base + kWinPages) load_window(first);
       if (valid) phys = win[tok / p.P - win_base];
     }
     if (phys < 0) phys = 0;
@@ -444,17 +556,36 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
     const int64_t dummy = __shfl(off, fv);
     const int sl = t % kOffSlotsDma;
     if (lane < kTileTokens) offs[sl * kTileTokens + lane] = valid ? off : dummy;
-    if (lane == 0) masks[sl] = mask;
+    if (lane == 0) {
+      masks[sl] = mask;
+      flags[sl] = fl;
+      tile_row[sl] = cur_row;
+      if (cur_tir == 0 && hg == 0) {
+        // This workgroup holds the row's first tile: record its span.
+        const int64_t last_g = g_cur + cur_n - 1;
+        const int64_t last_w = ((last_g + 1) * p.wgs - 1) / G;
+        p.meta[2 * cur_row] = w;
+        p.meta[2 * cur_row + 1] = static_cast<int>(last_w - w + 1);
+      }
+    }
+    ++g_cur;
+    ++cur_tir;
+    if (cur_tir == cur_n && t + 1 < ntiles) {
+      do {
+        ++cur_row;
+      } while (row_tiles(p, cur_row) == 0);
+      cur_tir = 0;
+      enter_row();
+    }
   };
   auto issue_dma = [&](int t) {
     char* buf = ring + (t % kRing) * kTileBytes;
     const int64_t* o = offs + (t % kOffSlotsDma) * kTileTokens;
-    // All sources first (one LDS round trip), then the DMA instructions.
     const char* src[CPT];
-    int row = row0, col = col0;
+    int row = row0d, col = col0d;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const bool real = static_cast<int>(threadIdx.x) + k * kAttendThreads < total_chunks;
+      const bool real = dtid + k * 256 < total_chunks;
       src[k] = cache + 2 * o[real ? row : 0] + (real ? 16 * (col ^ (row & swz)) : 0);
       row += step_rows;
       col += step_cols;
@@ -470,49 +601,102 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
                                        0, 0);
   };
 
+  // Query operand [q | q_rope | 0] of head h, chunks of 32 elements: Dc and
+  // Dr are multiples of 8, so each lane's 8-element group lies in q, in
+  // q_rope or past W (zero) and is one 16-byte load.
+  u32x4 qv[QCH];
+  auto load_query = [&](int64_t r) {
+    const char* qrow = static_cast<const char*>(p.q) + (r * p.H + (head_ok ? h : 0)) * p.Dc * 2;
+    const char* rrow = static_cast<const char*>(p.qr) + (r * p.H + (head_ok ? h : 0)) * p.Dr * 2;
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) {
+      const int c = slice + DS * i;
+      const int k = 32 * c + 8 * q4;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (head_ok && k < p.Dc) v = *reinterpret_cast<const u32x4*>(qrow + 2 * k);
+      else if (head_ok && k < p.W) v = *reinterpret_cast<const u32x4*>(rrow + 2 * (k - p.Dc));
+      qv[i] = v;
+    }
+  };
+
   float m_run = -INFINITY, l_run = 0.f;
-  f32x4 acc[NBLK][8];
-#pragma unroll
-  for (int blk = 0; blk < NBLK; ++blk)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[blk][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[NBLKW][8];
 
   if (ntiles > 0) {
     if (wv == 0) {
-      if (!sparse) load_window(i0 / p.P);
+      enter_row();
       for (int t = 0; t < kRing && t < ntiles; ++t) compute_offsets(t);
     }
     __syncthreads();
-    for (int t = 0; t < kRing - 1 && t < ntiles; ++t) issue_dma(t);
+    if (wv < kDmaWaves)
+      for (int t = 0; t < kRing - 1 && t < ntiles; ++t) issue_dma(t);
   }
-  for (int j = 0; j < ntiles; ++j) {
-    // Tile j's DMA done in every wave (tiles j+1 .. j+kRing-2 may fly on),
-    // and every wave is past tile j-1's compute.
-    if (ntiles - 1 - j >= kRing - 2)
-      dma_barrier<(kRing - 2) * CPT>();
-    else
-      dma_barrier<0>();
-    if (j + kRing - 1 < ntiles) issue_dma(j + kRing - 1);  // into tile j-1's buffer
+  // Row segments of this workgroup in order; the tiles of a segment in the
+  // inner loop.  Segment bounds come from the per-tile flags wave 0 wrote
+  // (identical in every wave, so every wave runs the same barriers).
+  for (int j = 0; j < ntiles;) {
+    const int64_t row = tile_row[j % kOffSlotsDma];
     if (active) {
-      const char* buf = ring + (j % kRing) * kTileBytes;
-      const uint32_t mask = masks[j % kOffSlotsDma];
-      if (mask != 0u) {
-        // S^T = C . Qcat^T for tokens 0-15 (s0) and 16-31 (s1), over all
-        // 2*CPT chunks: the query is zero past W, and a chunk past W reads
-        // the next row or the tile's filler chunks (finite cache data,
-        // inside the tile buffer since W/8 <= 8*CPT).  A fixed chunk count
-        // lets the LDS reads run ahead of the MFMAs.
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        const int ra = r16, rb = 16 + r16;
+      load_query(row);
+      m_run = -INFINITY;
+      l_run = 0.f;
 #pragma unroll
-        for (int c = 0; c < KMAX; ++c) {
-          const int c4 = 4 * c + q4;
-          const u32x4 a0 = *reinterpret_cast<const u32x4*>(buf + 16 * (ra * w8 + (c4 ^ (ra & swz))));
-          const u32x4 a1 = *reinterpret_cast<const u32x4*>(buf + 16 * (rb * w8 + (c4 ^ (rb & swz))));
-          s0 = Ops::mma32(a0, qv[c], s0);
-          s1 = Ops::mma32(a1, qv[c], s1);
+      for (int bb = 0; bb < NBLKW; ++bb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[bb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    int fl;
+    do {
+      // Tile j's DMA done in every wave (tiles j+1 .. j+kRing-2 may fly
+      // on), and every wave is past tile j-1's compute.
+      if (ntiles - 1 - j >= kRing - 2)
+        dma_barrier<(kRing - 2) * CPT>();
+      else
+        dma_barrier<0>();
+      if (wv < kDmaWaves && j + kRing - 1 < ntiles) issue_dma(j + kRing - 1);  // into tile j-1's buffer
+      const int sl = j % kOffSlotsDma;
+      fl = flags[sl];
+      const uint32_t mask = masks[sl];
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      if (mask != 0u) {
+        const char* buf = ring + (j % kRing) * kTileBytes;
+        // S^T = C . Qcat^T for tokens 0-15 (s0) and 16-31 (s1).  The DS
+        // waves of a head tile take the 32-element chunks c = slice + DS i
+        // and add their partial scores through LDS (in slice order, so every
+        // wave of the head tile gets the same bits).  All 2*CPT chunks are
+        // covered: the query is zero past W, and a chunk past W reads the
+        // next row or the tile's filler chunks (finite cache data, inside
+        // the tile buffer since W/8 <= 8*CPT).
+        if (active) {
+          const int ra = r16, rb = 16 + r16;
+#pragma unroll
+          for (int i = 0; i < QCH; ++i) {
+            const int c = slice + DS * i;
+            if (KMAX % DS == 0 || c < KMAX) {
+              const int c4 = 4 * c + q4;
+              const u32x4 a0 = *reinterpret_cast<const u32x4*>(buf + 16 * (ra * w8 + (c4 ^ (ra & swz))));
+              const u32x4 a1 = *reinterpret_cast<const u32x4*>(buf + 16 * (rb * w8 + (c4 ^ (rb & swz))));
+              s0 = Ops::mma32(a0, qv[i], s0);
+              s1 = Ops::mma32(a1, qv[i], s1);
+            }
+          }
         }
-
+        if constexpr (DS > 1) {
+          sx[(wv * 64 + lane) * 2] = s0;
+          sx[(wv * 64 + lane) * 2 + 1] = s1;
+          lds_barrier();
+          s0 = f32x4{0.f, 0.f, 0.f, 0.f};
+          s1 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int sl2 = 0; sl2 < DS; ++sl2) {
+            const int src = ht + p.nht * sl2;
+            s0 += sx[(src * 64 + lane) * 2];
+            s1 += sx[(src * 64 + lane) * 2 + 1];
+          }
+        }
+      }
+      if (active && mask != 0u) {
+        const char* buf = ring + (j % kRing) * kTileBytes;
         // Online softmax in log2 units.  The accumulator is rescaled only on
         // tiles that raise some head's running max (a wave-uniform branch;
         // rare once the max has been seen), so every probability is <= 1 and
@@ -533,9 +717,9 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
           m_run = move ? mx : m_run;
           l_run *= alpha;
 #pragma unroll
-          for (int blk = 0; blk < NBLK; ++blk)
+          for (int bb = 0; bb < NBLKW; ++bb)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[blk][e] *= alpha;
+            for (int e = 0; e < 8; ++e) acc[bb][e] *= alpha;
         }
         // The denominator sums the same 16-bit probabilities the PV product
         // uses, so the output is an exactly normalized average of values.
@@ -547,60 +731,147 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
                           Ops::pack2(pr[6], pr[7])};
         l_run += (Ops::sum2(pb[0]) + Ops::sum2(pb[1])) + (Ops::sum2(pb[2]) + Ops::sum2(pb[3]));
 
-        // O^T += C[:, :Dc]^T . P^T
+        // O^T += C[:, slice]^T . P^T
 #pragma unroll
-        for (int blk = 0; blk < NBLK; ++blk) {
-          const int cc = min(16 * blk + r16, p.Dc / 8 - 1);
-          u32x4 raw[8];
+        for (int bb = 0; bb < NBLKW; ++bb) {
+          if (blk0 + bb < nblk) {
+            const int cc = min(16 * (blk0 + bb) + r16, p.Dc / 8 - 1);
+            u32x4 raw[8];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const int tok = t < 4 ? 4 * q4 + t : 16 + 4 * q4 + (t - 4);
-            raw[t] = *reinterpret_cast<const u32x4*>(buf + 16 * (tok * w8 + (cc ^ (tok & swz))));
+            for (int t = 0; t < 8; ++t) {
+              const int tok = t < 4 ? 4 * q4 + t : 16 + 4 * q4 + (t - 4);
+              raw[t] = *reinterpret_cast<const u32x4*>(buf + 16 * (tok * w8 + (cc ^ (tok & swz))));
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              acc[bb][e] = Ops::mma32(transpose8x8_col_b16(raw, e), pb, acc[bb][e]);
           }
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            acc[blk][e] = Ops::mma32(transpose8x8_col_b16(raw, e), pb, acc[blk][e]);
         }
       }
-    }
-    if (wv == 0 && j + kRing < ntiles) compute_offsets(j + kRing);
-  }
-  if (!active || !head_ok) return;
+      if (wv == 0 && j + kRing < ntiles) compute_offsets(j + kRing);
+      ++j;
+    } while (!(fl & kFlagLast) && j < ntiles);  // tile ntiles-1 always carries kFlagLast
 
-  float l = l_run + __shfl_xor(l_run, 16);
-  l += __shfl_xor(l, 32);
-  if (p.splits == 1) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    S* orow = static_cast<S*>(p.out) + (r * p.H + h) * p.Dc;
+    if (active && head_ok) {
+      const float l = sum_over_lane_groups(l_run);
+      if (fl & kFlagWhole) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        S* orow = static_cast<S*>(p.out) + (row * p.H + h) * p.Dc;
 #pragma unroll
-    for (int blk = 0; blk < NBLK; ++blk)
+        for (int bb = 0; bb < NBLKW; ++bb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int dc0 = 128 * blk + 32 * q4 + 8 * i;
-        if (dc0 < p.Dc) {
-          uint32_t w[4];
+          for (int i = 0; i < 4; ++i) {
+            const int dc0 = 128 * (blk0 + bb) + 32 * q4 + 8 * i;
+            if (blk0 + bb < nblk && dc0 < p.Dc) {
+              uint32_t wd[4];
 #pragma unroll
-          for (int e = 0; e < 8; e += 2)
-            w[e / 2] = Ops::pack2(acc[blk][e][i] * inv, acc[blk][e + 1][i] * inv);
-          *reinterpret_cast<u32x4*>(orow + dc0) = u32x4{w[0], w[1], w[2], w[3]};
+              for (int e = 0; e < 8; e += 2)
+                wd[e / 2] = Ops::pack2(acc[bb][e][i] * inv, acc[bb][e + 1][i] * inv);
+              *reinterpret_cast<u32x4*>(orow + dc0) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+            }
+          }
+      } else {
+        float* pr = p.part + ((w + row) * p.H + h) * static_cast<int64_t>(p.Dc + 2);
+        if (slice == 0 && q4 == 0) {
+          pr[0] = m_run == -INFINITY ? -INFINITY : m_run * kLn2;
+          pr[1] = l;
         }
+#pragma unroll
+        for (int bb = 0; bb < NBLKW; ++bb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int dc0 = 128 * (blk0 + bb) + 32 * q4 + 8 * i;
+            if (blk0 + bb < nblk && dc0 < p.Dc) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) pr[2 + dc0 + e] = acc[bb][e][i];
+            }
+          }
       }
-  } else {
-    float* pr = partial_row(p, r, h, s);
-    if (q4 == 0) {
-      pr[0] = m_run == -INFINITY ? -INFINITY : m_run * kLn2;
-      pr[1] = l;
     }
+  }
+}
+
+// Merge of the stream-K partials: one wave per (row, head) of a row split
+// across workgroups (meta[row] = {first, count >= 2}); the partial of
+// workgroup k is in slot k + row, for the k in [first, first + count) whose
+// tile range is not empty (with fewer tiles than workgroups some are).  The
+// log-sum-exp combine of online_softmax.cuh:17-24 (empty partials skipped,
+// an all-empty row gives zeros) is evaluated in two passes: every partial's
+// {m, l} at once (one per lane), then the weighted sum of the accumulators,
+// four partials' loads in flight at a time.
+template <int DT>
+__global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
+  using E = Elem<DT>;
+  using S = typename E::S;
+  constexpr int kAcc = 8;
+  constexpr int kBatch = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (wid >= static_cast<int64_t>(p.B) * p.T * p.H) return;
+  const int64_t r = wid / p.H;
+  const int h = static_cast<int>(wid % p.H);
+  const int first = p.meta[2 * r], nwg = p.meta[2 * r + 1];
+  if (nwg < 2 || first < 0 || first + nwg > p.wgs) return;  // spans are always inside [0, wgs)
+  const int64_t G = *p.gtotal;
+  const int64_t stride = static_cast<int64_t>(p.H) * (p.Dc + 2);
+  const float* base = p.part + (r * p.H + h) * static_cast<int64_t>(p.Dc + 2);  // slot k: + (k) * stride
+  auto present = [&](int k) {
+    return static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
+  };
+  // Pass 1: M = max m over non-empty partials.
+  float M = -INFINITY;
+  for (int c = 0; c < nwg; c += 64) {
+    const int k = first + c + lane;
+    float m = -INFINITY;
+    if (c + lane < nwg && present(k)) {
+      const float* pr = base + k * stride;
+      if (pr[1] != 0.f) m = pr[0];
+    }
+    M = fmaxf(M, wave_max(m));
+  }
+  // Pass 2: weights e^(m_k - M), L = sum w_k l_k, acc = sum w_k acc_k.
+  float L = 0.f;
+  float acc[kAcc];
 #pragma unroll
-    for (int blk = 0; blk < NBLK; ++blk)
+  for (int j = 0; j < kAcc; ++j) acc[j] = 0.f;
+  for (int c = 0; c < nwg; c += 64) {
+    const int n = min(64, nwg - c);
+    const int k = first + c + lane;
+    float wgt = 0.f, lw = 0.f;
+    if (lane < n && present(k)) {
+      const float* pr = base + k * stride;
+      const float l = pr[1];
+      if (l != 0.f) {
+        wgt = fast_exp2((pr[0] - M) * kLog2e);
+        lw = wgt * l;
+      }
+    }
+    L += wave_sum(lw);
+    for (int t0 = 0; t0 < n; t0 += kBatch) {
+      float v[kBatch][kAcc];
+      float wt[kBatch];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int dc0 = 128 * blk + 32 * q4 + 8 * i;
-        if (dc0 < p.Dc) {
+      for (int t = 0; t < kBatch; ++t) {
+        wt[t] = t0 + t < n ? __shfl(wgt, t0 + t) : 0.f;
+        const float* pr = base + (first + c + min(t0 + t, n - 1)) * stride + 2;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) pr[2 + dc0 + e] = acc[blk][e][i];
+        for (int j = 0; j < kAcc; ++j) {
+          const int d = lane + 64 * j;
+          v[t][j] = (wt[t] != 0.f && d < p.Dc) ? pr[d] : 0.f;
         }
       }
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t)
+#pragma unroll
+        for (int j = 0; j < kAcc; ++j) acc[j] = fmaf(wt[t], v[t][j], acc[j]);
+    }
+  }
+  S* orow = static_cast<S*>(p.out) + wid * p.Dc;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int j = 0; j < kAcc; ++j) {
+    const int d = lane + 64 * j;
+    if (d < p.Dc) orow[d] = E::from_f(acc[j] * inv);
   }
 }
 
@@ -795,14 +1066,15 @@ struct AttendShape {
   int B, T, H, Dc, Dr, P, maxP, nk, dtype;
 };
 
-// Launch plan of the attention: kernel, splits, and the MFMA kernel's
-// instance (latent blocks of 128 columns, DMA chunks per thread per tile).
-// Depends on static shapes and the device only.
+// Launch plan of the attention.  VALU kernel: context splits per row.
+// MFMA kernel: stream-K ranges (workgroups per head group), head tiles per
+// workgroup and latent slices per head tile, DMA chunks per thread.  Depends
+// on static shapes and the device only.
 struct AttendPlan {
   bool mfma;
-  int nblk, cpt, kch, head_groups;
+  int nblk, cpt, kch, head_groups, nht, ds, wgs;
   size_t lds;
-  int splits;
+  int splits;  // VALU kernel
 };
 
 // Smallest instantiated DMA-chunk count covering ceil(W/64), 0 if none.
@@ -813,30 +1085,40 @@ int cpt_for(int W) {
   return 0;
 }
 
-AttendPlan plan_attend(const AttendShape& a, int forced_splits, int flags) {
+AttendPlan plan_attend(const AttendShape& a, int forced, int flags) {
   AttendPlan pl{};
   const int W = a.Dc + a.Dr;
   pl.nblk = (a.Dc + 127) / 128;
   pl.kch = (W + 31) / 32;
   pl.cpt = cpt_for(W);
-  if (pl.cpt == 5 && pl.nblk > 3) pl.cpt = 9;  // (4, 5) is not instantiated
-  if (pl.cpt == 2 && pl.nblk > 1) pl.cpt = 5;
   pl.lds = pl.cpt ? mla_mfma_lds_bytes(pl.cpt) : 0;
   const int ht = (a.H + 15) / 16;
-  pl.head_groups = (ht + 3) / 4;
+  // 4 waves = head tiles x latent slices: one head tile split 4 ways for up
+  // to 16 heads, else 2 head tiles split 2 ways.
+  if (ht == 1) {
+    pl.nht = 1;
+    pl.ds = 4;
+  } else {
+    pl.nht = 2;
+    pl.ds = 2;
+  }
+  pl.head_groups = (ht + pl.nht - 1) / pl.nht;
   pl.mfma = (flags & QD_FLAG_FORCE_GENERIC) == 0 && (a.dtype == QD_DTYPE_F16 || a.dtype == QD_DTYPE_BF16) &&
-            a.Dc % 8 == 0 && a.Dr % 8 == 0 && a.Dc <= 512 && pl.nblk >= 1 && pl.nblk <= 4 && pl.cpt > 0 &&
+            a.Dc % 8 == 0 && a.Dr % 8 == 0 && a.Dc <= 512 && pl.cpt > 0 &&
             pl.lds <= static_cast<size_t>(device_max_lds());
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
-  if (forced_splits > 0) {
-    pl.splits = forced_splits;
+  if (pl.mfma) {
+    // One resident workgroup per CU (the LDS ring), shared by the head groups.
+    pl.wgs = forced > 0 ? forced : std::max(1, device_cus() / pl.head_groups);
+    pl.splits = 1;
+  } else if (forced > 0) {
+    pl.splits = forced;
   } else {
-    // One resident workgroup per CU (the MFMA kernel's LDS ring) or two
-    // (VALU kernel), at least 256 listed tokens per split, at most
-    // kMaxSplits.
+    // Two resident workgroups per CU, at least 256 listed tokens per split,
+    // at most kMaxSplits.
     const int64_t cap = a.nk >= 0 ? a.nk : static_cast<int64_t>(a.maxP) * a.P;
-    const int64_t per_row = pl.mfma ? pl.head_groups : (static_cast<int64_t>(a.H) + 3) / 4;
-    const int64_t target = (pl.mfma ? 1 : 2) * static_cast<int64_t>(device_cus());
+    const int64_t per_row = (static_cast<int64_t>(a.H) + 3) / 4;
+    const int64_t target = 2 * static_cast<int64_t>(device_cus());
     const int64_t want = (target + rows * per_row - 1) / (rows * per_row);
     int64_t sp = std::min<int64_t>(want, std::max<int64_t>(1, cap / 256));
     pl.splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(sp, kMaxSplits)));
@@ -844,14 +1126,23 @@ AttendPlan plan_attend(const AttendShape& a, int forced_splits, int flags) {
   return pl;
 }
 
-size_t attend_partial_bytes(const AttendShape& a, int splits) {
-  if (splits <= 1) return 0;
-  return static_cast<size_t>(a.B) * a.T * a.H * splits * (a.Dc + 2) * sizeof(float);
+size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Workspace of the attention: VALU kernel [R, H, splits, Dc+2] fp32 when
+// splits > 1; MFMA kernel [wgs + R, H, Dc+2] fp32 partials, then the tile
+// count G (int64) and [R][2] int32 row spans.
+size_t attend_partial_bytes(const AttendShape& a, const AttendPlan& pl) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T;
+  if (pl.mfma)
+    return round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * (a.Dc + 2) * sizeof(float)) +
+           round_up256(sizeof(int64_t) + static_cast<size_t>(rows) * 2 * sizeof(int));
+  if (pl.splits <= 1) return 0;
+  return static_cast<size_t>(rows) * a.H * pl.splits * (a.Dc + 2) * sizeof(float);
 }
 
-template <int DT, int NBLK, int CPT>
+template <int DT, int DS, int CPT>
 hipError_t launch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
-  auto fn = mla_attend_mfma_kernel<DT, NBLK, CPT>;
+  auto fn = mla_attend_mfma_kernel<DT, DS, CPT>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&] {
@@ -859,25 +1150,21 @@ hipError_t launch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_
                                static_cast<int>(mla_mfma_lds_bytes(CPT)));
   });
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kAttendThreads), pl.lds, st, prm);
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(64 * pl.nht * pl.ds), pl.lds, st, prm);
   return hipSuccess;
 }
 
 template <int DT>
 hipError_t dispatch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
-  switch (pl.cpt * 8 + pl.nblk) {
-    case 2 * 8 + 1: return launch_attend_mfma<DT, 1, 2>(prm, pl, grid, st);
-    case 5 * 8 + 1: return launch_attend_mfma<DT, 1, 5>(prm, pl, grid, st);
+  switch (pl.cpt * 8 + pl.ds) {
+    case 2 * 8 + 4: return launch_attend_mfma<DT, 4, 2>(prm, pl, grid, st);
+    case 2 * 8 + 2: return launch_attend_mfma<DT, 2, 2>(prm, pl, grid, st);
+    case 5 * 8 + 4: return launch_attend_mfma<DT, 4, 5>(prm, pl, grid, st);
     case 5 * 8 + 2: return launch_attend_mfma<DT, 2, 5>(prm, pl, grid, st);
-    case 5 * 8 + 3: return launch_attend_mfma<DT, 3, 5>(prm, pl, grid, st);
-    case 9 * 8 + 1: return launch_attend_mfma<DT, 1, 9>(prm, pl, grid, st);
-    case 9 * 8 + 2: return launch_attend_mfma<DT, 2, 9>(prm, pl, grid, st);
-    case 9 * 8 + 3: return launch_attend_mfma<DT, 3, 9>(prm, pl, grid, st);
     case 9 * 8 + 4: return launch_attend_mfma<DT, 4, 9>(prm, pl, grid, st);
-    case 10 * 8 + 1: return launch_attend_mfma<DT, 1, 10>(prm, pl, grid, st);
-    case 10 * 8 + 2: return launch_attend_mfma<DT, 2, 10>(prm, pl, grid, st);
-    case 10 * 8 + 3: return launch_attend_mfma<DT, 3, 10>(prm, pl, grid, st);
+    case 9 * 8 + 2: return launch_attend_mfma<DT, 2, 9>(prm, pl, grid, st);
     case 10 * 8 + 4: return launch_attend_mfma<DT, 4, 10>(prm, pl, grid, st);
+    case 10 * 8 + 2: return launch_attend_mfma<DT, 2, 10>(prm, pl, grid, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -909,17 +1196,24 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   prm.splits = pl.splits;
   prm.head_groups = pl.head_groups;
   prm.kch = pl.kch;
-  prm.nt = pl.head_groups == 1 ? 1 : 0;
+  prm.nht = pl.nht;
+  prm.ds = pl.ds;
+  prm.wgs = pl.wgs;
   prm.num_blocks = num_blocks;
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
-  prm.units = rows * pl.splits;
   prm.sl2 = scale * kLog2e;
-  if (pl.splits > 1 && part_bytes < attend_partial_bytes(a, pl.splits))
-    return mla_fail(nullptr, 0, "workspace too small for the split partials");
+  const size_t need = attend_partial_bytes(a, pl);
+  if (need > 0 && (part_bytes < need || !part_ws || !aligned16(part_ws)))
+    return mla_fail(nullptr, 0, "workspace too small for the attention partials");
+  if (pl.mfma) {
+    char* meta = static_cast<char*>(part_ws) + round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * (a.Dc + 2) * 4);
+    prm.gtotal = reinterpret_cast<int64_t*>(meta);
+    prm.meta = reinterpret_cast<int*>(meta + sizeof(int64_t));
+  }
   (void)hipGetLastError();
   hipError_t err = hipSuccess;
   if (pl.mfma) {
-    const int64_t grid = (prm.units + 7) / 8 * 8 * pl.head_groups;
+    const int64_t grid = (static_cast<int64_t>(pl.wgs) + 7) / 8 * 8 * pl.head_groups;
     if (grid > 2147483647LL) return mla_fail(nullptr, 0, "mla_attend grid exceeds launch limits");
     err = a.dtype == QD_DTYPE_BF16 ? dispatch_attend_mfma<QD_DTYPE_BF16>(prm, pl, grid, st)
                                    : dispatch_attend_mfma<QD_DTYPE_F16>(prm, pl, grid, st);
@@ -944,8 +1238,15 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
     return static_cast<int>(err);
   }
   int rc = launch_status("mla_attend");
-  if (rc != QD_OK || pl.splits == 1) return rc;
+  if (rc != QD_OK || (!pl.mfma && pl.splits == 1)) return rc;
   const int64_t mgrid = (rows * a.H + 3) / 4;
+  if (pl.mfma) {
+    if (a.dtype == QD_DTYPE_BF16)
+      hipLaunchKernelGGL(mla_merge_sk_kernel<QD_DTYPE_BF16>, dim3(mgrid), dim3(256), 0, st, prm);
+    else
+      hipLaunchKernelGGL(mla_merge_sk_kernel<QD_DTYPE_F16>, dim3(mgrid), dim3(256), 0, st, prm);
+    return launch_status("mla_attend merge");
+  }
   switch (a.dtype) {
     case QD_DTYPE_F32: hipLaunchKernelGGL(mla_merge_kernel<QD_DTYPE_F32>, dim3(mgrid), dim3(256), 0, st, prm); break;
     case QD_DTYPE_F16: hipLaunchKernelGGL(mla_merge_kernel<QD_DTYPE_F16>, dim3(mgrid), dim3(256), 0, st, prm); break;
@@ -954,16 +1255,17 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   return launch_status("mla_attend merge");
 }
 
-bool project_mfma_applies(int di, int dout, int dtype, const void* x, const void* w, const void* out) {
+bool project_mfma_applies(int64_t rows, int di, int dout, int dtype, const void* x, const void* w,
+                          const void* out) {
   return (dtype == QD_DTYPE_F16 || dtype == QD_DTYPE_BF16) && di % 32 == 0 && dout % 8 == 0 && dout >= 8 &&
-         aligned16(x) && aligned16(w) && aligned16(out);
+         (rows + 63) / 64 <= 65535 && aligned16(x) && aligned16(w) && aligned16(out);  // grid.z limit
 }
 
 template <int DT>
 void launch_project(const ProjParams& prm, bool absorb, bool mfma, hipStream_t st) {
   if constexpr (DT != QD_DTYPE_F32) {
     if (mfma) {
-      const dim3 grid((prm.dout + 127) / 128, prm.H);
+      const dim3 grid((prm.dout + 127) / 128, prm.H, static_cast<unsigned>((prm.rows + 63) / 64));
       if (absorb)
         hipLaunchKernelGGL((mla_project_mfma_kernel<DT, true>), grid, dim3(256), 0, st, prm);
       else
@@ -988,7 +1290,7 @@ int run_project(const void* x, const void* w, void* out, int64_t rows, int H, in
   if (rows == 0) return QD_OK;
   if (!x || !w || !out) return mla_fail(nullptr, 0, "null tensor pointer");
   ProjParams prm{x, w, out, rows, H, di, dout};
-  const bool mfma = (flags & QD_FLAG_FORCE_GENERIC) == 0 && project_mfma_applies(di, dout, dtype, x, w, out);
+  const bool mfma = (flags & QD_FLAG_FORCE_GENERIC) == 0 && project_mfma_applies(rows, di, dout, dtype, x, w, out);
   if (!mfma && (rows * H * static_cast<int64_t>(dout) + 255) / 256 > 2147483647LL)
     return mla_fail(nullptr, 0, "mla_project grid exceeds launch limits");
   (void)hipGetLastError();
@@ -1000,21 +1302,19 @@ int run_project(const void* x, const void* w, void* out, int64_t rows, int H, in
   return launch_status("mla_project");
 }
 
-size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
-
 // Workspace of the fused decode: absorbed query and latent output
 // ([R, H, Dc] of the dtype each), then the split partials.
 struct DecodeLayout {
   size_t qa, latent, part, total;
 };
 
-DecodeLayout decode_layout(const AttendShape& a, int splits) {
+DecodeLayout decode_layout(const AttendShape& a, const AttendPlan& pl) {
   DecodeLayout d{};
   const size_t n = static_cast<size_t>(a.B) * a.T * a.H * a.Dc * elem_size(a.dtype);
   d.qa = 0;
   d.latent = round_up256(n);
   d.part = d.latent + round_up256(n);
-  d.total = d.part + attend_partial_bytes(a, splits);
+  d.total = d.part + attend_partial_bytes(a, pl);
   return d;
 }
 
@@ -1144,7 +1444,7 @@ size_t qd_mla_attend_workspace_bytes(int batch, int q_len, int heads, int latent
                                      int flags) {
   const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
   if (!attend_shape_ok(a)) return 0;
-  return attend_partial_bytes(a, plan_attend(a, splits, flags).splits);
+  return attend_partial_bytes(a, plan_attend(a, splits, flags));
 }
 
 int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope_dim, int block_size,
@@ -1153,7 +1453,7 @@ int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope
   const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
   if (!attend_shape_ok(a)) return -1;
   const AttendPlan pl = plan_attend(a, splits, flags);
-  if (out_splits) *out_splits = pl.splits;
+  if (out_splits) *out_splits = pl.mfma ? pl.wgs : pl.splits;
   if (head_groups) *head_groups = pl.mfma ? pl.head_groups : 0;
   return pl.mfma ? 1 : 0;
 }
@@ -1222,7 +1522,7 @@ size_t qd_mla_decode_workspace_bytes(int batch, int q_len, int heads, int latent
                                      int flags) {
   const AttendShape a{batch, q_len, heads, latent_dim, rope_dim, block_size, max_pages, num_indices, dtype};
   if (!attend_shape_ok(a)) return 0;
-  return decode_layout(a, plan_attend(a, splits, flags).splits).total;
+  return decode_layout(a, plan_attend(a, splits, flags)).total;
 }
 
 int qd_mla_decode(const void* q_nope, const void* q_rope, const void* cache, const int32_t* block_table,
@@ -1242,7 +1542,7 @@ int qd_mla_decode(const void* q_nope, const void* q_rope, const void* cache, con
   if (!q_nope || !q_rope || !cache || !block_table || !lengths || !positions || !w_uk || !w_uv || !out)
     return mla_fail(nullptr, 0, "null tensor pointer");
   AttendPlan pl = plan_attend(a, splits, flags);
-  const DecodeLayout lay = decode_layout(a, pl.splits);
+  const DecodeLayout lay = decode_layout(a, pl);
   if (!workspace || workspace_bytes < lay.total || !aligned16(workspace))
     return mla_fail(nullptr, 0, "workspace must hold qd_mla_decode_workspace_bytes() bytes, 16-byte aligned");
   char* ws = static_cast<char*>(workspace);

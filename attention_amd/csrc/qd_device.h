@@ -81,6 +81,20 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Inclusive prefix sum over the wave's 64 lanes.
+__device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t x, int lane) {
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t t = __shfl_up(x, off);
+    if (lane >= off) x += t;
+  }
+  return x;
+}
+
 // ----------------------------------------------------------------------------
 // MFMA wrappers
 // ----------------------------------------------------------------------------

@@ -288,10 +288,13 @@ def mla_mode(args) -> None:
     a_flops = 2 * rows * H * (Dc + Dr + Dc)
     a_tflops = a_flops / (a_ms * 1e-3) / 1e12
     kname = "mla_attend_mfma_kernel" if kind == 1 else "mla_attend_generic_kernel"
-    kernels = kname + ("+mla_merge_kernel" if splits > 1 else "")
+    if kind == 1:
+        kernels = kname + "+mla_merge_sk_kernel"
+    else:
+        kernels = kname + ("+mla_merge_kernel" if splits > 1 else "")
     log(f"{kernels}: {a_ms * 1e3:.2f} us, {a_gbs:.1f} GB/s ({100 * a_gbs / PEAK_HBM_GBS:.1f}% of HBM peak), "
         f"{a_tflops:.1f} TFLOP/s ({100 * a_tflops / PEAK_MFMA_BF16_TFLOPS:.1f}% of bf16 MFMA peak); "
-        f"splits={splits} head_groups={groups}")
+        f"{'workgroups' if kind == 1 else 'splits'}={splits} head_groups={groups}")
     result = {
         "metric": "paged MLA decode µs/call and achieved HBM GB/s, 1 MI355X",
         "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 3),
@@ -306,9 +309,10 @@ def mla_mode(args) -> None:
                      "unit": "GB/s", "frac": round(a_gbs / PEAK_HBM_GBS, 4),
                      "traffic": profiled_traffic(kname, cfg.name), "duration_us": round(a_ms * 1e3, 3),
                      "algorithmic_bytes": a_bytes, "mfma_tflops": round(a_tflops, 2),
-                     "mfma_frac": round(a_tflops / PEAK_MFMA_BF16_TFLOPS, 4), "splits": splits,
-                     "head_groups": groups,
-                     "note": "latent attention on the absorbed query (qd_mla_attend), HIP events on its stream; "
+                     "mfma_frac": round(a_tflops / PEAK_MFMA_BF16_TFLOPS, 4),
+                     ("workgroups" if kind == 1 else "splits"): splits, "head_groups": groups,
+                     "note": "latent attention on the absorbed query (qd_mla_attend: attention kernel + merge of "
+                             "rows split across workgroups), HIP events on its stream; "
                              f"{a_flops / a_bytes:.0f} flop/byte against a bf16 ridge of "
                              f"{PEAK_MFMA_BF16_TFLOPS / PEAK_HBM_GBS * 1e3:.0f}"},
     }

@@ -252,9 +252,14 @@ int qd_validate_paged_metadata(const int32_t* block_table, const int32_t* contex
  *   w_uk [heads, nope_dim, latent_dim]; w_uv [heads, value_dim, latent_dim]
  * Query row (b, t) sees tokens [0, end) with end = min(len, max(0, pos+1))
  * when `causal`, else len (clamped to max_pages*block_size); a row with no
- * visible token is zero.  `splits` 0 picks the context split from static
- * shapes and the device; > 0 forces it.  flags: QD_FLAG_FORCE_GENERIC
- * selects the VALU kernels.  Nothing here allocates or synchronizes. */
+ * visible token is zero.  `splits` 0 picks the partition from static shapes
+ * and the device; > 0 forces it: for the MFMA kernel (16-bit, latent and
+ * rope widths multiples of 8, latent <= 512) the number of workgroups that
+ * share the batch's (row, 32-token tile) space in equal ranges (stream-K),
+ * for the VALU kernel the number of context splits per row.
+ * qd_mla_attend_info() reports the kernel and the partition.  flags:
+ * QD_FLAG_FORCE_GENERIC selects the VALU kernels.  Nothing here allocates
+ * or synchronizes. */
 
 /* Reference checks in order, messages included (mla.cu:152-155). */
 int qd_latent_kv_write_validate(const qd_tensor_desc* latent, const qd_tensor_desc* rope,
@@ -285,14 +290,16 @@ int qd_mla_attend_validate(const qd_tensor_desc* q, const qd_tensor_desc* q_rope
                            const qd_tensor_desc* positions, const qd_tensor_desc* indices, double scale,
                            char* msg, size_t msg_cap);
 
-/* Bytes of float32 split partials qd_mla_attend needs (0 for one split). */
+/* Workspace bytes qd_mla_attend needs (partials of rows split across
+ * workgroups or splits, and per-row spans); 0 when none is needed. */
 size_t qd_mla_attend_workspace_bytes(int batch, int q_len, int heads, int latent_dim, int rope_dim,
                                      int block_size, int max_pages, int num_indices, int dtype, int splits,
                                      int flags);
 
-/* The plan qd_mla_attend would use: returns 1 for the MFMA kernel (with
- * *head_groups workgroups per query row and split), 0 for the VALU kernel,
- * -1 for invalid shapes; *out_splits gets the split count. */
+/* The plan qd_mla_attend would use: returns 1 for the MFMA kernel
+ * (*out_splits = stream-K workgroups per head group, *head_groups = head
+ * groups), 0 for the VALU kernel (*out_splits = context splits per row,
+ * *head_groups = 0), -1 for invalid shapes. */
 int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope_dim, int block_size,
                        int max_pages, int num_indices, int dtype, int splits, int flags, int* out_splits,
                        int* head_groups);

@@ -181,7 +181,13 @@ def test_attend_plan_queries():
     assert cabi.mla_attend_info(1, 1, 4, 36, 8, 16, 4)[0] == 0
     assert cabi.mla_attend_info(1, 1, 4, 32, 8, 16, 4, splits=5)[1] == 5
     assert cabi.mla_attend_info(0, 1, 4, 32, 8, 16, 4, nk=-2)[0] == -1
-    assert cabi.lib().qd_mla_attend_workspace_bytes(2, 1, 4, 32, 8, 16, 4, -1, BF16, 3, 0) == 2 * 4 * 3 * 34 * 4
-    assert cabi.lib().qd_mla_attend_workspace_bytes(2, 1, 4, 32, 8, 16, 4, -1, BF16, 1, 0) == 0
+    ws = cabi.lib().qd_mla_attend_workspace_bytes
+    # VALU kernel (fp32): [R, H, splits, Dc+2] fp32, none for one split.
+    assert ws(2, 1, 4, 32, 8, 16, 4, -1, F32, 3, 0) == 2 * 4 * 3 * 34 * 4
+    assert ws(2, 1, 4, 32, 8, 16, 4, -1, F32, 1, 0) == 0
+    # MFMA kernel: (workgroups + rows) partial slots, then G and the row spans.
+    assert cabi.mla_attend_info(2, 1, 4, 32, 8, 16, 4, splits=3)[0] == 1
+    r256 = lambda x: (x + 255) // 256 * 256
+    assert ws(2, 1, 4, 32, 8, 16, 4, -1, BF16, 3, 0) == r256((3 + 2) * 4 * 34 * 4) + r256(8 + 2 * 2 * 4)
     total = cabi.lib().qd_mla_decode_workspace_bytes(2, 1, 4, 32, 8, 16, 4, -1, BF16, 3, 0)
-    assert total == 512 + 512 + 2 * 4 * 3 * 34 * 4      # qa and latent ([2,1,4,32] bf16), then partials
+    assert total == 512 + 512 + ws(2, 1, 4, 32, 8, 16, 4, -1, BF16, 3, 0)   # qa, latent ([2,1,4,32] bf16), then those
