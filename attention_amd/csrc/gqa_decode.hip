@@ -640,64 +640,70 @@ __device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
   return (clamp_len(p, len_raw) + 15) >> 4;
 }
 
-// Merges the partials of the g heads of one kv-head, in place of the
+// Merges the partials of up to four heads of one kv-head, in place of the
 // reference's merge kernel (gqa_decode.cu:74-87): rows r = 0..nrows-1 at
-// base + r*row_stride, head j at + j*(D+2), each {m (natural log), l,
-// acc[D]}.  Rows are folded in order with SoftmaxState::merge
+// base + r*row_stride, head j < nheads at + j*(D+2), each {m (natural log),
+// l, acc[D]}.  Rows are folded in order with SoftmaxState::merge
 // (online_softmax.cuh:17-24): a row with l == 0 is skipped, the running
 // state is rescaled by exp(m - max).  Output acc/l rounded once, zeros when
-// l == 0 (gqa_decode.cu:84-86).  One wave: 16 lanes per head, D/16
-// elements per lane, 4 heads per pass; the rows are loaded kBatch at a time
-// so that one memory round trip covers a typical merge.
+// l == 0 (gqa_decode.cu:84-86), head j at out + j*D.  One wave: 16 lanes
+// per head, D/16 consecutive elements per lane (one vector store); the rows
+// are loaded kBatch at a time so that one memory round trip covers a
+// typical merge.
 template <int D, int DT, int kBatch>
-__device__ __forceinline__ void merge_kv_group(const float* base, int64_t row_stride, int nrows, int g,
-                                               typename Elem<DT>::S* out) {
+__device__ __forceinline__ void merge_heads4(const float* base, int64_t row_stride, int nrows, int nheads,
+                                             typename Elem<DT>::S* out) {
   // Partials come from an earlier kernel on the same stream: plain loads.
-  using E = Elem<DT>;
   constexpr int EPL = D / 16;
   const int lane = threadIdx.x & 63;
   const int j4 = lane >> 4;
   const int c16 = lane & 15;
-  for (int h0 = 0; h0 < g; h0 += 4) {
-    const int h = h0 + j4;
-    const float* hb = base + static_cast<int64_t>(h < g ? h : 0) * (D + 2);
-    float M = -INFINITY, L = 0.f;
-    float acc[EPL];
+  const bool active = j4 < nheads;
+  const float* hb = base + static_cast<int64_t>(active ? j4 : 0) * (D + 2);
+  float M = -INFINITY, L = 0.f;
+  float acc[EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-    for (int s0 = 0; s0 < nrows; s0 += kBatch) {
-      float ms[kBatch], ls[kBatch], av[kBatch][EPL];
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < nrows; s0 += kBatch) {
+    float ms[kBatch], ls[kBatch], av[kBatch][EPL];
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        const float* row = hb + static_cast<int64_t>(min(s0 + t, nrows - 1)) * row_stride;
-        ms[t] = row[0];
-        ls[t] = row[1];
-        // Rows are D+2 floats (D even): acc is 8-byte aligned.
+    for (int t = 0; t < kBatch; ++t) {
+      const float* row = hb + static_cast<int64_t>(min(s0 + t, nrows - 1)) * row_stride;
+      ms[t] = row[0];
+      ls[t] = row[1];
+      // Rows are D+2 floats (D even): acc is 8-byte aligned.
 #pragma unroll
-        for (int e = 0; e < EPL; e += 2) {
-          const f32x2 x = *reinterpret_cast<const f32x2*>(row + 2 + c16 * EPL + e);
-          av[t][e] = x[0];
-          av[t][e + 1] = x[1];
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        if (s0 + t >= nrows || ls[t] == 0.f) continue;
-        const float mn = fmaxf(M, ms[t]);
-        const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
-        const float bb = fast_exp2((ms[t] - mn) * kLog2e);
-        L = a * L + bb * ls[t];
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[e] = a * acc[e] + bb * av[t][e];
-        M = mn;
+      for (int e = 0; e < EPL; e += 2) {
+        const f32x2 x = *reinterpret_cast<const f32x2*>(row + 2 + c16 * EPL + e);
+        av[t][e] = x[0];
+        av[t][e + 1] = x[1];
       }
     }
-    if (h < g) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      typename E::S* o = out + static_cast<int64_t>(h) * D + c16 * EPL;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) o[e] = E::from_f(L > 0.f ? acc[e] * inv : 0.f);
+    for (int t = 0; t < kBatch; ++t) {
+      if (s0 + t >= nrows || ls[t] == 0.f) continue;
+      const float mn = fmaxf(M, ms[t]);
+      const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
+      const float bb = fast_exp2((ms[t] - mn) * kLog2e);
+      L = a * L + bb * ls[t];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] = a * acc[e] + bb * av[t][e];
+      M = mn;
     }
+  }
+  if (!active) return;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  uint32_t wv[EPL / 2];
+#pragma unroll
+  for (int e = 0; e < EPL; e += 2)
+    wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
+  char* dst = reinterpret_cast<char*>(out + static_cast<int64_t>(j4) * D + c16 * EPL);
+  if constexpr (EPL == 4) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
+  } else {
+#pragma unroll
+    for (int t = 0; t < EPL / 8; ++t)
+      *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
   }
 }
 
@@ -711,21 +717,41 @@ constexpr int sk_max_waves() {
   return (NKV == 1 && D <= 128) ? kMaxWgWaves : kMaxWgWaves / 2;
 }
 
+#ifndef QD_SK_SEQ_COST
+#define QD_SK_SEQ_COST 6
+#endif
+// Partition cost units: a 16-token group costs kSkGroupCost, and every
+// non-empty sequence adds kSkSeqCost at its start for the pipeline refill
+// (page-table window and first K/V round trips) that the workgroup entering
+// it pays; measured at about one group's streaming time.
+constexpr int64_t kSkGroupCost = 4;
+constexpr int64_t kSkSeqCost = QD_SK_SEQ_COST;
+
+__device__ __forceinline__ int64_t seq_cost(int groups) {
+  return groups > 0 ? kSkGroupCost * groups + kSkSeqCost : 0;
+}
+
 // Balanced ("stream-K") layout.  grid: W = p.splits workgroups of
 // p.wg_waves waves; wave j of a workgroup serves kv-heads j*NKV .. j*NKV +
 // NKV-1, then the same plus wg_waves*NKV, ... so that a workgroup reads
 // whole cache rows (all kv-heads of a token) at once, which streams faster
 // from HBM than kv-head slices read at unrelated times.
 //
-// Sequence b has n_b = ceil(len_b/16) groups; the sequences are laid end to
-// end into G = sum_b n_b groups and workgroup w takes groups
-// [w*G/W, (w+1)*G/W).  For every sequence it touches, the workgroup either
-// writes the output rows directly (it holds the whole sequence) or writes a
-// partial for all Hq heads into slot (w + b) of the workspace (Hq*(D+2)
-// floats per slot; the slot is unique per (sequence, workgroup) because the
-// workgroups of sequence b+1 start at or after the last one of b, so
-// W + B slots suffice).  merge_sk_kernel combines the slots of every split
-// sequence.  Rows of empty sequences are zero-filled by workgroup b % W.
+// Sequence b has n_b = ceil(len_b/16) groups and costs c_b = U*n_b + V
+// cost units (U = kSkGroupCost, V = kSkSeqCost; 0 when n_b = 0).  The
+// sequences are laid end to end into C = sum_b c_b units: sequence b spans
+// [C_b, C_b + c_b), its first V units are the start cost and group i owns
+// unit x_{b,i} = C_b + V + U*i.  The first Wu = min(W, C/U) workgroups take
+// the unit ranges [w*C/Wu, (w+1)*C/Wu) (each at least U long, so every
+// workgroup between the holders of a sequence's first and last group holds
+// at least one of its groups) and process the groups whose unit they hold.
+// For every sequence it touches, a workgroup either writes the output rows
+// directly (it holds the whole sequence) or writes a partial for all Hq
+// heads into slot (w + b) of the workspace (Hq*(D+2) floats per slot; the
+// slot is unique per (sequence, workgroup) because the workgroups of
+// sequence b+1 start at or after the last one of b, so W + B slots
+// suffice).  merge_sk_kernel combines the slots of every split sequence.
+// Rows of empty sequences are zero-filled by workgroup b % W.
 template <int D, int DT, int PF, int NKV>
 __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
@@ -738,8 +764,8 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   __shared__ __align__(16) char ktile[sk_max_waves<D, NKV>()][KTile<D>::kBytes];
 
   // Prologue, one memory round trip for B <= 64*kRegChunks: every lane loads
-  // the lengths of sequences c*64 + lane, and the group counts and their
-  // running sums stay in registers.
+  // the lengths of sequences c*64 + lane, and the group counts and the
+  // running sums of the costs stay in registers.
   constexpr int kRegChunks = 4;
   int n_r[kRegChunks];
   int64_t incl_r[kRegChunks];
@@ -751,14 +777,14 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   int64_t carry = 0;
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
-    incl_r[c] = carry + wave_incl_scan_i64(n_r[c], lane);
+    incl_r[c] = carry + wave_incl_scan_i64(seq_cost(n_r[c]), lane);
     carry = __shfl(incl_r[c], 63);
   }
   for (int c = 64 * kRegChunks; c < B; c += 64) {  // larger batches: re-read
     const int bb = c + lane;
-    carry += wave_sum_i64(bb < B ? seq_groups(p, p.lens[bb]) : 0);
+    carry += wave_sum_i64(seq_cost(bb < B ? seq_groups(p, p.lens[bb]) : 0));
   }
-  const int64_t G = carry;
+  const int64_t C = carry;
 
   // Empty sequences (no workgroup holds them): workgroup b % W writes their
   // zero rows and a meta entry that tells merge_sk_kernel to skip them.
@@ -784,22 +810,25 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
     zero_fill(__ballot(bb < B && bb % W == w && seq_groups(p, p.lens[bb]) == 0), c);
   }
 
-  const int64_t g0 = static_cast<int64_t>(w) * G / W;
-  const int64_t g1 = static_cast<int64_t>(w + 1) * G / W;
-  if (g0 >= g1) return;  // uniform across the workgroup
+  // Workgroups in use (uniform across the grid).
+  const int64_t wu_cap = C / kSkGroupCost;
+  const int Wu = static_cast<int>(wu_cap < W ? (wu_cap > 0 ? wu_cap : 1) : W);
+  if (w >= Wu || C == 0) return;
+  const int64_t c0 = static_cast<int64_t>(w) * C / Wu;
+  const int64_t c1 = static_cast<int64_t>(w + 1) * C / Wu;
 
-  // The sequence holding group g0 (the first whose running group end exceeds
-  // g0) and its first group gs.
+  // The sequence whose unit range holds c0 (the first whose running cost
+  // end exceeds c0) and its first unit cs.
   int b = B;
-  int64_t gs = 0;
+  int64_t cs = 0;
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
     if (b == B) {
       const int bb = c * 64 + lane;
-      const int cnt = __popcll(__ballot(bb < B && incl_r[c] <= g0));
+      const int cnt = __popcll(__ballot(bb < B && incl_r[c] <= c0));
       if (cnt < min(64, B - c * 64)) {
         b = c * 64 + cnt;
-        gs = __shfl(incl_r[c] - n_r[c], cnt);
+        cs = __shfl(incl_r[c] - seq_cost(n_r[c]), cnt);
       }
     }
   }
@@ -807,82 +836,88 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
     carry = __shfl(incl_r[kRegChunks - 1], 63);
     for (int c = 64 * kRegChunks; c < B; c += 64) {
       const int bb = c + lane;
-      const int64_t n = bb < B ? static_cast<int64_t>(seq_groups(p, p.lens[bb])) : 0;
+      const int64_t n = bb < B ? seq_cost(seq_groups(p, p.lens[bb])) : 0;
       const int64_t incl = carry + wave_incl_scan_i64(n, lane);
-      const int cnt = __popcll(__ballot(bb < B && incl <= g0));
+      const int cnt = __popcll(__ballot(bb < B && incl <= c0));
       if (cnt < min(64, B - c)) {
         b = c + cnt;
-        gs = __shfl(incl - n, cnt);
+        cs = __shfl(incl - n, cnt);
         break;
       }
       carry = __shfl(incl, 63);
     }
   }
-  if (b >= B) return;  // unreachable when G is consistent
+  if (b >= B) return;  // unreachable when C is consistent
 
-  // Workgroup holding flattened group x.
-  auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * W - 1) / G); };
+  // Workgroup whose unit range holds unit x.
+  auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * Wu - 1) / C); };
+  // Groups of the current sequence whose unit lies below x.
+  auto groups_below = [&](int64_t x, int64_t x0, int nb) {
+    if (x <= x0) return 0;
+    const int64_t i = (x - x0 + kSkGroupCost - 1) / kSkGroupCost;
+    return static_cast<int>(i < nb ? i : nb);
+  };
 
   MfmaWave<D, DT, PF, NKV> wv;
   wv.init_lane();
-  int len = clamp_len(p, p.lens[b]);
-  int nb = (len + 15) >> 4;
-  int gi = static_cast<int>(g0 - gs);
-  int64_t remaining = g1 - g0;
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
-  while (remaining > 0) {
-    const int seg = static_cast<int>(min(static_cast<int64_t>(nb - gi), remaining));
-    const bool whole = gi == 0 && gi + seg == nb;
-    float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
-    for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
-      wv.begin_item(p, b, kvh0, len);
-      wv.run(p, gi, gi + seg, ktile[wid]);
+  while (true) {
+    const int len = clamp_len(p, p.lens[b]);
+    const int nb = (len + 15) >> 4;
+    const int64_t x0 = cs + kSkSeqCost;  // unit of group 0
+    const int i0 = groups_below(c0, x0, nb);
+    const int i1 = groups_below(c1, x0, nb);
+    if (i1 > i0) {
+      const bool whole = i0 == 0 && i1 == nb;
+      float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
+      for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
+        wv.begin_item(p, b, kvh0, len);
+        wv.run(p, i0, i1, ktile[wid]);
 #pragma unroll
-      for (int j = 0; j < NKV; ++j) {
-        const float l_tot = wv.total_l(j);
-        if (whole)
-          wv.store_direct(p, b, kvh0, j, l_tot);
-        else
-          wv.template store_partial<false>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2), D + 2,
-                                           l_tot);
+        for (int j = 0; j < NKV; ++j) {
+          const float l_tot = wv.total_l(j);
+          if (whole)
+            wv.store_direct(p, b, kvh0, j, l_tot);
+          else
+            wv.template store_partial<false>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
+                                             D + 2, l_tot);
+        }
+      }
+      // The workgroup holding a sequence's first group records which
+      // workgroups span it, for merge_sk_kernel (also for a whole sequence,
+      // so that nothing from an earlier call survives).
+      if (i0 == 0 && threadIdx.x == 0) {
+        const int first = wg_of(x0);
+        p.meta[2 * b] = first;
+        p.meta[2 * b + 1] = wg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
       }
     }
-    // The workgroup holding a sequence's first group records which
-    // workgroups span it, for merge_sk_kernel (also for a whole sequence, so
-    // that nothing from an earlier call survives).
-    if (gi == 0 && threadIdx.x == 0) {
-      const int first = wg_of(gs);
-      p.meta[2 * b] = first;
-      p.meta[2 * b + 1] = wg_of(gs + nb - 1) - first + 1;
-    }
-    remaining -= seg;
-    if (remaining > 0) {
-      gs += nb;
-      gi = 0;
-      do {
-        if (++b >= B) return;  // unreachable when G is consistent
-        len = clamp_len(p, p.lens[b]);
-        nb = (len + 15) >> 4;
-      } while (nb == 0);
-    }
+    cs += seq_cost(nb);
+    if (cs >= c1) break;
+    do {
+      if (++b >= B) return;  // unreachable when C is consistent
+    } while (p.lens[b] <= 0);
   }
 }
 
-// Stream-K merge: grid (Hkv, B), block 64; one wave merges the g heads of
-// one kv-head of one sequence from slots first+b .. first+b+nwg-1.  Two
+// Stream-K merge: grid (Hkv * ceil(g/4), B), block 64; one wave merges up
+// to four heads of one kv-head of one sequence from slots first+b ..
+// first+b+nwg-1, so the heads of a kv-head merge in parallel.  Two
 // dependent memory round trips: the meta entry, then the partial rows.
 template <int D, int DT>
 __global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
-  const int kvh = blockIdx.x;
+  const int npass = (p.g + 3) >> 2;
+  const int kvh = blockIdx.x / npass;
+  const int pass = blockIdx.x - kvh * npass;
   const int b = blockIdx.y;
   const int first = p.meta[2 * b];
   const int nwg = p.meta[2 * b + 1];
   if (nwg <= 1) return;  // written directly, or an empty sequence (zero-filled)
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
-  const int64_t h0 = static_cast<int64_t>(kvh) * p.g;
-  merge_kv_group<D, DT, 16>(p.ws + static_cast<int64_t>(first + b) * slot_floats + h0 * (D + 2), slot_floats, nwg,
-                        p.g, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h0) * D);
+  const int64_t h0 = static_cast<int64_t>(kvh) * p.g + 4 * pass;
+  merge_heads4<D, DT, 16>(p.ws + static_cast<int64_t>(first + b) * slot_floats + h0 * (D + 2), slot_floats, nwg,
+                          min(4, p.g - 4 * pass), static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h0) * D);
 }
 
 // ----------------------------------------------------------------------------
@@ -1497,7 +1532,8 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
     hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0,
                        stm, prm);
   if (stages & QD_STAGE_MERGE)
-    hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim), dim3(kv_heads, batch), dim3(64), 0, stm, prm);
+    hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim), dim3(kv_heads * ((prm.g + 3) / 4), batch), dim3(64), 0,
+                       stm, prm);
   return launch_error();
 }
 

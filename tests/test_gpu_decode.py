@@ -392,6 +392,34 @@ def test_auto_workspace_reuse_across_length_mixes(gpu):
         assert torch.count_nonzero(ws[:ctrl]) == 0, "control region not left zero" 
 
 
+@pytest.mark.parametrize("lengths", [[40, 0], [48, 20], [1, 200, 3], [17] * 5], ids=["3g", "3g+2g", "1g+13g+1g", "5x2g"])
+def test_auto_few_groups_wide_table(gpu, lengths):
+    """A wide page table (256 pages) sizes the stream-K grid for long
+    sequences; with only a few 16-token groups in the batch most workgroups
+    get no group.  No workgroup between the first and the last holder of a
+    sequence may be left without one: the merge folds every slot in that
+    span, and the scratch here is NaN, so an unwritten slot shows."""
+    hq, hkv, d, p, maxp = 32, 8, 128, 16, 256
+    B = len(lengths)
+    kind, waves, _, _ = cabi.auto_info(B, hq, hkv, d, p, maxp, cabi.DTYPE[torch.bfloat16])
+    say(f"few groups, wide table: lengths {lengths} kind={kind} waves={waves}")
+    q, k, v, table, lens = make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
+                                            block_size=p, dtype=torch.bfloat16, seed=41)
+    tpad = torch.full((B, maxp), -1, dtype=torch.int32)
+    tpad[:, :table.shape[1]] = table
+    case = to_dev((q, k, v, tpad, lens), gpu)
+    ref, rows = oracle_rows(case)
+    nbytes = cabi.auto_workspace_bytes(B, hq, hkv, d, p, maxp, cabi.DTYPE[torch.bfloat16])
+    ctrl = cabi.auto_control_bytes(B)
+    ws = torch.full((nbytes,), 0xFF, device=gpu, dtype=torch.uint8)
+    ws[:ctrl] = 0
+    out = torch.full_like(case[0], float("nan"))
+    rc = cabi.auto_launch(*case, out, scale=1 / math.sqrt(d), workspace=ws)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert_close(out, ref, "bf16", rows, "few groups")
+
+
 _BIG_MIX = [int(x) for x in np.random.default_rng(5).integers(0, 120, 520)]
 for _i in range(0, 520, 37):
     _BIG_MIX[_i] = 0
