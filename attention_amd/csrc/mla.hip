@@ -29,6 +29,7 @@
 
 #include <hip/hip_runtime.h>
 
+
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
@@ -304,23 +305,10 @@ __device__ __forceinline__ float sum_over_lane_groups(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// LDS-only workgroup barrier for the DMA pipeline: waits for this wave's LDS
-// operations and for all but `kVm` of its vector-memory loads (LDS DMA
-// included), then s_barrier.  __syncthreads() would wait for every
-// outstanding load (vmcnt(0)) and drain the DMA ring at each tile.  The
-// empty asm statements keep the compiler from moving memory accesses across.
-template <int kVm>
-__device__ __forceinline__ void dma_barrier() {
-  static_assert(kVm >= 0 && kVm < 64, "vmcnt is 6 bits");
-  constexpr int imm = (kVm & 0xF) | ((kVm >> 4) << 14) | (0x7 << 4) | (0x0 << 8);  // lgkmcnt(0)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(imm);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
-// operations, not for its outstanding loads (the DMA ring keeps flowing).
+// operations, not for its outstanding loads (the staged tiles keep
+// flowing; __syncthreads() would wait for every load, vmcnt(0)).  The empty
+// asm statements keep the compiler from moving memory accesses across.
 __device__ __forceinline__ void lds_barrier() {
   constexpr int imm = 0x3F | (0x3 << 14) | (0x7 << 4) | (0x0 << 8);  // vmcnt max, lgkmcnt(0)
   asm volatile("" ::: "memory");
@@ -329,25 +317,28 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Tile ring depth for CPT DMA instructions per thread per tile (CPT * 4 KB
-// per tile buffer), within 160 KB of LDS.
-constexpr int ring_depth(int cpt) { return cpt <= 9 ? 4 : 3; }
-constexpr int kOffSlotsDma = 6;  // per-tile metadata slots (ring depth + 2)
-constexpr int kWinPages = 256;    // page-table window (dense rows)
-constexpr int kDmaWaves = 4;      // waves 0..3 issue the tile DMA
-constexpr int kFlagFirst = 1;     // first tile of a row segment in this workgroup
-constexpr int kFlagLast = 2;      // last tile of a row segment in this workgroup
-constexpr int kFlagWhole = 4;     // (with kFlagLast) the segment is the whole row
+// Tiles in flight ahead of the one being computed, staged in registers
+// (CPT u32x4 per thread per tile): as deep as the register file allows for
+// the wave layout (4 slices of one head tile, or 2 x 2).
+__host__ __device__ constexpr int stage_depth(int cpt, int ds) {
+  return ds == 4 ? (cpt <= 5 ? 6 : 4) : (cpt <= 5 ? 4 : 3);
+}
+constexpr int kRingTiles = 2;   // LDS tile buffers: the tile being computed and the next
+constexpr int kMetaSlots = 8;   // per-tile metadata slots (>= stage depth + 2)
+constexpr int kWinPages = 256;  // page-table window (dense rows)
+constexpr int kFlagFirst = 1;   // first tile of a row segment in this workgroup
+constexpr int kFlagLast = 2;    // last tile of a row segment in this workgroup
+constexpr int kFlagWhole = 4;   // (with kFlagLast) the segment is the whole row
 
 __host__ __device__ constexpr size_t mla_mfma_lds_bytes(int cpt) {
-  return static_cast<size_t>(ring_depth(cpt)) * cpt * 4096  // tile ring
-         + kOffSlotsDma * kTileTokens * 8                      // row offsets
-         + kOffSlotsDma * 8                                    // tile rows
-         + kOffSlotsDma * 4 * 2                                // masks, flags
-         + kWinPages * 4                                       // page window
-         + 32                                                  // prologue results
-         + kAttendThreads * 32                                 // score exchange
-         + 1024;                                               // slack
+  return static_cast<size_t>(kRingTiles) * cpt * 4096  // tile ring
+         + kMetaSlots * kTileTokens * 8                 // row offsets
+         + kMetaSlots * 8 * 2                           // tile rows, tile bases
+         + kMetaSlots * 4 * 2                           // masks, flags
+         + kWinPages * 4                                // page window
+         + 32                                           // prologue results
+         + kAttendThreads * 32                          // score exchange
+         + 1024;                                        // slack
 }
 
 // Tiles of 32 listed tokens of query row r (dense: the visible prefix).
@@ -371,17 +362,22 @@ __device__ __forceinline__ int row_tiles(const MlaParams& p, int64_t r) {
 // v / nht (NBLKW blocks of 128 columns).  Every wave of a head tile computes
 // the same scores (the QK product is cheap next to the stream) and the PV
 // product for its own slice only.  Per 32-token tile:
-//   load     waves 0..3 move the tile's cache rows HBM -> LDS with direct
-//            DMA (global_load_lds_dwordx4, 1 KB per wave instruction, CPT
-//            per thread) into a ring of ring_depth(CPT) buffers, up to
-//            ring_depth - 1 tiles ahead.  Rows are unpadded (2W bytes); when
-//            W/8 is a multiple of 8, 16-byte column c of row r sits at
-//            c ^ (r & 7) so the operand reads spread over the banks.  Wave 0
-//            walks the rows ahead of the ring: per tile it writes the row
-//            offsets (from a page-table window in LDS for dense rows, from
-//            the index list for sparse rows), the visibility mask, the row
-//            and the segment flags.  A token that is not visible is loaded
-//            as a duplicate of a visible row of its tile and gets weight 0.
+//   load     all 256 threads load the tile's cache rows into registers
+//            (CPT 16-byte nontemporal loads per thread, 1 KB per wave
+//            instruction) PF = stage_depth tiles ahead, and write a tile
+//            into one of two LDS buffers just before it is computed, so the
+//            bytes in flight are bounded by the register file rather than by
+//            LDS.  Rows are unpadded (2W bytes); when W/8 is a multiple of 8,
+//            16-byte column c of row r sits at c ^ (r & 7) so the operand
+//            reads spread over the banks.  Wave 0 walks the rows PF + 1
+//            tiles ahead: per tile it writes the row offsets (from a
+//            page-table window in LDS for dense rows, from the index list
+//            for sparse rows), the visibility mask, the row and the segment
+//            flags.  A token that is not visible is loaded as a duplicate of
+//            a visible row of its tile and gets weight 0.  Loads complete in
+//            issue order, so the query of a row segment is loaded PF tiles
+//            before the segment starts (a load at the start would wait for
+//            every tile in flight).
 //   QK       lane (r16, q4): A = row r16 (+16), 16-byte column 4c + q4,
 //            B = [q | q_rope | 0] of head r16, elements 32c + 8 q4 .. +7
 //            -> S0/S1: tokens 4 q4 + i and 16 + 4 q4 + i.
@@ -402,7 +398,8 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
   constexpr int KMAX = 2 * CPT;            // W <= 64 CPT  ->  ceil(W/32) <= 2 CPT
   constexpr int NBLKW = 4 / DS;            // latent blocks of 128 columns per wave
   constexpr int QCH = (KMAX + DS - 1) / DS;  // query chunks per wave (c = slice + DS i)
-  constexpr int kRing = ring_depth(CPT);
+  constexpr int PF = stage_depth(CPT, DS);
+  static_assert(kMetaSlots >= PF + 2, "metadata slots");
   constexpr int kTileBytes = CPT * 4096;
   extern __shared__ __align__(16) char smem[];
   const int lane = threadIdx.x & 63;
@@ -415,13 +412,13 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
   if (w >= p.wgs) return;  // whole workgroup: uniform
 
   char* ring = smem;
-  int64_t* offs = reinterpret_cast<int64_t*>(smem + kRing * kTileBytes);  // [slots][32]
-  int64_t* tile_row = offs + kOffSlotsDma * kTileTokens;                   // [slots]
-  uint32_t* masks = reinterpret_cast<uint32_t*>(tile_row + kOffSlotsDma);  // [slots]
-  int* flags = reinterpret_cast<int*>(masks + kOffSlotsDma);               // [slots]
-  int32_t* win = flags + kOffSlotsDma;                                     // [kWinPages]
-  int64_t* scal = reinterpret_cast<int64_t*>(win + kWinPages);             // {G, row0, tir0}
-  f32x4* sx = reinterpret_cast<f32x4*>(scal + 4);                           // [waves][64][2] partial scores
+  int64_t* offs = reinterpret_cast<int64_t*>(smem + kRingTiles * kTileBytes);  // [slots][32]
+  int64_t* tile_row = offs + kMetaSlots * kTileTokens;                         // [slots]
+  int64_t* tile_base = tile_row + kMetaSlots;                                  // [slots]
+  uint32_t* masks = reinterpret_cast<uint32_t*>(tile_base + kMetaSlots);       // [slots]
+  int* flags = reinterpret_cast<int*>(masks + kMetaSlots);                     // [slots]
+  int32_t* win = flags + kMetaSlots;                                           // [kWinPages]
+  f32x4* sx = reinterpret_cast<f32x4*>(win + kWinPages + 8);               // [waves][64][2] partial scores
 
   const int64_t rows = static_cast<int64_t>(p.B) * p.T;
   const bool sparse = p.nk >= 0;
@@ -435,44 +432,72 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
   const bool head_ok = h < p.H;
   const int blk0 = slice * NBLKW;
 
-  // Prologue (wave 0): total tiles G and the (row, tile) where this
-  // workgroup's range starts.
-  if (wv == 0) {
-    int64_t G = 0;
-    for (int64_t base = 0; base < rows; base += 64) {
-      const int64_t r = base + lane;
-      G += wave_sum_i64(r < rows ? row_tiles(p, r) : 0);
+  // Prologue, in every wave: the visible end and the tile count of rows
+  // 64 c + lane (c < kRegChunks) stay in registers (one round trip for up
+  // to 256 rows; later rows are re-read), then the total G, this
+  // workgroup's first (row, tile) and the empty rows it zero-fills.
+  constexpr int kRegChunks = 4;
+  constexpr int64_t kRegRows = 64 * kRegChunks;
+  int end_r[kRegChunks], nt_r[kRegChunks];
+  int64_t incl_r[kRegChunks];
+  auto tiles_for = [&](int end) {
+    const int count = sparse ? p.nk : end;
+    return (count + kTileTokens - 1) / kTileTokens;
+  };
+#pragma unroll
+  for (int c = 0; c < kRegChunks; ++c) {
+    const int64_t r = 64 * c + lane;
+    end_r[c] = r < rows ? row_end(p, static_cast<int>(r / p.T), r) : 0;
+    nt_r[c] = r < rows ? tiles_for(end_r[c]) : 0;
+  }
+  int64_t carry = 0;
+#pragma unroll
+  for (int c = 0; c < kRegChunks; ++c) {
+    incl_r[c] = carry + wave_incl_scan_i64(nt_r[c], lane);
+    carry = __shfl(incl_r[c], 63);
+  }
+  for (int64_t base = kRegRows; base < rows; base += 64) {
+    const int64_t r = base + lane;
+    carry += wave_sum_i64(r < rows ? row_tiles(p, r) : 0);
+  }
+  const int64_t G = carry;
+  const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
+  const int ntiles = static_cast<int>(static_cast<int64_t>(w + 1) * G / p.wgs - g0);
+  if (w == 0 && hg == 0 && threadIdx.x == 0) *p.gtotal = G;
+
+  // Row and tile of flattened tile g0.
+  int64_t row0 = 0;
+  int tir0 = 0;
+  if (ntiles > 0) {
+    bool found = false;
+#pragma unroll
+    for (int c = 0; c < kRegChunks; ++c) {
+      const uint64_t hit = __ballot(64 * c + lane < rows && incl_r[c] > g0);
+      if (!found && hit) {
+        const int f = __builtin_ctzll(hit);
+        row0 = 64 * c + f;
+        tir0 = static_cast<int>(g0 - (__shfl(incl_r[c], f) - __shfl(nt_r[c], f)));
+        found = true;
+      }
     }
-    const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
-    int64_t carry = 0, row0 = 0, tir0 = 0;
-    for (int64_t base = 0; base < rows; base += 64) {
+    int64_t cr = __shfl(incl_r[kRegChunks - 1], 63);
+    for (int64_t base = kRegRows; !found && base < rows; base += 64) {
       const int64_t r = base + lane;
       const int64_t n = r < rows ? row_tiles(p, r) : 0;
-      const int64_t incl = carry + wave_incl_scan_i64(n, lane);
+      const int64_t incl = cr + wave_incl_scan_i64(n, lane);
       const uint64_t hit = __ballot(r < rows && incl > g0);
       if (hit) {
         const int f = __builtin_ctzll(hit);
         row0 = base + f;
-        tir0 = g0 - (__shfl(incl, f) - __shfl(n, f));
-        break;
+        tir0 = static_cast<int>(g0 - (__shfl(incl, f) - __shfl(n, f)));
+        found = true;
       }
-      carry = __shfl(incl, 63);
-    }
-    if (lane == 0) {
-      scal[0] = G;
-      scal[1] = row0;
-      scal[2] = tir0;
-      if (w == 0 && hg == 0) *p.gtotal = G;
+      cr = __shfl(incl, 63);
     }
   }
-  __syncthreads();
-  const int64_t G = scal[0];
-  const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
-  const int ntiles = static_cast<int>(static_cast<int64_t>(w + 1) * G / p.wgs - g0);
 
   // Rows with no tile: zeros from workgroup (row % wgs), meta {0, 0}.
-  for (int64_t r = w; r < rows; r += p.wgs) {
-    if (row_tiles(p, r) != 0) continue;
+  auto zero_row = [&](int64_t r) {
     if (active && head_ok) {
       S* orow = static_cast<S*>(p.out) + (r * p.H + h) * p.Dc;
 #pragma unroll
@@ -487,7 +512,32 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
       p.meta[2 * r] = 0;
       p.meta[2 * r + 1] = 0;
     }
+  };
+#pragma unroll
+  for (int c = 0; c < kRegChunks; ++c) {
+    const int64_t r = 64 * c + lane;
+    uint64_t zm = __ballot(r < rows && nt_r[c] == 0 && r % p.wgs == w);
+    while (zm) {
+      zero_row(64 * c + __builtin_ctzll(zm));
+      zm &= zm - 1;
+    }
   }
+  for (int64_t r = kRegRows + (w - kRegRows % p.wgs + p.wgs) % p.wgs; r < rows; r += p.wgs)
+    if (row_tiles(p, r) == 0) zero_row(r);
+
+  // Per-row values of the cursor: from the registers, or re-read past them.
+  auto pick = [&](const int (&arr)[kRegChunks], int64_t r) {
+    const int c = static_cast<int>(r >> 6);
+    const int v = c == 0 ? arr[0] : c == 1 ? arr[1] : c == 2 ? arr[2] : arr[3];
+    return __builtin_amdgcn_readlane(v, static_cast<int>(r & 63));
+  };
+  auto end_of = [&](int64_t r) {
+    return r < kRegRows ? pick(end_r, r)
+                        : __builtin_amdgcn_readfirstlane(row_end(p, static_cast<int>(r / p.T), r));
+  };
+  auto tiles_of = [&](int64_t r) {
+    return r < kRegRows ? pick(nt_r, r) : __builtin_amdgcn_readfirstlane(row_tiles(p, r));
+  };
 
   const int kch = p.kch;
   (void)kch;
@@ -495,24 +545,33 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
   const int swz = (w8 & 7) == 0 ? 7 : 0;
   const char* cache = static_cast<const char*>(p.cache);
 
-  // This thread's DMA work (waves 0..3): LDS chunk k*256 + tid of a tile is
-  // row-major (row, c) = divmod(., W/8) and holds global column
-  // c ^ (row & swz); chunks past the 32 rows are fillers that reread row 0.
+  // This thread's share of a tile: LDS chunk k*256 + tid is row-major
+  // (row, c) = divmod(., W/8) and holds global column c ^ (row & swz);
+  // chunks past the 32 rows are fillers that reread row 0.
   const int total_chunks = kTileTokens * w8;
   const int dtid = static_cast<int>(threadIdx.x) & 255;
   const int row0d = dtid / w8, col0d = dtid % w8;
   const int step_rows = 256 / w8, step_cols = 256 % w8;
 
+  // Dense rows with P a multiple of 32: every tile is one page's rows.
+  const bool contig = !sparse && p.P % kTileTokens == 0;
+
   // Wave 0's cursor over the workgroup's tiles.
-  int64_t cur_row = scal[1];
-  int cur_tir = static_cast<int>(scal[2]);
+  int64_t cur_row = row0;
+  int cur_tir = tir0;
   int cur_n = 0, cur_end = 0, cur_b = 0, seg_tir = cur_tir;
   int64_t g_cur = g0;
   int win_base = -kWinPages;
+  // Wave 0 reads metadata (lengths, positions, page table, index lists)
+  // while tiles are in flight.  Loads complete in issue order, so a value
+  // loaded here waits for every tile issued before it; each such value is
+  // consumed inside the branch that loads it (wave-uniform values through
+  // readfirstlane), so the steady path, which loads nothing, keeps exact
+  // wait counts for the tiles.
   auto enter_row = [&]() {
     cur_b = static_cast<int>(cur_row / p.T);
-    cur_end = row_end(p, cur_b, cur_row);
-    cur_n = row_tiles(p, cur_row);
+    cur_end = end_of(cur_row);
+    cur_n = tiles_of(cur_row);
     win_base = -kWinPages;  // window belongs to one sequence
   };
   auto load_window = [&](int first) {
@@ -520,7 +579,13 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
       const int pg = first + i;
       win[i] = pg < p.maxP ? p.table[static_cast<int64_t>(cur_b) * p.maxP + pg] : 0;
     }
+    __builtin_amdgcn_s_waitcnt(0);
     win_base = first;
+  };
+  auto clamp_phys = [&](int32_t phys) {
+    if (phys < 0) phys = 0;
+    if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
+    return phys;
   };
   // wave 0: metadata of the workgroup's tile t (called for t = 0, 1, ...).
   auto compute_offsets = [&](int t) {
@@ -533,79 +598,126 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
       fl |= kFlagLast;
       if (seg_tir == 0 && cur_tir == cur_n - 1) fl |= kFlagWhole;
     }
+    const int sl = t % kMetaSlots;
+    if (contig) {
+      // Dense row, P a multiple of 32: the tile is rows tok0 .. tok0 + 31
+      // of one page; rows past the visible end read row 0 (finite data,
+      // weight 0).
+      const int tok0 = kTileTokens * cur_tir;
+      const int pg = tok0 / p.P;
+      if (pg < win_base || pg >= win_base + kWinPages) load_window(pg);
+      const int32_t phys = clamp_phys(win[pg - win_base]);
+      const int nv = min(kTileTokens, cur_end - tok0);
+      if (lane == 0) {
+        tile_base[sl] = (static_cast<int64_t>(phys) * p.P + (tok0 - pg * p.P)) * p.W;
+        masks[sl] = nv >= kTileTokens ? 0xFFFFFFFFu : ((1u << nv) - 1u);
+        flags[sl] = fl;
+        tile_row[sl] = cur_row;
+      }
+    } else {
     const int count = sparse ? p.nk : cur_end;
     const int i = kTileTokens * cur_tir + lane;
     bool valid = lane < kTileTokens && i < count;
-    int tok = i;
-    int32_t phys = 0;
+    int64_t off = 0;
     if (sparse) {
-      tok = valid ? p.idx[cur_row * p.nk + i] : -1;
+      const int tok = valid ? p.idx[cur_row * p.nk + i] : -1;
       valid = valid && tok >= 0 && tok < cur_end;
-      if (valid) phys = p.table[static_cast<int64_t>(cur_b) * p.maxP + tok / p.P];
+      const int32_t phys = clamp_phys(valid ? p.table[static_cast<int64_t>(cur_b) * p.maxP + tok / p.P] : 0);
+      off = valid ? (static_cast<int64_t>(phys) * p.P + tok % p.P) * p.W : 0;
+      __builtin_amdgcn_s_waitcnt(0);  // consumed here: see above
     } else {
       const int first = (kTileTokens * cur_tir) / p.P;
       const int last = (min(kTileTokens * cur_tir + kTileTokens, count) - 1) / p.P;
       if (first < win_base || last >= win_base + kWinPages) load_window(first);
-      if (valid) phys = win[tok / p.P - win_base];
+      const int32_t phys = clamp_phys(valid ? win[i / p.P - win_base] : 0);
+      off = valid ? (static_cast<int64_t>(phys) * p.P + i % p.P) * p.W : 0;
     }
-    if (phys < 0) phys = 0;
-    if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
-    const int64_t off = valid ? (static_cast<int64_t>(phys) * p.P + tok % p.P) * p.W : 0;
     const uint32_t mask = static_cast<uint32_t>(__ballot(valid));
     const int fv = mask ? __builtin_ctz(mask) : 0;
     const int64_t dummy = __shfl(off, fv);
-    const int sl = t % kOffSlotsDma;
     if (lane < kTileTokens) offs[sl * kTileTokens + lane] = valid ? off : dummy;
     if (lane == 0) {
+      tile_base[sl] = -1;
       masks[sl] = mask;
       flags[sl] = fl;
       tile_row[sl] = cur_row;
-      if (cur_tir == 0 && hg == 0) {
-        // This workgroup holds the row's first tile: record its span.
-        const int64_t last_g = g_cur + cur_n - 1;
-        const int64_t last_w = ((last_g + 1) * p.wgs - 1) / G;
+    }
+    }
+    if (cur_tir == 0 && hg == 0) {
+      // This workgroup holds the row's first tile: record its span.  The
+      // wait keeps the stores from leaving loads and stores both pending on
+      // the steady path (the compiler would then wait for everything).
+      const int64_t last_g = g_cur + cur_n - 1;
+      const int64_t last_w = ((last_g + 1) * p.wgs - 1) / G;
+      if (lane == 0) {
         p.meta[2 * cur_row] = w;
         p.meta[2 * cur_row + 1] = static_cast<int>(last_w - w + 1);
       }
+      __builtin_amdgcn_s_waitcnt(0);
     }
     ++g_cur;
     ++cur_tir;
     if (cur_tir == cur_n && t + 1 < ntiles) {
       do {
         ++cur_row;
-      } while (row_tiles(p, cur_row) == 0);
+      } while (tiles_of(cur_row) == 0);
       cur_tir = 0;
       enter_row();
     }
   };
-  auto issue_dma = [&](int t) {
-    char* buf = ring + (t % kRing) * kTileBytes;
-    const int64_t* o = offs + (t % kOffSlotsDma) * kTileTokens;
-    const char* src[CPT];
+  // Loads tile t's chunks of this thread into registers; past the last
+  // tile (live false) every lane loads the first 16 bytes of the cache
+  // instead (one line per instruction), so every path issues the same loads
+  // and the compiler's wait counts stay exact.
+  auto issue = [&](int t, bool live, u32x4 (&dst)[CPT]) {
+    const int sl = t % kMetaSlots;
+    const int64_t tb = tile_base[sl];
     int row = row0d, col = col0d;
+    if (tb >= 0) {  // contiguous tile: row r at tb + r W
+      const int nv = __popc(masks[sl]);
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const bool real = dtid + k * 256 < total_chunks;
-      src[k] = cache + 2 * o[real ? row : 0] + (real ? 16 * (col ^ (row & swz)) : 0);
-      row += step_rows;
-      col += step_cols;
-      if (col >= w8) {
-        col -= w8;
-        ++row;
+      for (int k = 0; k < CPT; ++k) {
+        const bool real = dtid + k * 256 < total_chunks;
+        const int rr = real && row < nv ? row : 0;
+        const char* src = cache + 2 * (tb + static_cast<int64_t>(rr) * p.W) + (real ? 16 * (col ^ (row & swz)) : 0);
+        dst[k] = stream_load16(live ? src : cache);
+        row += step_rows;
+        col += step_cols;
+        if (col >= w8) {
+          col -= w8;
+          ++row;
+        }
+      }
+    } else {  // gathered rows
+      const int64_t* o = offs + sl * kTileTokens;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const bool real = dtid + k * 256 < total_chunks;
+        const char* src = cache + 2 * o[real ? row : 0] + (real ? 16 * (col ^ (row & swz)) : 0);
+        dst[k] = stream_load16(live ? src : cache);
+        row += step_rows;
+        col += step_cols;
+        if (col >= w8) {
+          col -= w8;
+          ++row;
+        }
       }
     }
+    // Keep each tile's loads in program order relative to the other tiles'
+    // (the waits assume the oldest tile completes first).
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Writes tile t's registers into its LDS buffer.
+  auto stage = [&](int t, const u32x4 (&src)[CPT]) {
+    char* buf = ring + (t & 1) * kTileBytes;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src[k]),
-                                       (__attribute__((address_space(3))) void*)(buf + (4 * k + wv) * 1024), 16,
-                                       0, 0);
+    for (int k = 0; k < CPT; ++k) *reinterpret_cast<u32x4*>(buf + 16 * (dtid + 256 * k)) = src[k];
   };
 
   // Query operand [q | q_rope | 0] of head h, chunks of 32 elements: Dc and
   // Dr are multiples of 8, so each lane's 8-element group lies in q, in
   // q_rope or past W (zero) and is one 16-byte load.
-  u32x4 qv[QCH];
-  auto load_query = [&](int64_t r) {
+  auto load_query = [&](int64_t r, u32x4 (&qv)[QCH]) {
     const char* qrow = static_cast<const char*>(p.q) + (r * p.H + (head_ok ? h : 0)) * p.Dc * 2;
     const char* rrow = static_cast<const char*>(p.qr) + (r * p.H + (head_ok ? h : 0)) * p.Dr * 2;
 #pragma unroll
@@ -619,25 +731,47 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
     }
   };
 
+  u32x4 st[PF][CPT];            // tiles in flight: tile t in st[t % PF]
+  u32x4 qv[QCH], qn[QCH];       // query of the current segment / of the next one
+  int qn_tile = -1;             // tile whose segment query sits in qn
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 acc[NBLKW][8];
 
-  if (ntiles > 0) {
-    if (wv == 0) {
-      enter_row();
-      for (int t = 0; t < kRing && t < ntiles; ++t) compute_offsets(t);
+  // One tile: stage it into LDS, refill its registers with tile j + PF,
+  // compute, and close the row segment on its last tile.  Segment bounds
+  // come from the per-tile flags wave 0 wrote (identical in every wave, so
+  // every wave runs the same barriers).
+  // Steps past the last tile (the rest of the last group of PF) only stage,
+  // synchronize and issue their placeholder loads.
+  auto step = [&](int j, u32x4 (&stu)[CPT]) {
+    stage(j, stu);
+    // Tile j is in LDS for every wave, and every wave is past tile j-1 (so
+    // the buffer written next, tile j-2's, is free).
+    lds_barrier();
+    const bool live = j < ntiles;
+    const int sl = j % kMetaSlots;
+    const int fl = live ? flags[sl] : 0;
+    const uint32_t mask = live ? masks[sl] : 0u;
+    const int64_t row = tile_row[sl];
+    if (j + PF < ntiles) {
+      const int sn = (j + PF) % kMetaSlots;
+      if (active && qn_tile < 0 && (flags[sn] & kFlagFirst)) {
+        load_query(tile_row[sn], qn);
+        qn_tile = j + PF;
+      }
     }
-    __syncthreads();
-    if (wv < kDmaWaves)
-      for (int t = 0; t < kRing - 1 && t < ntiles; ++t) issue_dma(t);
-  }
-  // Row segments of this workgroup in order; the tiles of a segment in the
-  // inner loop.  Segment bounds come from the per-tile flags wave 0 wrote
-  // (identical in every wave, so every wave runs the same barriers).
-  for (int j = 0; j < ntiles;) {
-    const int64_t row = tile_row[j % kOffSlotsDma];
-    if (active) {
-      load_query(row);
+    issue(j + PF, j + PF < ntiles, stu);
+    if ((fl & kFlagFirst) && active) {
+      if (qn_tile == j) {
+#pragma unroll
+        for (int i = 0; i < QCH; ++i) qv[i] = qn[i];
+        qn_tile = -1;
+      } else if (j > 0) {
+        // Two segments began within PF tiles: load now and wait (this path
+        // only), so that qv is never pending on the steady path.
+        load_query(row, qv);
+        __builtin_amdgcn_s_waitcnt(0);
+      }
       m_run = -INFINITY;
       l_run = 0.f;
 #pragma unroll
@@ -645,115 +779,99 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[bb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    int fl;
-    do {
-      // Tile j's DMA done in every wave (tiles j+1 .. j+kRing-2 may fly
-      // on), and every wave is past tile j-1's compute.
-      if (ntiles - 1 - j >= kRing - 2)
-        dma_barrier<(kRing - 2) * CPT>();
-      else
-        dma_barrier<0>();
-      if (wv < kDmaWaves && j + kRing - 1 < ntiles) issue_dma(j + kRing - 1);  // into tile j-1's buffer
-      const int sl = j % kOffSlotsDma;
-      fl = flags[sl];
-      const uint32_t mask = masks[sl];
-      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      if (mask != 0u) {
-        const char* buf = ring + (j % kRing) * kTileBytes;
-        // S^T = C . Qcat^T for tokens 0-15 (s0) and 16-31 (s1).  The DS
-        // waves of a head tile take the 32-element chunks c = slice + DS i
-        // and add their partial scores through LDS (in slice order, so every
-        // wave of the head tile gets the same bits).  All 2*CPT chunks are
-        // covered: the query is zero past W, and a chunk past W reads the
-        // next row or the tile's filler chunks (finite cache data, inside
-        // the tile buffer since W/8 <= 8*CPT).
-        if (active) {
-          const int ra = r16, rb = 16 + r16;
+    const char* buf = ring + (j & 1) * kTileBytes;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    if (mask != 0u) {
+      // S^T = C . Qcat^T for tokens 0-15 (s0) and 16-31 (s1).  The DS
+      // waves of a head tile take the 32-element chunks c = slice + DS i
+      // and add their partial scores through LDS (in slice order, so every
+      // wave of the head tile gets the same bits).  All 2*CPT chunks are
+      // covered: the query is zero past W, and a chunk past W reads the
+      // next row or the tile's filler chunks (finite cache data, inside
+      // the tile buffer since W/8 <= 8*CPT).
+      if (active) {
+        const int ra = r16, rb = 16 + r16;
 #pragma unroll
-          for (int i = 0; i < QCH; ++i) {
-            const int c = slice + DS * i;
-            if (KMAX % DS == 0 || c < KMAX) {
-              const int c4 = 4 * c + q4;
-              const u32x4 a0 = *reinterpret_cast<const u32x4*>(buf + 16 * (ra * w8 + (c4 ^ (ra & swz))));
-              const u32x4 a1 = *reinterpret_cast<const u32x4*>(buf + 16 * (rb * w8 + (c4 ^ (rb & swz))));
-              s0 = Ops::mma32(a0, qv[i], s0);
-              s1 = Ops::mma32(a1, qv[i], s1);
-            }
-          }
-        }
-        if constexpr (DS > 1) {
-          sx[(wv * 64 + lane) * 2] = s0;
-          sx[(wv * 64 + lane) * 2 + 1] = s1;
-          lds_barrier();
-          s0 = f32x4{0.f, 0.f, 0.f, 0.f};
-          s1 = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int sl2 = 0; sl2 < DS; ++sl2) {
-            const int src = ht + p.nht * sl2;
-            s0 += sx[(src * 64 + lane) * 2];
-            s1 += sx[(src * 64 + lane) * 2 + 1];
+        for (int i = 0; i < QCH; ++i) {
+          const int c = slice + DS * i;
+          if (KMAX % DS == 0 || c < KMAX) {
+            const int c4 = 4 * c + q4;
+            const u32x4 a0 = *reinterpret_cast<const u32x4*>(buf + 16 * (ra * w8 + (c4 ^ (ra & swz))));
+            const u32x4 a1 = *reinterpret_cast<const u32x4*>(buf + 16 * (rb * w8 + (c4 ^ (rb & swz))));
+            s0 = Ops::mma32(a0, qv[i], s0);
+            s1 = Ops::mma32(a1, qv[i], s1);
           }
         }
       }
-      if (active && mask != 0u) {
-        const char* buf = ring + (j % kRing) * kTileBytes;
-        // Online softmax in log2 units.  The accumulator is rescaled only on
-        // tiles that raise some head's running max (a wave-uniform branch;
-        // rare once the max has been seen), so every probability is <= 1 and
-        // the largest score's is exactly 1 in the 16-bit PV operand.
-        float x[8];
+      if constexpr (DS > 1) {
+        sx[(wv * 64 + lane) * 2] = s0;
+        sx[(wv * 64 + lane) * 2 + 1] = s1;
+        lds_barrier();
+        s0 = f32x4{0.f, 0.f, 0.f, 0.f};
+        s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[i] = (mask >> (4 * q4 + i)) & 1u ? s0[i] * p.sl2 : -INFINITY;
-          x[4 + i] = (mask >> (16 + 4 * q4 + i)) & 1u ? s1[i] * p.sl2 : -INFINITY;
-        }
-        float mx = x[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
-        mx = max_over_lane_groups(mx);
-        const bool move = mx > m_run;
-        if (__ballot(move)) {
-          const float alpha = move ? fast_exp2(m_run - mx) : 1.f;
-          m_run = move ? mx : m_run;
-          l_run *= alpha;
-#pragma unroll
-          for (int bb = 0; bb < NBLKW; ++bb)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[bb][e] *= alpha;
-        }
-        // The denominator sums the same 16-bit probabilities the PV product
-        // uses, so the output is an exactly normalized average of values.
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float pr[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pr[e] = fast_exp2(x[e] - m_use);
-        const u32x4 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3]), Ops::pack2(pr[4], pr[5]),
-                          Ops::pack2(pr[6], pr[7])};
-        l_run += (Ops::sum2(pb[0]) + Ops::sum2(pb[1])) + (Ops::sum2(pb[2]) + Ops::sum2(pb[3]));
-
-        // O^T += C[:, slice]^T . P^T
-#pragma unroll
-        for (int bb = 0; bb < NBLKW; ++bb) {
-          if (blk0 + bb < nblk) {
-            const int cc = min(16 * (blk0 + bb) + r16, p.Dc / 8 - 1);
-            u32x4 raw[8];
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              const int tok = t < 4 ? 4 * q4 + t : 16 + 4 * q4 + (t - 4);
-              raw[t] = *reinterpret_cast<const u32x4*>(buf + 16 * (tok * w8 + (cc ^ (tok & swz))));
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              acc[bb][e] = Ops::mma32(transpose8x8_col_b16(raw, e), pb, acc[bb][e]);
-          }
+        for (int sl2 = 0; sl2 < DS; ++sl2) {
+          const int src = ht + p.nht * sl2;
+          s0 += sx[(src * 64 + lane) * 2];
+          s1 += sx[(src * 64 + lane) * 2 + 1];
         }
       }
-      if (wv == 0 && j + kRing < ntiles) compute_offsets(j + kRing);
-      ++j;
-    } while (!(fl & kFlagLast) && j < ntiles);  // tile ntiles-1 always carries kFlagLast
+    }
+    if (active && mask != 0u) {
+      // Online softmax in log2 units.  The accumulator is rescaled only on
+      // tiles that raise some head's running max (a wave-uniform branch;
+      // rare once the max has been seen), so every probability is <= 1 and
+      // the largest score's is exactly 1 in the 16-bit PV operand.
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = (mask >> (4 * q4 + i)) & 1u ? s0[i] * p.sl2 : -INFINITY;
+        x[4 + i] = (mask >> (16 + 4 * q4 + i)) & 1u ? s1[i] * p.sl2 : -INFINITY;
+      }
+      float mx = x[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
+      mx = max_over_lane_groups(mx);
+      const bool move = mx > m_run;
+      if (__ballot(move)) {
+        const float alpha = move ? fast_exp2(m_run - mx) : 1.f;
+        m_run = move ? mx : m_run;
+        l_run *= alpha;
+#pragma unroll
+        for (int bb = 0; bb < NBLKW; ++bb)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[bb][e] *= alpha;
+      }
+      // The denominator sums the same 16-bit probabilities the PV product
+      // uses, so the output is an exactly normalized average of values.
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      float pr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pr[e] = fast_exp2(x[e] - m_use);
+      const u32x4 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3]), Ops::pack2(pr[4], pr[5]),
+                        Ops::pack2(pr[6], pr[7])};
+      l_run += (Ops::sum2(pb[0]) + Ops::sum2(pb[1])) + (Ops::sum2(pb[2]) + Ops::sum2(pb[3]));
 
-    if (active && head_ok) {
+      // O^T += C[:, slice]^T . P^T
+#pragma unroll
+      for (int bb = 0; bb < NBLKW; ++bb) {
+        if (blk0 + bb < nblk) {
+          const int cc = min(16 * (blk0 + bb) + r16, p.Dc / 8 - 1);
+          u32x4 raw[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int tok = t < 4 ? 4 * q4 + t : 16 + 4 * q4 + (t - 4);
+            raw[t] = *reinterpret_cast<const u32x4*>(buf + 16 * (tok * w8 + (cc ^ (tok & swz))));
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[bb][e] = Ops::mma32(transpose8x8_col_b16(raw, e), pb, acc[bb][e]);
+        }
+      }
+    }
+
+    if ((fl & kFlagLast) && active) {
       const float l = sum_over_lane_groups(l_run);
+      if (head_ok) {
       if (fl & kFlagWhole) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
         S* orow = static_cast<S*>(p.out) + (row * p.H + h) * p.Dc;
@@ -765,8 +883,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
             if (blk0 + bb < nblk && dc0 < p.Dc) {
               uint32_t wd[4];
 #pragma unroll
-              for (int e = 0; e < 8; e += 2)
-                wd[e / 2] = Ops::pack2(acc[bb][e][i] * inv, acc[bb][e + 1][i] * inv);
+              for (int e = 0; e < 8; e += 2) wd[e / 2] = Ops::pack2(acc[bb][e][i] * inv, acc[bb][e + 1][i] * inv);
               *reinterpret_cast<u32x4*>(orow + dc0) = u32x4{wd[0], wd[1], wd[2], wd[3]};
             }
           }
@@ -787,8 +904,453 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
             }
           }
       }
+      }
+      // Stores pending next to the tile loads would make every later wait
+      // a full drain; drain once here (segment ends only) instead.
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    if (wv == 0 && j + PF + 1 < ntiles) compute_offsets(j + PF + 1);
+  };
+
+  // A tile's registers are waited for by the compiler, and its wait counts
+  // stay exact (not vmcnt(0)) only where every path into a wait issued the
+  // same loads: the loop runs whole groups of PF steps with unconditional
+  // issues.
+  if (ntiles > 0) {
+    if (wv == 0) {
+      enter_row();
+      for (int t = 0; t < PF + 1 && t < ntiles; ++t) compute_offsets(t);
+    }
+    __syncthreads();
+    // Queries first (the oldest loads): the first segment's, and the next
+    // segment's when it starts within the first PF tiles.
+    if (active) {
+      load_query(tile_row[0], qv);
+      for (int t = 1; t < PF && t < ntiles; ++t)
+        if (flags[t % kMetaSlots] & kFlagFirst) {
+          load_query(tile_row[t % kMetaSlots], qn);
+          qn_tile = t;
+          break;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < PF; ++u) issue(u, u < ntiles, st[u]);
+    for (int j0 = 0; j0 < ntiles; j0 += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) step(j0 + u, st[u]);
     }
   }
+}
+
+// ----------------------------------------------------------------------------
+// Paged latent attention, wave-streamed kernel: dense rows, latent width
+// 128*NB, rope width 32*RC, up to 16 heads per head group
+// ----------------------------------------------------------------------------
+
+constexpr int kSubTokens = 16;        // tokens per wave tile
+constexpr int kWaveRows = 1024;       // query rows the prologue scans in LDS
+constexpr int kWaveListTiles = 1024;  // tiles of one workgroup's range
+constexpr int kWavePF = 2;            // tiles in flight per wave
+
+template <int NB, int RC>
+struct WaveLayout {
+  static constexpr int kDc = 128 * NB;
+  static constexpr int kW = kDc + 32 * RC;
+  static constexpr int kChunks = 4 * NB + RC;        // 32-element QK chunks
+  static constexpr int kStride = 2 * kW + 16;        // padded LDS row (bank spread)
+  static constexpr int kBuf = kSubTokens * kStride;  // one wave's tile buffer
+  static constexpr int kRopeBytes = 4 * RC;          // rope bytes per lane per row
+};
+
+__host__ __device__ constexpr size_t mla_wave_lds_bytes(int nb, int rc) {
+  return 5 * static_cast<size_t>(kSubTokens) * (2 * (128 * nb + 32 * rc) + 16)  // wave tiles, query
+         + 4 * 64 * 32 * 4                                                      // merge exchange
+         + 4 * 16 * 2 * 4                                                       // merge m, l
+         + static_cast<size_t>(kWaveRows) * (4 + 4 + 8)                         // row tiles, ends, prefix
+         + static_cast<size_t>(kWaveListTiles) * (8 + 4 + 4)                    // tile bases, counts, rows
+         + 256;
+}
+
+// Registers of one tile in flight: lane (r16, q4) holds rows 4 q4 + i of
+// latent columns 128 blk + 8 r16 .. +7 and rope columns Dc + 2 RC r16 ..
+template <int NB, int RC>
+struct WaveTile {
+  u32x4 c[NB][4];
+  uint32_t r[4][RC];
+};
+
+// Stream-K like mla_attend_mfma_kernel (same grid, meta, slots and merge),
+// over 16-token tiles.  Each workgroup's range of tiles is dealt round-robin
+// to its 4 waves (tile g to wave (g - g0) % 4); each wave streams its tiles
+// on its own, with no per-tile barrier:
+//   load     the 16 cache rows of a tile (one page: P % 16 == 0) into
+//            registers, kWavePF tiles ahead, in the layout of the PV operand
+//            (4 rows x 16 bytes per lane per latent block); the row's query
+//            enters the same stream as a 16-row pseudo-tile (heads for
+//            tokens) when a wave reaches a new row, so a row change never
+//            waits for the tiles in flight (loads complete in issue order).
+//   QK       the tile is written to the wave's LDS buffer (rows padded by 16
+//            bytes) and read back as A = rows (tokens) x 32 columns; B = the
+//            query chunks held in registers -> S^T[token 4 q4 + i][head r16].
+//   softmax  as mla_attend_mfma_kernel (exact running max, rescale only when
+//            it rises, denominator over the 16-bit weights).
+//   PV       16x16x16 with A = C^T from 4 LDS rows (8x8 transposes by byte
+//            permutes) and B = P^T, the lane's own 4 weights; C tile (blk, e)
+//            row r <-> latent column 128 blk + 8 r + e.
+// At the end of a row segment the 4 waves' states are merged through LDS
+// (the only barriers of the main loop; every wave merges every row of the
+// range in order): common max, rescale, then per 128-column block one wave
+// sums the 4 accumulators and writes the output (whole row) or the partial.
+// The prologue scans the rows' lengths into LDS, lists this range's tiles
+// (row, page base, visible count: one page-table round trip for all of
+// them), writes meta, gtotal and the empty rows.
+template <int DT, int NB, int RC>
+__global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaParams p) {
+  using E = Elem<DT>;
+  using Ops = MfmaOps<DT>;
+  using S = typename E::S;
+  using Lay = WaveLayout<NB, RC>;
+  using Tile = WaveTile<NB, RC>;
+  constexpr int PF = kWavePF;
+  constexpr int KC = Lay::kChunks;
+  extern __shared__ __align__(16) char smem[];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, q4 = lane >> 4;
+
+  const int L = blockIdx.x;
+  const int hg = (L >> 3) % p.head_groups;
+  const int w = ((L >> 3) / p.head_groups) * 8 + (L & 7);
+  if (w >= p.wgs) return;  // whole workgroup: uniform
+
+  char* tbuf = smem + wv * Lay::kBuf;                                     // this wave's tile
+  char* qbuf = smem + 4 * Lay::kBuf;                                      // the current row's query
+  float* red = reinterpret_cast<float*>(smem + 5 * Lay::kBuf);          // [4][64][32]
+  float* ml = red + 4 * 64 * 32;                                          // [4][16][2]
+  int* rt = reinterpret_cast<int*>(ml + 4 * 16 * 2);                      // [rows] tiles
+  int* re = rt + kWaveRows;                                               // [rows] visible end
+  int64_t* incl = reinterpret_cast<int64_t*>(re + kWaveRows);            // [rows] prefix of tiles
+  int64_t* lbase = incl + kWaveRows;                                      // [tiles] page row 0 offset
+  int* lnv = reinterpret_cast<int*>(lbase + kWaveListTiles);              // [tiles] visible rows
+  int* lrow = lnv + kWaveListTiles;                                       // [tiles] query row
+
+  const int rows = p.B * p.T;  // <= kWaveRows (host check)
+  const int h0 = 16 * hg;
+  const int nh = min(16, p.H - h0);
+  const int h = h0 + r16;
+  const bool head_ok = r16 < nh;
+  const char* cache = static_cast<const char*>(p.cache);
+
+  // --- Prologue -----------------------------------------------------------
+  for (int r = tid; r < rows; r += kAttendThreads) {
+    const int end = row_end(p, r / p.T, r);
+    re[r] = end;
+    rt[r] = (end + kSubTokens - 1) / kSubTokens;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    int64_t carry = 0;
+    for (int base = 0; base < rows; base += 64) {
+      const int r = base + lane;
+      const int64_t n = r < rows ? rt[r] : 0;
+      const int64_t v = carry + wave_incl_scan_i64(n, lane);
+      if (r < rows) incl[r] = v;
+      carry = __shfl(v, 63);
+    }
+  }
+  __syncthreads();
+  const int64_t G = incl[rows - 1];
+  const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
+  const int64_t g1 = static_cast<int64_t>(w + 1) * G / p.wgs;
+  const int nt = static_cast<int>(g1 - g0);  // <= kWaveListTiles (host check)
+  if (w == 0 && hg == 0 && tid == 0) *p.gtotal = G;
+  auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * p.wgs - 1) / G); };
+  // This range's tiles: row (binary search of the prefix), page base, rows.
+  for (int t = tid; t < nt; t += kAttendThreads) {
+    const int64_t g = g0 + t;
+    int lo = 0, hi = rows - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (incl[mid] > g) hi = mid; else lo = mid + 1;
+    }
+    const int r = lo;
+    const int tir = static_cast<int>(g - (incl[r] - rt[r]));
+    const int tok0 = kSubTokens * tir;
+    const int pg = tok0 / p.P;
+    int32_t phys = p.table[static_cast<int64_t>(r / p.T) * p.maxP + pg];
+    if (phys < 0) phys = 0;
+    if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
+    lbase[t] = (static_cast<int64_t>(phys) * p.P + (tok0 - pg * p.P)) * Lay::kW;
+    lnv[t] = min(kSubTokens, re[r] - tok0);
+    lrow[t] = r;
+    if (tir == 0 && hg == 0) {
+      // This workgroup holds the row's first tile: record its span.
+      p.meta[2 * r] = w;
+      p.meta[2 * r + 1] = wg_of(incl[r] - 1) - w + 1;
+    }
+  }
+  // Rows with no tile: zeros from workgroup (row % wgs), meta {0, 0}.
+  for (int r = w; r < rows; r += p.wgs) {
+    if (rt[r] != 0) continue;
+    S* orow = static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h0) * Lay::kDc;
+    for (int i = tid; i < nh * Lay::kDc / 8; i += kAttendThreads)
+      *reinterpret_cast<u32x4*>(orow + 8 * i) = u32x4{0u, 0u, 0u, 0u};
+    if (hg == 0 && tid == 0) {
+      p.meta[2 * r] = 0;
+      p.meta[2 * r + 1] = 0;
+    }
+  }
+  __syncthreads();
+
+  // --- Per-wave item stream -------------------------------------------------
+  // Items in order: for each row of this wave's tiles, the query pseudo-tile,
+  // then the row's tiles.  Past the end, placeholder loads of the first
+  // cache bytes keep every path's load count equal (exact wait counts).
+  constexpr int kNone = 0, kQuery = 1, kTile = 2;
+  int is_k = 0;        // next tile ordinal of this wave: g = g0 + wv + 4 k
+  int is_row = -1;     // row of the last issued item
+  auto issue = [&](Tile& dst, int& kind, int& row, int& nv) {
+    const int t = wv + 4 * is_k;
+    kind = kNone;
+    row = -1;
+    nv = 0;
+    if (t < nt) {
+      row = lrow[t];
+      if (row != is_row) {
+        kind = kQuery;
+        is_row = row;
+      } else {
+        kind = kTile;
+        nv = lnv[t];
+        ++is_k;
+      }
+    }
+    // Row offsets (elements) of rows 4 q4 + i and the base of each column.
+    const char* lat;
+    const char* rop;
+    int64_t rs_l, rs_r;  // row strides in bytes
+    int nrow;            // valid rows (others reread row 0)
+    if (kind == kTile) {
+      const int64_t b = lbase[t];
+      lat = cache + 2 * b;
+      rop = cache + 2 * (b + Lay::kDc);
+      rs_l = rs_r = 2 * static_cast<int64_t>(Lay::kW);
+      nrow = nv;
+    } else if (kind == kQuery) {
+      lat = static_cast<const char*>(p.q) + (static_cast<int64_t>(row) * p.H + h0) * Lay::kDc * 2;
+      rop = static_cast<const char*>(p.qr) + (static_cast<int64_t>(row) * p.H + h0) * (32 * RC) * 2;
+      rs_l = 2 * Lay::kDc;
+      rs_r = 2 * 32 * RC;
+      nrow = nh;
+    } else {
+      lat = rop = cache;
+      rs_l = rs_r = 0;
+      nrow = 1;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 4 * q4 + i < nrow ? 4 * q4 + i : 0;
+      const char* lrow_p = lat + rr * rs_l + 16 * r16;
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk) dst.c[blk][i] = stream_load16(lrow_p + 256 * blk);
+      const char* rp = rop + rr * rs_r + Lay::kRopeBytes * r16;
+      if constexpr (RC == 1) {
+        dst.r[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(rp));
+      } else if constexpr (RC == 2) {
+        const u32x2 x = stream_load8(rp);
+        dst.r[i][0] = x[0];
+        dst.r[i][1] = x[1];
+      } else {
+        const u32x4 x = stream_load16(rp);
+#pragma unroll
+        for (int k = 0; k < RC; ++k) dst.r[i][k] = x[k];
+      }
+    }
+    // Keep each item's loads in program order relative to the others'.
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Writes an item's rows (4 q4 + i) into an LDS buffer.
+  auto stage = [&](const Tile& src, int valid, char* buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = 4 * q4 + i < valid;
+      char* rowp = buf + (4 * q4 + i) * Lay::kStride;
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk)
+        *reinterpret_cast<u32x4*>(rowp + 256 * blk + 16 * r16) = ok ? src.c[blk][i] : u32x4{0u, 0u, 0u, 0u};
+      char* rp = rowp + 2 * Lay::kDc + Lay::kRopeBytes * r16;
+      if constexpr (RC == 1) {
+        *reinterpret_cast<uint32_t*>(rp) = ok ? src.r[i][0] : 0u;
+      } else if constexpr (RC == 2) {
+        *reinterpret_cast<u32x2*>(rp) = ok ? u32x2{src.r[i][0], src.r[i][1]} : u32x2{0u, 0u};
+      } else {
+        *reinterpret_cast<u32x4*>(rp) = ok ? u32x4{src.r[i][0], src.r[i][1], src.r[i][2], src.r[i][3]}
+                                           : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  // --- State and the row merge ----------------------------------------------
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 acc[NB][8];
+  auto reset = [&]() {
+    m_run = -INFINITY;
+    l_run = 0.f;
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[bb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  reset();
+  // Rows of the range in order; merged_row: the next one to merge.
+  int merge_row = nt > 0 ? lrow[0] : rows;
+  auto merge = [&](int r) {
+    const float lw = sum_over_lane_groups(l_run);
+    if (q4 == 0) {
+      ml[(wv * 16 + r16) * 2] = m_run;
+      ml[(wv * 16 + r16) * 2 + 1] = lw;
+    }
+    lds_barrier();
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) M = fmaxf(M, ml[(v * 16 + r16) * 2]);
+    float Lt = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float mv = ml[(v * 16 + r16) * 2];
+      if (mv != -INFINITY) Lt += ml[(v * 16 + r16) * 2 + 1] * fast_exp2(mv - M);
+    }
+    const float sc = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
+    const int64_t first_tile = incl[r] - rt[r];
+    const bool whole = first_tile >= g0 && incl[r] <= g1;
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      // Every wave deposits its scaled block bb; wave bb % 4 sums them.
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<f32x4*>(red + ((wv * 64 + lane) * 32 + 4 * e)) = acc[bb][e] * sc;
+      lds_barrier();
+      if (wv == bb % 4 && head_ok) {
+        f32x4 o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          o[e] = *reinterpret_cast<const f32x4*>(red + ((0 * 64 + lane) * 32 + 4 * e));
+#pragma unroll
+          for (int v = 1; v < 4; ++v) o[e] += *reinterpret_cast<const f32x4*>(red + ((v * 64 + lane) * 32 + 4 * e));
+        }
+        if (whole) {
+          const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+          S* orow = static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * Lay::kDc;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            uint32_t wd[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) wd[e / 2] = Ops::pack2(o[e][i] * inv, o[e + 1][i] * inv);
+            *reinterpret_cast<u32x4*>(orow + 128 * bb + 32 * q4 + 8 * i) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+          }
+        } else {
+          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(Lay::kDc + 2);
+          if (bb == 0 && q4 == 0) {
+            pr[0] = M == -INFINITY ? -INFINITY : M * kLn2;
+            pr[1] = Lt;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pr[2 + 128 * bb + 32 * q4 + 8 * i + e] = o[e][i];
+        }
+      }
+      lds_barrier();
+    }
+    // Stores pending next to the loads in flight would make every later
+    // wait a full drain; drain here (row ends only) instead.
+    __builtin_amdgcn_s_waitcnt(0);
+    reset();
+  };
+  // Merges the rows before row r (r = rows: all of them).
+  auto merge_before = [&](int r) {
+    while (merge_row < r) {
+      merge(merge_row);
+      const int64_t nxt = incl[merge_row];  // first tile of the following rows
+      merge_row = nxt < g1 ? lrow[nxt - g0] : rows;
+    }
+  };
+
+  // --- Main loop --------------------------------------------------------------
+  Tile st[PF];
+  int s_kind[PF], s_row[PF], s_nv[PF];
+#pragma unroll
+  for (int u = 0; u < PF; ++u) issue(st[u], s_kind[u], s_row[u], s_nv[u]);
+  int pending = 0;
+#pragma unroll
+  for (int u = 0; u < PF; ++u) pending += s_kind[u] != kNone;
+
+  auto step = [&](Tile& stu, int& skind, int& srow, int& snv) {
+    const int kind = skind, row = srow, nv = snv;
+    if (kind == kQuery) {
+      // The row's query goes to the shared slot: every wave with tiles in
+      // the row writes the same rows, after the previous row's merge (no
+      // wave still reads the old query).
+      merge_before(row);
+      stage(stu, nh, qbuf);
+    } else if (kind == kTile) {
+      stage(stu, kSubTokens, tbuf);
+    }
+    issue(stu, skind, srow, snv);
+    pending += (skind != kNone) - (kind != kNone);
+    if (kind == kTile) {
+      // A = cache rows (tokens), B = query rows (heads), both row r16.
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(tbuf + r16 * Lay::kStride + 64 * c + 16 * q4);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(qbuf + r16 * Lay::kStride + 64 * c + 16 * q4);
+        s = Ops::mma32(a, b, s);
+      }
+      float x[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = 4 * q4 + i < nv ? s[i] * p.sl2 : -INFINITY;
+      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      mx = max_over_lane_groups(mx);
+      const bool move = mx > m_run;
+      if (__ballot(move)) {
+        const float alpha = move ? fast_exp2(m_run - mx) : 1.f;
+        m_run = move ? mx : m_run;
+        l_run *= alpha;
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[bb][e] *= alpha;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - m_use);
+      const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
+      l_run += Ops::sum2(pb[0]) + Ops::sum2(pb[1]);
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) {
+        u32x4 raw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          raw[i] = *reinterpret_cast<const u32x4*>(tbuf + (4 * q4 + i) * Lay::kStride + 256 * bb + 16 * r16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int wd = e >> 1;
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const u32x2 a = {__builtin_amdgcn_perm(raw[1][wd], raw[0][wd], sel),
+                           __builtin_amdgcn_perm(raw[3][wd], raw[2][wd], sel)};
+          acc[bb][e] = Ops::pv(a, pb, acc[bb][e]);
+        }
+      }
+    }
+  };
+  while (pending > 0) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) step(st[u], s_kind[u], s_row[u], s_nv[u]);
+  }
+  merge_before(rows);
 }
 
 // Merge of the stream-K partials: one wave per (row, head) of a row split
@@ -1075,6 +1637,7 @@ struct AttendPlan {
   int nblk, cpt, kch, head_groups, nht, ds, wgs;
   size_t lds;
   int splits;  // VALU kernel
+  bool wave;   // MFMA path through mla_attend_wave_kernel
 };
 
 // Smallest instantiated DMA-chunk count covering ceil(W/64), 0 if none.
@@ -1111,6 +1674,22 @@ AttendPlan plan_attend(const AttendShape& a, int forced, int flags) {
     // One resident workgroup per CU (the LDS ring), shared by the head groups.
     pl.wgs = forced > 0 ? forced : std::max(1, device_cus() / pl.head_groups);
     pl.splits = 1;
+    // The wave-streamed kernel: dense rows, Dc 512 / Dr 64 (instantiated),
+    // pages of whole 16-token tiles, up to 16 heads, rows and tiles per
+    // workgroup within its LDS lists.
+    const int64_t gmax = rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens);
+    const size_t wlds = mla_wave_lds_bytes(4, 2);
+    if ((flags & QD_FLAG_MLA_STAGED) == 0 && a.Dc == 512 && a.Dr == 64 && a.nk < 0 && a.P % kSubTokens == 0 &&
+        a.H <= 16 && rows <= kWaveRows && wlds <= static_cast<size_t>(device_max_lds())) {
+      const int wgs = forced > 0 ? forced : std::max(1, device_cus());
+      if ((gmax + wgs - 1) / wgs + 1 <= kWaveListTiles) {
+        pl.wave = true;
+        pl.nht = 1;
+        pl.head_groups = 1;
+        pl.wgs = wgs;
+        pl.lds = wlds;
+      }
+    }
   } else if (forced > 0) {
     pl.splits = forced;
   } else {
@@ -1151,6 +1730,20 @@ hipError_t launch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_
   });
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(64 * pl.nht * pl.ds), pl.lds, st, prm);
+  return hipSuccess;
+}
+
+template <int DT>
+hipError_t launch_attend_wave(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
+  auto fn = mla_attend_wave_kernel<DT, 4, 2>;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [&] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(mla_wave_lds_bytes(4, 2)));
+  });
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kAttendThreads), pl.lds, st, prm);
   return hipSuccess;
 }
 
@@ -1215,8 +1808,12 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   if (pl.mfma) {
     const int64_t grid = (static_cast<int64_t>(pl.wgs) + 7) / 8 * 8 * pl.head_groups;
     if (grid > 2147483647LL) return mla_fail(nullptr, 0, "mla_attend grid exceeds launch limits");
-    err = a.dtype == QD_DTYPE_BF16 ? dispatch_attend_mfma<QD_DTYPE_BF16>(prm, pl, grid, st)
-                                   : dispatch_attend_mfma<QD_DTYPE_F16>(prm, pl, grid, st);
+    if (pl.wave)
+      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_wave<QD_DTYPE_BF16>(prm, pl, grid, st)
+                                     : launch_attend_wave<QD_DTYPE_F16>(prm, pl, grid, st);
+    else
+      err = a.dtype == QD_DTYPE_BF16 ? dispatch_attend_mfma<QD_DTYPE_BF16>(prm, pl, grid, st)
+                                     : dispatch_attend_mfma<QD_DTYPE_F16>(prm, pl, grid, st);
   } else {
     const int64_t waves = rows * a.H * pl.splits;
     const int64_t grid = (waves + 3) / 4;
@@ -1455,7 +2052,7 @@ int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope
   const AttendPlan pl = plan_attend(a, splits, flags);
   if (out_splits) *out_splits = pl.mfma ? pl.wgs : pl.splits;
   if (head_groups) *head_groups = pl.mfma ? pl.head_groups : 0;
-  return pl.mfma ? 1 : 0;
+  return pl.mfma ? (pl.wave ? 2 : 1) : 0;
 }
 
 int qd_mla_attend(const void* q, const void* q_rope, const void* cache, const int32_t* block_table,

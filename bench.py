@@ -287,14 +287,14 @@ def mla_mode(args) -> None:
     a_gbs = a_bytes / (a_ms * 1e-3) / 1e9
     a_flops = 2 * rows * H * (Dc + Dr + Dc)
     a_tflops = a_flops / (a_ms * 1e-3) / 1e12
-    kname = "mla_attend_mfma_kernel" if kind == 1 else "mla_attend_generic_kernel"
-    if kind == 1:
+    kname = {2: "mla_attend_wave_kernel", 1: "mla_attend_mfma_kernel"}.get(kind, "mla_attend_generic_kernel")
+    if kind >= 1:
         kernels = kname + "+mla_merge_sk_kernel"
     else:
         kernels = kname + ("+mla_merge_kernel" if splits > 1 else "")
     log(f"{kernels}: {a_ms * 1e3:.2f} us, {a_gbs:.1f} GB/s ({100 * a_gbs / PEAK_HBM_GBS:.1f}% of HBM peak), "
         f"{a_tflops:.1f} TFLOP/s ({100 * a_tflops / PEAK_MFMA_BF16_TFLOPS:.1f}% of bf16 MFMA peak); "
-        f"{'workgroups' if kind == 1 else 'splits'}={splits} head_groups={groups}")
+        f"{'workgroups' if kind >= 1 else 'splits'}={splits} head_groups={groups}")
     result = {
         "metric": "paged MLA decode µs/call and achieved HBM GB/s, 1 MI355X",
         "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 3),
@@ -310,7 +310,7 @@ def mla_mode(args) -> None:
                      "traffic": profiled_traffic(kname, cfg.name), "duration_us": round(a_ms * 1e3, 3),
                      "algorithmic_bytes": a_bytes, "mfma_tflops": round(a_tflops, 2),
                      "mfma_frac": round(a_tflops / PEAK_MFMA_BF16_TFLOPS, 4),
-                     ("workgroups" if kind == 1 else "splits"): splits, "head_groups": groups,
+                     ("workgroups" if kind >= 1 else "splits"): splits, "head_groups": groups,
                      "note": "latent attention on the absorbed query (qd_mla_attend: attention kernel + merge of "
                              "rows split across workgroups), HIP events on its stream; "
                              f"{a_flops / a_bytes:.0f} flop/byte against a bf16 ridge of "

@@ -59,10 +59,13 @@ enum {
  * the message of the last failure on the calling thread. */
 enum { QD_OK = 0, QD_ERR_INVALID_VALUE = 1 };
 
-/* qd_gqa_decode_launch flags. */
+/* Kernel-selection flags (qd_gqa_decode_launch, qd_mla_*). */
 enum {
   /* Use the portable VALU kernel even where the MFMA kernel applies. */
-  QD_FLAG_FORCE_GENERIC = 1
+  QD_FLAG_FORCE_GENERIC = 1,
+  /* MLA attention: use the workgroup-staged MFMA kernel even where the
+   * wave-streamed one applies (testing and comparison). */
+  QD_FLAG_MLA_STAGED = 2
 };
 
 /* Shape/placement descriptor of one tensor, for validation only. */
@@ -296,10 +299,12 @@ size_t qd_mla_attend_workspace_bytes(int batch, int q_len, int heads, int latent
                                      int block_size, int max_pages, int num_indices, int dtype, int splits,
                                      int flags);
 
-/* The plan qd_mla_attend would use: returns 1 for the MFMA kernel
- * (*out_splits = stream-K workgroups per head group, *head_groups = head
- * groups), 0 for the VALU kernel (*out_splits = context splits per row,
- * *head_groups = 0), -1 for invalid shapes. */
+/* The plan qd_mla_attend would use: returns 2 for the wave-streamed MFMA
+ * kernel (dense rows, latent 512, rope 64, up to 16 heads), 1 for the
+ * workgroup-staged MFMA kernel (*out_splits = stream-K workgroups per head
+ * group, *head_groups = head groups for both), 0 for the VALU kernel
+ * (*out_splits = context splits per row, *head_groups = 0), -1 for invalid
+ * shapes. */
 int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope_dim, int block_size,
                        int max_pages, int num_indices, int dtype, int splits, int flags, int* out_splits,
                        int* head_groups);

@@ -21,6 +21,7 @@ from oracle.mla_oracle import (default_mla_scale, oracle_latent_kv_write, oracle
 pytestmark = pytest.mark.gpu
 
 QD_FLAG_FORCE_GENERIC = 1
+QD_FLAG_MLA_STAGED = 2
 TOL = {torch.bfloat16: (2e-3, 1e-2), torch.float16: (2e-3, 1e-2), torch.float32: (1e-4, 1e-4)}
 ODT = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
 
@@ -63,6 +64,10 @@ ATTEND_SHAPES = [
     ("ref-bench-bf16", dict(lengths=[512, 1024], q_len=1, heads=4, nope_dim=32, latent_dim=64, rope_dim=16,
                             value_dim=32, block_size=16, dtype=torch.bfloat16)),
     ("deepseek-h16", dict(lengths=[1, 17, 300, 1031], q_len=1, heads=16, block_size=64, dtype=torch.bfloat16)),
+    ("deepseek-h16-t3-empty", dict(lengths=[0, 16, 2500, 33], q_len=3, heads=16, block_size=16,
+                                   dtype=torch.bfloat16)),
+    ("deepseek-h12-fp16", dict(lengths=[700, 64, 1, 129, 4000], q_len=1, heads=12, block_size=32,
+                               dtype=torch.float16)),
     ("deepseek-h128", dict(lengths=[0, 65, 777, 2048], q_len=1, heads=128, block_size=64, dtype=torch.bfloat16)),
     ("h20-fp16-p16", dict(lengths=[5, 200, 33], q_len=2, heads=20, block_size=16, dtype=torch.float16)),
     ("dc192-dr32", dict(lengths=[90, 257], q_len=1, heads=24, latent_dim=192, rope_dim=32, block_size=32,
@@ -71,7 +76,7 @@ ATTEND_SHAPES = [
 
 
 @pytest.mark.parametrize("name,kw", ATTEND_SHAPES, ids=[s[0] for s in ATTEND_SHAPES])
-@pytest.mark.parametrize("variant", ["auto", "split1", "split3", "generic"])   # split<n>: forced partition
+@pytest.mark.parametrize("variant", ["auto", "split1", "split3", "generic", "staged"])   # split<n>: forced partition
 def test_mla_attend_matches_oracle(gpu, name, kw, variant):
     say(f"mla_attend {name} {variant}")
     dtype = kw["dtype"]
@@ -80,8 +85,8 @@ def test_mla_attend_matches_oracle(gpu, name, kw, variant):
     B, T, H, Dc = qa.shape
     scale = default_mla_scale(c["q_nope"].shape[-1], c["q_rope"].shape[-1])
     out = torch.empty_like(qa)
-    splits = {"auto": 0, "split1": 1, "split3": 3, "generic": 0}[variant]
-    flags = QD_FLAG_FORCE_GENERIC if variant == "generic" else 0
+    splits = {"auto": 0, "split1": 1, "split3": 3, "generic": 0, "staged": 0}[variant]
+    flags = {"generic": QD_FLAG_FORCE_GENERIC, "staged": QD_FLAG_MLA_STAGED}.get(variant, 0)
     rc = cabi.mla_attend(qa, c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"], out, scale=scale,
                          splits=splits, flags=flags)
     assert rc == 0, cabi.error_string(rc)
@@ -93,6 +98,10 @@ def test_mla_attend_kernel_choice(gpu):
     say("mla_attend plan on the device")
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64)
     assert kind == 1 and groups >= 1 and wgs * groups <= 2 * 256
+    assert cabi.mla_attend_info(128, 1, 16, 512, 64, 64, 64)[0] == 2       # wave-streamed kernel
+    assert cabi.mla_attend_info(128, 1, 16, 512, 64, 64, 64, flags=QD_FLAG_MLA_STAGED)[0] == 1
+    assert cabi.mla_attend_info(128, 1, 16, 512, 64, 64, 64, nk=32)[0] == 1  # index lists: staged kernel
+    assert cabi.mla_attend_info(128, 1, 16, 512, 64, 8, 64)[0] == 1         # pages of 8 tokens
     assert cabi.mla_attend_info(1, 4, 4, 32, 8, 16, 4, dtype=0)[0] == 0      # fp32: VALU kernel
     assert cabi.mla_attend_info(1, 1, 4, 36, 8, 16, 4)[0] == 0              # Dc % 8 != 0
 
@@ -118,12 +127,13 @@ def test_mla_attend_sparse_and_causal(gpu, causal, kernel):
         _close(out, _oracle_attend(c, qa, scale, causal, sparse, dtype), dtype, f"sparse={sparse is not None}")
 
 
-def test_mla_attend_page_permutation_and_poison_bitwise(gpu):
+@pytest.mark.parametrize("heads", [64, 16], ids=["staged-h64", "wave-h16"])
+def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads):
     """Physical page order and unreferenced cache contents do not change a bit
     of the output (index handling is exact)."""
-    say("mla_attend permutation + poison invariance")
+    say(f"mla_attend permutation + poison invariance heads={heads}")
     dtype = torch.bfloat16
-    c = _case(gpu, lengths=[100, 513, 64], q_len=1, heads=64, block_size=64, dtype=dtype)
+    c = _case(gpu, lengths=[100, 513, 64], q_len=1, heads=heads, block_size=64, dtype=dtype)
     qa = _absorbed(c, dtype).to(dtype).to(gpu)
     scale = 0.05
 
