@@ -950,7 +950,14 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
 constexpr int kSubTokens = 16;        // tokens per wave tile
 constexpr int kWaveRows = 1024;       // query rows the prologue scans in LDS
 constexpr int kWaveListTiles = 1024;  // tiles of one workgroup's range
-constexpr int kWavePF = 2;            // tiles in flight per wave
+constexpr int kWavePF = 2;            // tiles staged per wave
+#ifndef QD_MLA_ROW_COST
+#define QD_MLA_ROW_COST 24
+#endif
+// Partition cost of a row's start, in tile units: the row merge, the query
+// pseudo-tile and the pipeline refill a workgroup pays entering a row cost
+// about this many tiles of streaming.
+constexpr int kWaveRowCost = QD_MLA_ROW_COST;
 
 template <int NB, int RC>
 struct WaveLayout {
@@ -967,7 +974,7 @@ __host__ __device__ constexpr size_t mla_wave_lds_bytes(int nb, int rc) {
          + 4 * 64 * 32 * 4                                                      // merge exchange
          + 4 * 16 * 2 * 4                                                       // merge m, l
          + static_cast<size_t>(kWaveRows) * (4 + 4 + 8)                         // row tiles, ends, prefix
-         + static_cast<size_t>(kWaveListTiles) * (8 + 4 + 4)                    // tile bases, counts, rows
+         + static_cast<size_t>(kWaveListTiles) * 16                             // tiles {base, rows, row}
          + 256;
 }
 
@@ -1031,9 +1038,8 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
   int* rt = reinterpret_cast<int*>(ml + 4 * 16 * 2);                      // [rows] tiles
   int* re = rt + kWaveRows;                                               // [rows] visible end
   int64_t* incl = reinterpret_cast<int64_t*>(re + kWaveRows);            // [rows] prefix of tiles
-  int64_t* lbase = incl + kWaveRows;                                      // [tiles] page row 0 offset
-  int* lnv = reinterpret_cast<int*>(lbase + kWaveListTiles);              // [tiles] visible rows
-  int* lrow = lnv + kWaveListTiles;                                       // [tiles] query row
+  // [tiles] {element offset of the tile's row 0 (2 words), visible rows, query row}
+  int* tl = reinterpret_cast<int*>(incl + kWaveRows);
 
   const int rows = p.B * p.T;  // <= kWaveRows (host check)
   const int h0 = 16 * hg;
@@ -1049,11 +1055,12 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
     rt[r] = (end + kSubTokens - 1) / kSubTokens;
   }
   __syncthreads();
+  auto row_cost = [&](int tiles) { return tiles > 0 ? tiles + kWaveRowCost : 0; };
   if (wv == 0) {
     int64_t carry = 0;
     for (int base = 0; base < rows; base += 64) {
       const int r = base + lane;
-      const int64_t n = r < rows ? rt[r] : 0;
+      const int64_t n = r < rows ? row_cost(rt[r]) : 0;
       const int64_t v = carry + wave_incl_scan_i64(n, lane);
       if (r < rows) incl[r] = v;
       carry = __shfl(v, 63);
@@ -1063,10 +1070,12 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
   const int64_t G = incl[rows - 1];
   const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
   const int64_t g1 = static_cast<int64_t>(w + 1) * G / p.wgs;
-  const int nt = static_cast<int>(g1 - g0);  // <= kWaveListTiles (host check)
+  const int nt = static_cast<int>(g1 - g0);  // positions, <= kWaveListTiles (host check)
   if (w == 0 && hg == 0 && tid == 0) *p.gtotal = G;
   auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * p.wgs - 1) / G); };
-  // This range's tiles: row (binary search of the prefix), page base, rows.
+  // This range's cost positions: row (binary search of the prefix); the
+  // first kWaveRowCost positions of a row hold no tile (row -1), the others
+  // tile i: page base and visible rows.
   for (int t = tid; t < nt; t += kAttendThreads) {
     const int64_t g = g0 + t;
     int lo = 0, hi = rows - 1;
@@ -1076,14 +1085,18 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
     }
     const int r = lo;
     const int tir = static_cast<int>(g - (incl[r] - rt[r]));
+    if (tir < 0) {
+      *reinterpret_cast<i32x4*>(tl + 4 * t) = i32x4{0, 0, 0, -1};
+      continue;
+    }
     const int tok0 = kSubTokens * tir;
     const int pg = tok0 / p.P;
     int32_t phys = p.table[static_cast<int64_t>(r / p.T) * p.maxP + pg];
     if (phys < 0) phys = 0;
     if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
-    lbase[t] = (static_cast<int64_t>(phys) * p.P + (tok0 - pg * p.P)) * Lay::kW;
-    lnv[t] = min(kSubTokens, re[r] - tok0);
-    lrow[t] = r;
+    const int64_t base = (static_cast<int64_t>(phys) * p.P + (tok0 - pg * p.P)) * Lay::kW;
+    *reinterpret_cast<i32x4*>(tl + 4 * t) =
+        i32x4{static_cast<int>(base & 0xFFFFFFFF), static_cast<int>(base >> 32), min(kSubTokens, re[r] - tok0), r};
     if (tir == 0 && hg == 0) {
       // This workgroup holds the row's first tile: record its span.
       p.meta[2 * r] = w;
@@ -1111,18 +1124,27 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
   int is_k = 0;        // next tile ordinal of this wave: g = g0 + wv + 4 k
   int is_row = -1;     // row of the last issued item
   auto issue = [&](Tile& dst, int& kind, int& row, int& nv) {
-    const int t = wv + 4 * is_k;
+    int t = wv + 4 * is_k;
     kind = kNone;
     row = -1;
     nv = 0;
+    int64_t tbase = 0;
+    i32x4 m = {0, 0, 0, -1};
+    while (t < nt) {  // skip the rows' start positions (no tile)
+      m = *reinterpret_cast<const i32x4*>(tl + 4 * t);
+      if (m[3] >= 0) break;
+      ++is_k;
+      t += 4;
+    }
     if (t < nt) {
-      row = lrow[t];
+      row = m[3];
       if (row != is_row) {
         kind = kQuery;
         is_row = row;
       } else {
         kind = kTile;
-        nv = lnv[t];
+        nv = m[2];
+        tbase = static_cast<int64_t>(static_cast<uint32_t>(m[0])) | (static_cast<int64_t>(m[1]) << 32);
         ++is_k;
       }
     }
@@ -1132,7 +1154,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
     int64_t rs_l, rs_r;  // row strides in bytes
     int nrow;            // valid rows (others reread row 0)
     if (kind == kTile) {
-      const int64_t b = lbase[t];
+      const int64_t b = tbase;
       lat = cache + 2 * b;
       rop = cache + 2 * (b + Lay::kDc);
       rs_l = rs_r = 2 * static_cast<int64_t>(Lay::kW);
@@ -1204,7 +1226,14 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
   };
   reset();
   // Rows of the range in order; merged_row: the next one to merge.
-  int merge_row = nt > 0 ? lrow[0] : rows;
+  auto row_at = [&](int64_t from) {  // row of the first tile at or after position from
+    for (int64_t x = from; x < g1; ++x) {
+      const int r = tl[4 * (x - g0) + 3];
+      if (r >= 0) return r;
+    }
+    return rows;
+  };
+  int merge_row = row_at(g0);
   auto merge = [&](int r) {
     const float lw = sum_over_lane_groups(l_run);
     if (q4 == 0) {
@@ -1272,8 +1301,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
   auto merge_before = [&](int r) {
     while (merge_row < r) {
       merge(merge_row);
-      const int64_t nxt = incl[merge_row];  // first tile of the following rows
-      merge_row = nxt < g1 ? lrow[nxt - g0] : rows;
+      merge_row = row_at(incl[merge_row]);  // first tile of the following rows
     }
   };
 
@@ -1302,12 +1330,31 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
     if (kind == kTile) {
       // A = cache rows (tokens), B = query rows (heads), both row r16.
       f32x4 s = {0.f, 0.f, 0.f, 0.f};
+      // Operands read kAhead chunks before their MFMA (LDS latency), two
+      // accumulators to halve the dependent MFMA chain.
+      constexpr int kAhead = 3;
+      const char* ta = tbuf + r16 * Lay::kStride + 16 * q4;
+      const char* qa = qbuf + r16 * Lay::kStride + 16 * q4;
+      u32x4 ar[kAhead], br[kAhead];
+#pragma unroll
+      for (int c = 0; c < kAhead; ++c) {
+        ar[c] = *reinterpret_cast<const u32x4*>(ta + 64 * c);
+        br[c] = *reinterpret_cast<const u32x4*>(qa + 64 * c);
+      }
+      f32x4 s2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(tbuf + r16 * Lay::kStride + 64 * c + 16 * q4);
-        const u32x4 b = *reinterpret_cast<const u32x4*>(qbuf + r16 * Lay::kStride + 64 * c + 16 * q4);
-        s = Ops::mma32(a, b, s);
+        const u32x4 a = ar[c % kAhead], b = br[c % kAhead];
+        if (c + kAhead < KC) {
+          ar[c % kAhead] = *reinterpret_cast<const u32x4*>(ta + 64 * (c + kAhead));
+          br[c % kAhead] = *reinterpret_cast<const u32x4*>(qa + 64 * (c + kAhead));
+        }
+        if (c & 1)
+          s2 = Ops::mma32(a, b, s2);
+        else
+          s = Ops::mma32(a, b, s);
       }
+      s += s2;
       float x[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[i] = 4 * q4 + i < nv ? s[i] * p.sl2 : -INFINITY;
@@ -1329,12 +1376,21 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
       for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - m_use);
       const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
       l_run += Ops::sum2(pb[0]) + Ops::sum2(pb[1]);
+      // The next block's 4 rows are read while this block multiplies.
+      const char* pv0 = tbuf + 4 * q4 * Lay::kStride + 16 * r16;
+      u32x4 nraw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nraw[i] = *reinterpret_cast<const u32x4*>(pv0 + i * Lay::kStride);
 #pragma unroll
       for (int bb = 0; bb < NB; ++bb) {
         u32x4 raw[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          raw[i] = *reinterpret_cast<const u32x4*>(tbuf + (4 * q4 + i) * Lay::kStride + 256 * bb + 16 * r16);
+        for (int i = 0; i < 4; ++i) raw[i] = nraw[i];
+        if (bb + 1 < NB) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            nraw[i] = *reinterpret_cast<const u32x4*>(pv0 + i * Lay::kStride + 256 * (bb + 1));
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int wd = e >> 1;
@@ -1677,7 +1733,8 @@ AttendPlan plan_attend(const AttendShape& a, int forced, int flags) {
     // The wave-streamed kernel: dense rows, Dc 512 / Dr 64 (instantiated),
     // pages of whole 16-token tiles, up to 16 heads, rows and tiles per
     // workgroup within its LDS lists.
-    const int64_t gmax = rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens);
+    const int64_t gmax =
+        rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens + kWaveRowCost);
     const size_t wlds = mla_wave_lds_bytes(4, 2);
     if ((flags & QD_FLAG_MLA_STAGED) == 0 && a.Dc == 512 && a.Dr == 64 && a.nk < 0 && a.P % kSubTokens == 0 &&
         a.H <= 16 && rows <= kWaveRows && wlds <= static_cast<size_t>(device_max_lds())) {
