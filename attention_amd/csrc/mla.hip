@@ -998,7 +998,9 @@ struct WaveTile {
 //            waits for the tiles in flight (loads complete in issue order).
 //   QK       the tile is written to the wave's LDS buffer (rows padded by 16
 //            bytes) and read back as A = rows (tokens) x 32 columns; B = the
-//            query chunks held in registers -> S^T[token 4 q4 + i][head r16].
+//            same chunks of the row's query, which the waves stage into one
+//            shared LDS slot -> S^T[token 4 q4 + i][head r16]; operands are
+//            read 3 chunks ahead into two accumulators.
 //   softmax  as mla_attend_mfma_kernel (exact running max, rescale only when
 //            it rises, denominator over the 16-bit weights).
 //   PV       16x16x16 with A = C^T from 4 LDS rows (8x8 transposes by byte

@@ -259,10 +259,12 @@ int qd_validate_paged_metadata(const int32_t* block_table, const int32_t* contex
  * and the device; > 0 forces it: for the MFMA kernel (16-bit, latent and
  * rope widths multiples of 8, latent <= 512) the number of workgroups that
  * share the batch's (row, 32-token tile) space in equal ranges (stream-K),
- * for the VALU kernel the number of context splits per row.
+ * (16-token tiles for the wave-streamed kernel, in cost units), for the
+ * VALU kernel the number of context splits per row.
  * qd_mla_attend_info() reports the kernel and the partition.  flags:
- * QD_FLAG_FORCE_GENERIC selects the VALU kernels.  Nothing here allocates
- * or synchronizes. */
+ * QD_FLAG_FORCE_GENERIC selects the VALU kernels, QD_FLAG_MLA_STAGED the
+ * workgroup-staged MFMA kernel where the wave-streamed one would run.
+ * Nothing here allocates or synchronizes. */
 
 /* Reference checks in order, messages included (mla.cu:152-155). */
 int qd_latent_kv_write_validate(const qd_tensor_desc* latent, const qd_tensor_desc* rope,
