@@ -640,35 +640,37 @@ __device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
   return (clamp_len(p, len_raw) + 15) >> 4;
 }
 
-// Merges the partials of up to four heads of one kv-head, in place of the
-// reference's merge kernel (gqa_decode.cu:74-87): rows r = 0..nrows-1 at
-// base + r*row_stride, head j < nheads at + j*(D+2), each {m (natural log),
-// l, acc[D]}.  Rows are folded in order with SoftmaxState::merge
-// (online_softmax.cuh:17-24): a row with l == 0 is skipped, the running
-// state is rescaled by exp(m - max).  Output acc/l rounded once, zeros when
-// l == 0 (gqa_decode.cu:84-86), head j at out + j*D.  One wave: 16 lanes
-// per head, D/16 consecutive elements per lane (one vector store); the rows
-// are loaded kBatch at a time so that one memory round trip covers a
-// typical merge.
-template <int D, int DT, int kBatch>
-__device__ __forceinline__ void merge_heads4(const float* base, int64_t row_stride, int nrows, int nheads,
-                                             typename Elem<DT>::S* out) {
-  // Partials come from an earlier kernel on the same stream: plain loads.
-  constexpr int EPL = D / 16;
-  const int lane = threadIdx.x & 63;
-  const int j4 = lane >> 4;
-  const int c16 = lane & 15;
-  const bool active = j4 < nheads;
-  const float* hb = base + static_cast<int64_t>(active ? j4 : 0) * (D + 2);
+// Merge of the partials of up to four heads of one kv-head, in place of the
+// reference's merge kernel (gqa_decode.cu:74-87).  Each partial row is
+// {m (natural log), l, acc[D]}; rows are folded in order with
+// SoftmaxState::merge (online_softmax.cuh:17-24): a row with l == 0 is
+// skipped, the running state is rescaled by exp(m - max).  Output acc/l
+// rounded once, zeros when l == 0 (gqa_decode.cu:84-86).  One wave: 16 lanes
+// per head (head j4 = lane / 16), D/16 consecutive elements per lane (one
+// vector store).  Partials come from an earlier kernel on the same stream:
+// plain loads.
+template <int D>
+struct MergeRows {
+  static constexpr int EPL = D / 16;
+  static constexpr int kBatch = 16;  // rows loaded per memory round trip
+  int c16;
   float M = -INFINITY, L = 0.f;
   float acc[EPL];
+  float ms[kBatch], ls[kBatch], av[kBatch][EPL];
+
+  __device__ MergeRows() : c16(threadIdx.x & 15) {
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < nrows; s0 += kBatch) {
-    float ms[kBatch], ls[kBatch], av[kBatch][EPL];
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  }
+
+  // Loads row t < kBatch of the batch from `row` (the lane's head) when
+  // `present` (wave-uniform).
+  __device__ void load(int t, bool present, const float* row) {
+    ms[t] = -INFINITY;
+    ls[t] = 0.f;
 #pragma unroll
-    for (int t = 0; t < kBatch; ++t) {
-      const float* row = hb + static_cast<int64_t>(min(s0 + t, nrows - 1)) * row_stride;
+    for (int e = 0; e < EPL; ++e) av[t][e] = 0.f;
+    if (present) {
       ms[t] = row[0];
       ls[t] = row[1];
       // Rows are D+2 floats (D even): acc is 8-byte aligned.
@@ -679,9 +681,13 @@ __device__ __forceinline__ void merge_heads4(const float* base, int64_t row_stri
         av[t][e + 1] = x[1];
       }
     }
+  }
+
+  // Folds rows t < n of the loaded batch, in order.
+  __device__ void fold(int n) {
 #pragma unroll
     for (int t = 0; t < kBatch; ++t) {
-      if (s0 + t >= nrows || ls[t] == 0.f) continue;
+      if (t >= n || ls[t] == 0.f) continue;
       const float mn = fmaxf(M, ms[t]);
       const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
       const float bb = fast_exp2((ms[t] - mn) * kLog2e);
@@ -691,21 +697,36 @@ __device__ __forceinline__ void merge_heads4(const float* base, int64_t row_stri
       M = mn;
     }
   }
-  if (!active) return;
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  uint32_t wv[EPL / 2];
+
+  // Folds `nrows` rows at base + r*row_stride (the lane's head), kBatch
+  // rows per round trip; only rows that exist are loaded.
+  __device__ void fold_rows(const float* base, int64_t row_stride, int nrows) {
+    for (int s0 = 0; s0 < nrows; s0 += kBatch) {
 #pragma unroll
-  for (int e = 0; e < EPL; e += 2)
-    wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
-  char* dst = reinterpret_cast<char*>(out + static_cast<int64_t>(j4) * D + c16 * EPL);
-  if constexpr (EPL == 4) {
-    *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
-  } else {
-#pragma unroll
-    for (int t = 0; t < EPL / 8; ++t)
-      *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+      for (int t = 0; t < kBatch; ++t) load(t, s0 + t < nrows, base + static_cast<int64_t>(s0 + t) * row_stride);
+      fold(nrows - s0);
+    }
   }
-}
+
+  // Writes head j4's output row at out (when the head exists).
+  template <int DT>
+  __device__ void store(bool active, typename Elem<DT>::S* out) const {
+    if (!active) return;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint32_t wv[EPL / 2];
+#pragma unroll
+    for (int e = 0; e < EPL; e += 2)
+      wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
+    char* dst = reinterpret_cast<char*>(out + c16 * EPL);
+    if constexpr (EPL == 4) {
+      *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
+    } else {
+#pragma unroll
+      for (int t = 0; t < EPL / 8; ++t)
+        *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+    }
+  }
+};
 
 constexpr int kMaxWgWaves = 8;
 
@@ -858,6 +879,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
     return static_cast<int>(i < nb ? i : nb);
   };
 
+
   MfmaWave<D, DT, PF, NKV> wv;
   wv.init_lane();
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
@@ -914,10 +936,13 @@ __global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
   const int first = p.meta[2 * b];
   const int nwg = p.meta[2 * b + 1];
   if (nwg <= 1) return;  // written directly, or an empty sequence (zero-filled)
+  const int j4 = (threadIdx.x & 63) >> 4;
+  const bool active = j4 < min(4, p.g - 4 * pass);
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
-  const int64_t h0 = static_cast<int64_t>(kvh) * p.g + 4 * pass;
-  merge_heads4<D, DT, 16>(p.ws + static_cast<int64_t>(first + b) * slot_floats + h0 * (D + 2), slot_floats, nwg,
-                          min(4, p.g - 4 * pass), static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h0) * D);
+  const int64_t h = static_cast<int64_t>(kvh) * p.g + 4 * pass + (active ? j4 : 0);
+  MergeRows<D> mr;
+  mr.fold_rows(p.ws + static_cast<int64_t>(first + b) * slot_floats + h * (D + 2), slot_floats, nwg);
+  mr.template store<DT>(active, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
 }
 
 // ----------------------------------------------------------------------------
@@ -1069,10 +1094,12 @@ bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int d
 constexpr int kPrefetch = QD_PREFETCH;
 
 // Stream-K path limits: each wave scans all lengths, so the batch is capped;
-// a wave gets at least kSkMinGroups groups of the largest possible batch.
+// a workgroup gets at least kSkMinGroups groups of the largest possible
+// batch.  Small batches are latency-bound: 4 groups per workgroup took a
+// 57-group batch from 10.7 to 6.3 us, and 2 lost that back in the merge.
 constexpr int kSkMaxBatch = 4096;
 #ifndef QD_SK_MIN_GROUPS
-#define QD_SK_MIN_GROUPS 16
+#define QD_SK_MIN_GROUPS 4
 #endif
 constexpr int64_t kSkMinGroups = QD_SK_MIN_GROUPS;
 // Waves launched per resident wave slot.  Above 1 the hardware dispatcher
