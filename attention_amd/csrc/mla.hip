@@ -1013,7 +1013,9 @@ struct WaveTile {
 // The prologue scans the rows' lengths into LDS, lists this range's tiles
 // (row, page base, visible count: one page-table round trip for all of
 // them), writes meta, gtotal and the empty rows.
-template <int DT, int NB, int RC>
+// NT: nontemporal cache loads (one head group); with several head groups the
+// tiles are loaded into L2 for the other groups' workgroups on the XCD.
+template <int DT, int NB, int RC, bool NT>
 __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaParams p) {
   using E = Elem<DT>;
   using Ops = MfmaOps<DT>;
@@ -1177,16 +1179,17 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
       const int rr = 4 * q4 + i < nrow ? 4 * q4 + i : 0;
       const char* lrow_p = lat + rr * rs_l + 16 * r16;
 #pragma unroll
-      for (int blk = 0; blk < NB; ++blk) dst.c[blk][i] = stream_load16(lrow_p + 256 * blk);
+      for (int blk = 0; blk < NB; ++blk) dst.c[blk][i] = load16<NT>(lrow_p + 256 * blk);
       const char* rp = rop + rr * rs_r + Lay::kRopeBytes * r16;
       if constexpr (RC == 1) {
-        dst.r[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(rp));
+        dst.r[i][0] = NT ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(rp))
+                         : *reinterpret_cast<const uint32_t*>(rp);
       } else if constexpr (RC == 2) {
-        const u32x2 x = stream_load8(rp);
+        const u32x2 x = load8<NT>(rp);
         dst.r[i][0] = x[0];
         dst.r[i][1] = x[1];
       } else {
-        const u32x4 x = stream_load16(rp);
+        const u32x4 x = load16<NT>(rp);
 #pragma unroll
         for (int k = 0; k < RC; ++k) dst.r[i][k] = x[k];
       }
@@ -1286,10 +1289,12 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
             pr[0] = M == -INFINITY ? -INFINITY : M * kLn2;
             pr[1] = Lt;
           }
+          // Rows are Dc+2 floats: the accumulator starts 8 bytes in.
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pr[2 + 128 * bb + 32 * q4 + 8 * i + e] = o[e][i];
+            for (int e = 0; e < 8; e += 2)
+              *reinterpret_cast<f32x2*>(pr + 2 + 128 * bb + 32 * q4 + 8 * i + e) = f32x2{o[e][i], o[e + 1][i]};
         }
       }
       lds_barrier();
@@ -1343,18 +1348,23 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
         ar[c] = *reinterpret_cast<const u32x4*>(ta + 64 * c);
         br[c] = *reinterpret_cast<const u32x4*>(qa + 64 * c);
       }
+      // The scheduling barriers keep each chunk's reads kAhead MFMAs ahead:
+      // left free, the scheduler sinks them next to their MFMA and every
+      // MFMA waits out a whole LDS round trip.
+      __builtin_amdgcn_sched_barrier(0);
       f32x4 s2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
         const u32x4 a = ar[c % kAhead], b = br[c % kAhead];
-        if (c + kAhead < KC) {
-          ar[c % kAhead] = *reinterpret_cast<const u32x4*>(ta + 64 * (c + kAhead));
-          br[c % kAhead] = *reinterpret_cast<const u32x4*>(qa + 64 * (c + kAhead));
-        }
         if (c & 1)
           s2 = Ops::mma32(a, b, s2);
         else
           s = Ops::mma32(a, b, s);
+        if (c + kAhead < KC) {
+          ar[c % kAhead] = *reinterpret_cast<const u32x4*>(ta + 64 * (c + kAhead));
+          br[c % kAhead] = *reinterpret_cast<const u32x4*>(qa + 64 * (c + kAhead));
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
       s += s2;
       float x[4];
@@ -1393,6 +1403,8 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
           for (int i = 0; i < 4; ++i)
             nraw[i] = *reinterpret_cast<const u32x4*>(pv0 + i * Lay::kStride + 256 * (bb + 1));
         }
+        // As in QK: the next block's reads stay ahead of this block's MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int wd = e >> 1;
@@ -1733,18 +1745,20 @@ AttendPlan plan_attend(const AttendShape& a, int forced, int flags) {
     pl.wgs = forced > 0 ? forced : std::max(1, device_cus() / pl.head_groups);
     pl.splits = 1;
     // The wave-streamed kernel: dense rows, Dc 512 / Dr 64 (instantiated),
-    // pages of whole 16-token tiles, up to 16 heads, rows and tiles per
-    // workgroup within its LDS lists.
+    // pages of whole 16-token tiles, rows and tiles per workgroup within its
+    // LDS lists.  Each group of 16 heads is a workgroup of its own over the
+    // same tile range, on the same XCD (shared L2), one per CU in all.
     const int64_t gmax =
         rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens + kWaveRowCost);
     const size_t wlds = mla_wave_lds_bytes(4, 2);
     if ((flags & QD_FLAG_MLA_STAGED) == 0 && a.Dc == 512 && a.Dr == 64 && a.nk < 0 && a.P % kSubTokens == 0 &&
-        a.H <= 16 && rows <= kWaveRows && wlds <= static_cast<size_t>(device_max_lds())) {
-      const int wgs = forced > 0 ? forced : std::max(1, device_cus());
+        rows <= kWaveRows && wlds <= static_cast<size_t>(device_max_lds())) {
+      const int groups = ht;
+      const int wgs = forced > 0 ? forced : std::max(1, device_cus() / groups);
       if ((gmax + wgs - 1) / wgs + 1 <= kWaveListTiles) {
         pl.wave = true;
         pl.nht = 1;
-        pl.head_groups = 1;
+        pl.head_groups = groups;
         pl.wgs = wgs;
         pl.lds = wlds;
       }
@@ -1792,9 +1806,9 @@ hipError_t launch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_
   return hipSuccess;
 }
 
-template <int DT>
+template <int DT, bool NT>
 hipError_t launch_attend_wave(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
-  auto fn = mla_attend_wave_kernel<DT, 4, 2>;
+  auto fn = mla_attend_wave_kernel<DT, 4, 2, NT>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&] {
@@ -1867,9 +1881,12 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   if (pl.mfma) {
     const int64_t grid = (static_cast<int64_t>(pl.wgs) + 7) / 8 * 8 * pl.head_groups;
     if (grid > 2147483647LL) return mla_fail(nullptr, 0, "mla_attend grid exceeds launch limits");
-    if (pl.wave)
-      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_wave<QD_DTYPE_BF16>(prm, pl, grid, st)
-                                     : launch_attend_wave<QD_DTYPE_F16>(prm, pl, grid, st);
+    if (pl.wave && pl.head_groups == 1)
+      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_wave<QD_DTYPE_BF16, true>(prm, pl, grid, st)
+                                     : launch_attend_wave<QD_DTYPE_F16, true>(prm, pl, grid, st);
+    else if (pl.wave)
+      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_wave<QD_DTYPE_BF16, false>(prm, pl, grid, st)
+                                     : launch_attend_wave<QD_DTYPE_F16, false>(prm, pl, grid, st);
     else
       err = a.dtype == QD_DTYPE_BF16 ? dispatch_attend_mfma<QD_DTYPE_BF16>(prm, pl, grid, st)
                                      : dispatch_attend_mfma<QD_DTYPE_F16>(prm, pl, grid, st);

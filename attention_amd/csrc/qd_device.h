@@ -180,6 +180,20 @@ __device__ __forceinline__ u32x2 stream_load8(const char* ptr) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(ptr));
 }
 
+// Streaming (nontemporal) load when NT, else a plain cached load: data that
+// other workgroups of the same XCD read soon after should stay in L2.
+template <bool NT>
+__device__ __forceinline__ u32x4 load16(const char* ptr) {
+  if constexpr (NT) return stream_load16(ptr);
+  else return *reinterpret_cast<const u32x4*>(ptr);
+}
+
+template <bool NT>
+__device__ __forceinline__ u32x2 load8(const char* ptr) {
+  if constexpr (NT) return stream_load8(ptr);
+  else return *reinterpret_cast<const u32x2*>(ptr);
+}
+
 }  // namespace
 
 #endif  // QD_DEVICE_H

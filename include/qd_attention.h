@@ -302,7 +302,7 @@ size_t qd_mla_attend_workspace_bytes(int batch, int q_len, int heads, int latent
                                      int flags);
 
 /* The plan qd_mla_attend would use: returns 2 for the wave-streamed MFMA
- * kernel (dense rows, latent 512, rope 64, up to 16 heads), 1 for the
+ * kernel (dense rows, latent 512, rope 64, 16-token pages), 1 for the
  * workgroup-staged MFMA kernel (*out_splits = stream-K workgroups per head
  * group, *head_groups = head groups for both), 0 for the VALU kernel
  * (*out_splits = context splits per row, *head_groups = 0), -1 for invalid

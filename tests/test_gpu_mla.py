@@ -97,6 +97,8 @@ def test_mla_attend_matches_oracle(gpu, name, kw, variant):
 def test_mla_attend_kernel_choice(gpu):
     say("mla_attend plan on the device")
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64)
+    assert kind == 2 and groups == 8 and wgs * groups <= 256      # wave-streamed kernel, 8 head groups
+    kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64, flags=QD_FLAG_MLA_STAGED)
     assert kind == 1 and groups >= 1 and wgs * groups <= 2 * 256
     assert cabi.mla_attend_info(128, 1, 16, 512, 64, 64, 64)[0] == 2       # wave-streamed kernel
     assert cabi.mla_attend_info(128, 1, 16, 512, 64, 64, 64, flags=QD_FLAG_MLA_STAGED)[0] == 1
