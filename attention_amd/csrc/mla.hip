@@ -418,7 +418,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
   uint32_t* masks = reinterpret_cast<uint32_t*>(tile_base + kMetaSlots);       // [slots]
   int* flags = reinterpret_cast<int*>(masks + kMetaSlots);                     // [slots]
   int32_t* win = flags + kMetaSlots;                                           // [kWinPages]
-  f32x4* sx = reinterpret_cast<f32x4*>(win + kWinPages + 8);               // [waves][64][2] partial scores
+  f32x4* sx = reinterpret_cast<f32x4*>(win + kWinPages + 8);               // [waves][2][64] partial scores
 
   const int64_t rows = static_cast<int64_t>(p.B) * p.T;
   const bool sparse = p.nk >= 0;
@@ -804,16 +804,17 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
         }
       }
       if constexpr (DS > 1) {
-        sx[(wv * 64 + lane) * 2] = s0;
-        sx[(wv * 64 + lane) * 2 + 1] = s1;
+        // [wave][half][lane]: lane-contiguous, free of bank conflicts.
+        sx[(wv * 2) * 64 + lane] = s0;
+        sx[(wv * 2 + 1) * 64 + lane] = s1;
         lds_barrier();
         s0 = f32x4{0.f, 0.f, 0.f, 0.f};
         s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int sl2 = 0; sl2 < DS; ++sl2) {
           const int src = ht + p.nht * sl2;
-          s0 += sx[(src * 64 + lane) * 2];
-          s1 += sx[(src * 64 + lane) * 2 + 1];
+          s0 += sx[(src * 2) * 64 + lane];
+          s1 += sx[(src * 2 + 1) * 64 + lane];
         }
       }
     }
@@ -1037,7 +1038,9 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
 
   char* tbuf = smem + wv * Lay::kBuf;                                     // this wave's tile
   char* qbuf = smem + 4 * Lay::kBuf;                                      // the current row's query
-  float* red = reinterpret_cast<float*>(smem + 5 * Lay::kBuf);          // [4][64][32]
+  // [wave][e][lane] f32x4: consecutive lanes at consecutive 16 bytes, so
+  // the exchange's LDS accesses are free of bank conflicts.
+  float* red = reinterpret_cast<float*>(smem + 5 * Lay::kBuf);          // [4][8][64] x 4
   float* ml = red + 4 * 64 * 32;                                          // [4][16][2]
   int* rt = reinterpret_cast<int*>(ml + 4 * 16 * 2);                      // [rows] tiles
   int* re = rt + kWaveRows;                                               // [rows] visible end
@@ -1263,15 +1266,15 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
       // Every wave deposits its scaled block bb; wave bb % 4 sums them.
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<f32x4*>(red + ((wv * 64 + lane) * 32 + 4 * e)) = acc[bb][e] * sc;
+        *reinterpret_cast<f32x4*>(red + 4 * ((wv * 8 + e) * 64 + lane)) = acc[bb][e] * sc;
       lds_barrier();
       if (wv == bb % 4 && head_ok) {
         f32x4 o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          o[e] = *reinterpret_cast<const f32x4*>(red + ((0 * 64 + lane) * 32 + 4 * e));
+          o[e] = *reinterpret_cast<const f32x4*>(red + 4 * ((0 * 8 + e) * 64 + lane));
 #pragma unroll
-          for (int v = 1; v < 4; ++v) o[e] += *reinterpret_cast<const f32x4*>(red + ((v * 64 + lane) * 32 + 4 * e));
+          for (int v = 1; v < 4; ++v) o[e] += *reinterpret_cast<const f32x4*>(red + 4 * ((v * 8 + e) * 64 + lane));
         }
         if (whole) {
           const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
