@@ -959,6 +959,10 @@ constexpr int kWavePF = 2;            // tiles staged per wave
 // pseudo-tile and the pipeline refill a workgroup pays entering a row cost
 // about this many tiles of streaming.
 constexpr int kWaveRowCost = QD_MLA_ROW_COST;
+#ifndef QD_MLA_LAZY_LOG2
+#define QD_MLA_LAZY_LOG2 8
+#endif
+constexpr float kWaveLazyLog2 = QD_MLA_LAZY_LOG2;
 
 template <int NB, int RC>
 struct WaveLayout {
@@ -1377,10 +1381,17 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
       for (int i = 0; i < 4; ++i) x[i] = 4 * q4 + i < nv ? s[i] * p.sl2 : -INFINITY;
       float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
       mx = max_over_lane_groups(mx);
-      const bool move = mx > m_run;
+      // Lazy reference max: a head's m_run may trail its running max by up
+      // to kWaveLazyLog2, so its weights stay <= 2^kWaveLazyLog2 (exact
+      // scaling in fp32, far inside the 16-bit range).  The accumulators,
+      // 128 AGPRs a lane, are rescaled only when some head's max moves past
+      // that, and then every head catches up.  With the exact max, 16 heads
+      // rescaled on about 80% of the tiles.
+      const bool move = mx > m_run + kWaveLazyLog2;
       if (__ballot(move)) {
-        const float alpha = move ? fast_exp2(m_run - mx) : 1.f;
-        m_run = move ? mx : m_run;
+        const float mn = fmaxf(m_run, mx);
+        const float alpha = mn == m_run ? 1.f : fast_exp2(m_run - mn);  // m_run = -inf: 0
+        m_run = mn;
         l_run *= alpha;
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb)
