@@ -489,7 +489,10 @@ struct MfmaWave {
 #pragma unroll
         for (int d = 0; d < DV; ++d) acc[j][d] *= alpha;
       }
+      // The weights as hi + lo for bf16 (MfmaOps::kSplitWeights): the PV
+      // product then sees them to ~2^-17, as the fp32 denominator does.
       const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
+      const u32x2 pl = {Ops::rest2(pr[0], pr[1], pb[0]), Ops::rest2(pr[2], pr[3], pb[1])};
 #pragma unroll
       for (int d = 0; d < DV; ++d) {
         const int w = d >> 1;
@@ -497,6 +500,7 @@ struct MfmaWave {
         const u32x2 a = {__builtin_amdgcn_perm(buf.v[j][1].w[w], buf.v[j][0].w[w], sel),
                          __builtin_amdgcn_perm(buf.v[j][3].w[w], buf.v[j][2].w[w], sel)};
         acc[j][d] = Ops::pv(a, pb, acc[j][d]);
+        if constexpr (Ops::kSplitWeights) acc[j][d] = Ops::pv(a, pl, acc[j][d]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);

@@ -843,15 +843,23 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc[bb][e] *= alpha;
       }
-      // The denominator sums the same 16-bit probabilities the PV product
-      // uses, so the output is an exactly normalized average of values.
+      // The denominator sums the weights the PV product uses: for bf16 both
+      // carry them as hi + lo (MfmaOps::kSplitWeights, ~2^-17), for fp16 the
+      // 16-bit values, so the output is a normalized average of values.
       const float m_use = m_run == -INFINITY ? 0.f : m_run;
       float pr[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pr[e] = fast_exp2(x[e] - m_use);
       const u32x4 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3]), Ops::pack2(pr[4], pr[5]),
                         Ops::pack2(pr[6], pr[7])};
-      l_run += (Ops::sum2(pb[0]) + Ops::sum2(pb[1])) + (Ops::sum2(pb[2]) + Ops::sum2(pb[3]));
+      u32x4 pl = {0u, 0u, 0u, 0u};
+      if constexpr (Ops::kSplitWeights) {
+        pl = u32x4{Ops::rest2(pr[0], pr[1], pb[0]), Ops::rest2(pr[2], pr[3], pb[1]), Ops::rest2(pr[4], pr[5], pb[2]),
+                   Ops::rest2(pr[6], pr[7], pb[3])};
+        l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+      } else {
+        l_run += (Ops::sum2(pb[0]) + Ops::sum2(pb[1])) + (Ops::sum2(pb[2]) + Ops::sum2(pb[3]));
+      }
 
       // O^T += C[:, slice]^T . P^T
 #pragma unroll
@@ -865,7 +873,11 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
             raw[t] = *reinterpret_cast<const u32x4*>(buf + 16 * (tok * w8 + (cc ^ (tok & swz))));
           }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[bb][e] = Ops::mma32(transpose8x8_col_b16(raw, e), pb, acc[bb][e]);
+          for (int e = 0; e < 8; ++e) {
+            const u32x4 va = transpose8x8_col_b16(raw, e);
+            acc[bb][e] = Ops::mma32(va, pb, acc[bb][e]);
+            if constexpr (Ops::kSplitWeights) acc[bb][e] = Ops::mma32(va, pl, acc[bb][e]);
+          }
         }
       }
     }
@@ -1402,8 +1414,16 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
       float pr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - m_use);
+      // Weights as hi + lo for bf16 (MfmaOps::kSplitWeights); the
+      // denominator sums what the PV product uses.
       const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
-      l_run += Ops::sum2(pb[0]) + Ops::sum2(pb[1]);
+      u32x2 pl = {0u, 0u};
+      if constexpr (Ops::kSplitWeights) {
+        pl = u32x2{Ops::rest2(pr[0], pr[1], pb[0]), Ops::rest2(pr[2], pr[3], pb[1])};
+        l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      } else {
+        l_run += Ops::sum2(pb[0]) + Ops::sum2(pb[1]);
+      }
       // The next block's 4 rows are read while this block multiplies.
       const char* pv0 = tbuf + 4 * q4 * Lay::kStride + 16 * r16;
       u32x4 nraw[4];
@@ -1428,6 +1448,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
           const u32x2 a = {__builtin_amdgcn_perm(raw[1][wd], raw[0][wd], sel),
                            __builtin_amdgcn_perm(raw[3][wd], raw[2][wd], sel)};
           acc[bb][e] = Ops::pv(a, pb, acc[bb][e]);
+          if constexpr (Ops::kSplitWeights) acc[bb][e] = Ops::pv(a, pl, acc[bb][e]);
         }
       }
     }

@@ -125,6 +125,15 @@ struct MfmaOps<QD_DTYPE_BF16> {
   }
   // Sum of the two 16-bit values packed in w, in fp32.
   __device__ static float sum2(uint32_t w) { return __uint_as_float(w << 16) + __uint_as_float(w & 0xFFFF0000u); }
+  // Weights for the PV product as hi + lo: bf16 keeps 8 significant bits,
+  // and a single rounding of the softmax weights (relative 2^-9 each) put
+  // the output past the 16-bit bar on random inputs (the reference keeps
+  // them in fp32).  lo = pack2 of what hi left out, so hi + lo holds each
+  // weight to about 2^-17 and the PV product takes two MFMAs.
+  static constexpr bool kSplitWeights = true;
+  __device__ static uint32_t rest2(float x, float y, uint32_t hi) {
+    return pack2(x - __uint_as_float(hi << 16), y - __uint_as_float(hi & 0xFFFF0000u));
+  }
 };
 
 template <>
@@ -146,6 +155,10 @@ struct MfmaOps<QD_DTYPE_F16> {
     const f32x2 v = __builtin_convertvector(__builtin_bit_cast(f16x2, w), f32x2);
     return v[0] + v[1];
   }
+  // fp16 keeps 11 significant bits: one rounding of the weights stays far
+  // inside the 16-bit bar (measured 0.2 of it at worst), so no split.
+  static constexpr bool kSplitWeights = false;
+  __device__ static uint32_t rest2(float, float, uint32_t) { return 0u; }
 };
 
 // 8x8 transpose of 16-bit elements held in one lane: in[t] holds elements

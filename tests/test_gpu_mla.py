@@ -69,6 +69,8 @@ ATTEND_SHAPES = [
     ("deepseek-h12-fp16", dict(lengths=[700, 64, 1, 129, 4000], q_len=1, heads=12, block_size=32,
                                dtype=torch.float16)),
     ("deepseek-h128", dict(lengths=[0, 65, 777, 2048], q_len=1, heads=128, block_size=64, dtype=torch.bfloat16)),
+    ("deepseek-h64-fp16-t2", dict(lengths=[0, 40, 1500, 3000], q_len=2, heads=64, block_size=16,
+                                  dtype=torch.float16)),
     ("h20-fp16-p16", dict(lengths=[5, 200, 33], q_len=2, heads=20, block_size=16, dtype=torch.float16)),
     ("dc192-dr32", dict(lengths=[90, 257], q_len=1, heads=24, latent_dim=192, rope_dim=32, block_size=32,
                         dtype=torch.bfloat16)),
@@ -98,6 +100,8 @@ def test_mla_attend_kernel_choice(gpu):
     say("mla_attend plan on the device")
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64)
     assert kind == 2 and groups == 8 and wgs * groups <= 256      # wave-streamed kernel, 8 head groups
+    kind, wgs, groups = cabi.mla_attend_info(32, 1, 20, 512, 64, 64, 64)
+    assert kind == 2 and groups == 2 and wgs * groups <= 256      # 2 head groups, the second of 4 heads
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64, flags=QD_FLAG_MLA_STAGED)
     assert kind == 1 and groups >= 1 and wgs * groups <= 2 * 256
     assert cabi.mla_attend_info(128, 1, 16, 512, 64, 64, 64)[0] == 2       # wave-streamed kernel
@@ -129,11 +133,12 @@ def test_mla_attend_sparse_and_causal(gpu, causal, kernel):
         _close(out, _oracle_attend(c, qa, scale, causal, sparse, dtype), dtype, f"sparse={sparse is not None}")
 
 
-@pytest.mark.parametrize("heads", [64, 16], ids=["staged-h64", "wave-h16"])
-def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads):
+@pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_STAGED), (16, 0)],
+                         ids=["wave-h64", "staged-h64", "wave-h16"])
+def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads, flags):
     """Physical page order and unreferenced cache contents do not change a bit
     of the output (index handling is exact)."""
-    say(f"mla_attend permutation + poison invariance heads={heads}")
+    say(f"mla_attend permutation + poison invariance heads={heads} flags={flags}")
     dtype = torch.bfloat16
     c = _case(gpu, lengths=[100, 513, 64], q_len=1, heads=heads, block_size=64, dtype=dtype)
     qa = _absorbed(c, dtype).to(dtype).to(gpu)
@@ -141,7 +146,8 @@ def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads):
 
     def run(cache, table):
         out = torch.empty_like(qa)
-        rc = cabi.mla_attend(qa, c["q_rope"], cache, table, c["lens"], c["positions"], out, scale=scale, splits=2)
+        rc = cabi.mla_attend(qa, c["q_rope"], cache, table, c["lens"], c["positions"], out, scale=scale, splits=2,
+                             flags=flags)
         assert rc == 0, cabi.error_string(rc)
         torch.cuda.synchronize()
         return out
