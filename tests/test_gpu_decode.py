@@ -445,3 +445,20 @@ def test_repeat_calls_deterministic(gpu):
     b = attention_amd.gqa_decode(*case)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("seed", range(1, 9))
+def test_bf16_accuracy_over_seeds(gpu, seed):
+    """Random lengths with short, peaked rows in bf16.  With one bf16 rounding
+    of the softmax weights in the PV product some of these seeds landed past
+    the 16-bit bar (worst 1.3x of it); the MFMA kernels carry the weights as
+    hi + lo (MfmaOps::kSplitWeights) and stay near 0.6x."""
+    rng = np.random.default_rng(seed)
+    lengths = [int(x) for x in rng.integers(1, 700, size=6)] + [1, 2, 3, 17]
+    say(f"bf16 accuracy seed {seed} lengths {lengths}")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                                   dtype=torch.bfloat16, seed=seed), gpu)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    ref, rows = oracle_rows(case)
+    assert_close(out, ref, "bf16", rows, f"seed {seed}")

@@ -133,6 +133,26 @@ def test_mla_attend_sparse_and_causal(gpu, causal, kernel):
         _close(out, _oracle_attend(c, qa, scale, causal, sparse, dtype), dtype, f"sparse={sparse is not None}")
 
 
+@pytest.mark.parametrize("seed", range(1, 9))
+@pytest.mark.parametrize("flags", [0, QD_FLAG_MLA_STAGED], ids=["wave", "staged"])
+def test_mla_attend_bf16_accuracy_over_seeds(gpu, flags, seed):
+    """Random DeepSeek-shaped inputs with short rows in bf16: with one bf16
+    rounding of the softmax weights in the PV product, 3 of these 8 seeds
+    landed past the 16-bit bar (worst 1.23x); the kernels carry the weights
+    as hi + lo and stay under 0.5x."""
+    say(f"mla_attend bf16 accuracy seed {seed} flags {flags}")
+    dtype = torch.bfloat16
+    c = _case(gpu, lengths=[3, 300, 1031, 2500], q_len=1, heads=16, block_size=64, dtype=dtype, seed=seed)
+    qa = _absorbed(c, dtype).to(dtype).to(gpu)
+    scale = default_mla_scale(c["q_nope"].shape[-1], c["q_rope"].shape[-1])
+    out = torch.empty_like(qa)
+    rc = cabi.mla_attend(qa, c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"], out, scale=scale,
+                         flags=flags)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    _close(out, _oracle_attend(c, qa, scale, dtype=dtype), dtype, f"seed {seed}")
+
+
 @pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_STAGED), (16, 0)],
                          ids=["wave-h64", "staged-h64", "wave-h16"])
 def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads, flags):
