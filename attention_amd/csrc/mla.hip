@@ -385,7 +385,8 @@ __device__ __forceinline__ int row_tiles(const MlaParams& p, int64_t r) {
 //            groups with permlane swaps; the accumulator is rescaled only
 //            when a head's running max rises (wave-uniform branch).
 //   PV       k index 8 q4 + e <-> token 4 q4 + e (e < 4) / 16 + 4 q4 + e - 4,
-//            so B = P^T is the lane's own 8 probabilities; A = C^T for
+//            so B = P^T is the lane's own 8 probabilities (as hi + lo for
+//            bf16: two MFMAs with the same A); A = C^T for
 //            latent columns 128 blk + 8 r16 + e of those tokens (8 LDS
 //            reads + 8x8 transpose); C tile (blk, e) row r <-> column
 //            128 blk + 8 r + e: lane rows 4 q4 + i hold the 32 contiguous
@@ -822,7 +823,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
       // Online softmax in log2 units.  The accumulator is rescaled only on
       // tiles that raise some head's running max (a wave-uniform branch;
       // rare once the max has been seen), so every probability is <= 1 and
-      // the largest score's is exactly 1 in the 16-bit PV operand.
+      // the largest score's is exactly 1.
       float x[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1020,11 +1021,13 @@ struct WaveTile {
 //            same chunks of the row's query, which the waves stage into one
 //            shared LDS slot -> S^T[token 4 q4 + i][head r16]; operands are
 //            read 3 chunks ahead into two accumulators.
-//   softmax  as mla_attend_mfma_kernel (exact running max, rescale only when
-//            it rises, denominator over the 16-bit weights).
+//   softmax  fp32, with a lazy reference max (it may trail a head's
+//            running max by up to 2^kWaveLazyLog2; the accumulators are
+//            rescaled only past that).
 //   PV       16x16x16 with A = C^T from 4 LDS rows (8x8 transposes by byte
-//            permutes) and B = P^T, the lane's own 4 weights; C tile (blk, e)
-//            row r <-> latent column 128 blk + 8 r + e.
+//            permutes) and B = P^T, the lane's own 4 weights (as hi + lo for
+//            bf16: two MFMAs); C tile (blk, e) row r <-> latent column
+//            128 blk + 8 r + e.
 // At the end of a row segment the 4 waves' states are merged through LDS
 // (the only barriers of the main loop; every wave merges every row of the
 // range in order): common max, rescale, then per 128-column block one wave
