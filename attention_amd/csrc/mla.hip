@@ -111,39 +111,42 @@ struct ProjParams {
   int H, di, dout;
 };
 
-// grid (ceil(dout/128), H, ceil(rows/64)), block 256.  The workgroup owns
-// 128 output columns of one head for 64 rows; its 4 waves split the k range
-// (pairs of 32-wide chunks: wave v takes chunks 2v, 2v+1, 2v+8, 2v+9, ...,
-// all loads of a pair in flight together) and their partial tiles are summed
-// in LDS.  A wave covers 64 rows x 128 columns: 4 row tiles x 8 column tiles
-// of v_mfma_f32_16x16x32, column tile e holding columns base + 8*(l%16) + e,
-// so the absorb layout (columns contiguous in memory) is turned into the B
+// grid (ceil(dout/128), H, ceil(rows/(16 RT))), block 256.  The workgroup
+// owns 128 output columns of one head for 16*RT rows; its 4 waves split the
+// k range (groups of PAIR 32-wide chunks: wave v takes chunks PAIR*v ..
+// PAIR*v + PAIR-1, then the same plus 4*PAIR, ..., all loads of a group in
+// flight together) and their partial tiles are summed in LDS.  A wave covers
+// 16*RT rows x 128 columns: RT row tiles x 8 column tiles of
+// v_mfma_f32_16x16x32, column tile e holding columns base + 8*(l%16) + e, so
+// the absorb layout (columns contiguous in memory) is turned into the B
 // operand by an 8x8 in-register transpose and the value layout (k
-// contiguous) is loaded as is.
-template <int DT, bool ABSORB>
+// contiguous) is loaded as is.  Small batches take RT = 1 (four times the
+// workgroups; the per-head weights are then re-read from L2) and, for a long
+// k range, PAIR = 4 (one round trip for a wave's loads).
+template <int DT, bool ABSORB, int RT, int PAIR>
 __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   using E = Elem<DT>;
   using Ops = MfmaOps<DT>;
   using S = typename E::S;
-  constexpr int kPair = 2;
+  constexpr int kPair = PAIR;
   __shared__ f32x4 red[4][8][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r16 = lane & 15, q4 = lane >> 4;
   const int h = blockIdx.y;
   const int cbase = 128 * blockIdx.x;
-  const int64_t r0 = 64 * static_cast<int64_t>(blockIdx.z);
+  const int64_t r0 = 16 * RT * static_cast<int64_t>(blockIdx.z);
   const int col = min(cbase + 8 * r16, p.dout - 8);  // clamped load column
   const int nch = p.di / 32;
   const char* xb = static_cast<const char*>(p.x);
   const char* wb = static_cast<const char*>(p.w);
   S* out = static_cast<S*>(p.out);
-  f32x4 acc[4][8];
+  f32x4 acc[RT][8];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[rt][e] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int c0 = kPair * wv; c0 < nch; c0 += 4 * kPair) {
-    u32x4 bop[kPair][8], a[kPair][4];
+    u32x4 bop[kPair][8], a[kPair][RT];
 #pragma unroll
     for (int u = 0; u < kPair; ++u) {
       const int c = min(c0 + u, nch - 1);  // a missing second chunk repeats the first, weight 0 below
@@ -162,25 +165,25 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
               wb + ((static_cast<int64_t>(h) * p.dout + col + e) * p.di + k0) * 2);
       }
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         int64_t row = r0 + 16 * rt + r16;
         if (row >= p.rows) row = p.rows - 1;
         a[u][rt] = *reinterpret_cast<const u32x4*>(xb + ((row * p.H + h) * p.di + k0) * 2);
       }
       if (c0 + u >= nch) {
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) a[u][rt] = u32x4{0u, 0u, 0u, 0u};
+        for (int rt = 0; rt < RT; ++rt) a[u][rt] = u32x4{0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
     for (int u = 0; u < kPair; ++u)
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[rt][e] = Ops::mma32(a[u][rt], bop[u][e], acc[rt][e]);
   }
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[wv][e][lane] = acc[rt][e];
     __syncthreads();
@@ -1978,11 +1981,24 @@ template <int DT>
 void launch_project(const ProjParams& prm, bool absorb, bool mfma, hipStream_t st) {
   if constexpr (DT != QD_DTYPE_F32) {
     if (mfma) {
-      const dim3 grid((prm.dout + 127) / 128, prm.H, static_cast<unsigned>((prm.rows + 63) / 64));
-      if (absorb)
-        hipLaunchKernelGGL((mla_project_mfma_kernel<DT, true>), grid, dim3(256), 0, st, prm);
-      else
-        hipLaunchKernelGGL((mla_project_mfma_kernel<DT, false>), grid, dim3(256), 0, st, prm);
+      // 64-row workgroups when they already fill the GPU twice over, else
+      // 16-row ones (grid.z stays within 65535: rows are few then).
+      const int64_t col_tiles = (prm.dout + 127) / 128;
+      const bool small = col_tiles * prm.H * ((prm.rows + 63) / 64) < 2 * static_cast<int64_t>(device_cus()) &&
+                         (prm.rows + 15) / 16 <= 65535;
+      const bool long_k = prm.di / 32 >= 16;
+      const dim3 grid(static_cast<unsigned>(col_tiles), prm.H,
+                      static_cast<unsigned>(small ? (prm.rows + 15) / 16 : (prm.rows + 63) / 64));
+      auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, prm); };
+      if (absorb) {
+        if (!small) go(mla_project_mfma_kernel<DT, true, 4, 2>);
+        else if (long_k) go(mla_project_mfma_kernel<DT, true, 1, 4>);
+        else go(mla_project_mfma_kernel<DT, true, 1, 1>);
+      } else {
+        if (!small) go(mla_project_mfma_kernel<DT, false, 4, 2>);
+        else if (long_k) go(mla_project_mfma_kernel<DT, false, 1, 4>);
+        else go(mla_project_mfma_kernel<DT, false, 1, 1>);
+      }
       return;
     }
   }
