@@ -491,16 +491,21 @@ struct MfmaWave {
       }
       // The weights as hi + lo for bf16 (MfmaOps::kSplitWeights): the PV
       // product then sees them to ~2^-17, as the fp32 denominator does.
+      // One 16x16x32 MFMA takes both: a lane's k-block of 8 is its 4 tokens
+      // twice, V in A and [hi, lo] in B (the MFMA sums over any consistent
+      // k order), so the split costs no extra instruction.
       const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
-      const u32x2 pl = {Ops::rest2(pr[0], pr[1], pb[0]), Ops::rest2(pr[2], pr[3], pb[1])};
+      const u32x4 pbl = {pb[0], pb[1], Ops::rest2(pr[0], pr[1], pb[0]), Ops::rest2(pr[2], pr[3], pb[1])};
 #pragma unroll
       for (int d = 0; d < DV; ++d) {
         const int w = d >> 1;
         const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
         const u32x2 a = {__builtin_amdgcn_perm(buf.v[j][1].w[w], buf.v[j][0].w[w], sel),
                          __builtin_amdgcn_perm(buf.v[j][3].w[w], buf.v[j][2].w[w], sel)};
-        acc[j][d] = Ops::pv(a, pb, acc[j][d]);
-        if constexpr (Ops::kSplitWeights) acc[j][d] = Ops::pv(a, pl, acc[j][d]);
+        if constexpr (Ops::kSplitWeights)
+          acc[j][d] = Ops::mma32(u32x4{a[0], a[1], a[0], a[1]}, pbl, acc[j][d]);
+        else
+          acc[j][d] = Ops::pv(a, pb, acc[j][d]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);

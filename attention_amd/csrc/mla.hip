@@ -1028,9 +1028,9 @@ struct WaveTile {
 //            running max by up to 2^kWaveLazyLog2; the accumulators are
 //            rescaled only past that).
 //   PV       16x16x16 with A = C^T from 4 LDS rows (8x8 transposes by byte
-//            permutes) and B = P^T, the lane's own 4 weights (as hi + lo for
-//            bf16: two MFMAs); C tile (blk, e) row r <-> latent column
-//            128 blk + 8 r + e.
+//            permutes) and B = P^T, the lane's own 4 weights (for bf16 as
+//            hi + lo: one 16x16x32 with the 4 tokens twice in A); C tile
+//            (blk, e) row r <-> latent column 128 blk + 8 r + e.
 // At the end of a row segment the 4 waves' states are merged through LDS
 // (the only barriers of the main loop; every wave merges every row of the
 // range in order): common max, rescale, then per 128-column block one wave
@@ -1423,9 +1423,10 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
       // Weights as hi + lo for bf16 (MfmaOps::kSplitWeights); the
       // denominator sums what the PV product uses.
       const u32x2 pb = {Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
-      u32x2 pl = {0u, 0u};
+      u32x4 pbl = {pb[0], pb[1], 0u, 0u};
       if constexpr (Ops::kSplitWeights) {
-        pl = u32x2{Ops::rest2(pr[0], pr[1], pb[0]), Ops::rest2(pr[2], pr[3], pb[1])};
+        pbl[2] = Ops::rest2(pr[0], pr[1], pb[0]);
+        pbl[3] = Ops::rest2(pr[2], pr[3], pb[1]);
         l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
       } else {
         l_run += Ops::sum2(pb[0]) + Ops::sum2(pb[1]);
@@ -1453,8 +1454,12 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
           const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
           const u32x2 a = {__builtin_amdgcn_perm(raw[1][wd], raw[0][wd], sel),
                            __builtin_amdgcn_perm(raw[3][wd], raw[2][wd], sel)};
-          acc[bb][e] = Ops::pv(a, pb, acc[bb][e]);
-          if constexpr (Ops::kSplitWeights) acc[bb][e] = Ops::pv(a, pl, acc[bb][e]);
+          // bf16: one 16x16x32 MFMA over the lane's 4 tokens twice, [hi, lo]
+          // weights in B (any consistent k order sums the same).
+          if constexpr (Ops::kSplitWeights)
+            acc[bb][e] = Ops::mma32(u32x4{a[0], a[1], a[0], a[1]}, pbl, acc[bb][e]);
+          else
+            acc[bb][e] = Ops::pv(a, pb, acc[bb][e]);
         }
       }
     }
