@@ -1475,16 +1475,16 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
 // across workgroups (meta[row] = {first, count >= 2}); the partial of
 // workgroup k is in slot k + row, for the k in [first, first + count) whose
 // tile range is not empty (with fewer tiles than workgroups some are).  The
-// log-sum-exp combine of online_softmax.cuh:17-24 (empty partials skipped,
-// an all-empty row gives zeros) is evaluated in two passes: every partial's
-// {m, l} at once (one per lane), then the weighted sum of the accumulators,
-// four partials' loads in flight at a time.
+// partials are folded in workgroup order with the log-sum-exp merge of
+// online_softmax.cuh:17-24 (empty partials skipped, an all-empty row gives
+// zeros), kBatch of them loaded per memory round trip: one trip after the
+// meta entry covers a typical row.
 template <int DT>
 __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
   using E = Elem<DT>;
   using S = typename E::S;
   constexpr int kAcc = 8;
-  constexpr int kBatch = 4;
+  constexpr int kBatch = 8;
   const int lane = threadIdx.x & 63;
   const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (wid >= static_cast<int64_t>(p.B) * p.T * p.H) return;
@@ -1498,52 +1498,40 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
   auto present = [&](int k) {
     return static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
   };
-  // Pass 1: M = max m over non-empty partials.
-  float M = -INFINITY;
-  for (int c = 0; c < nwg; c += 64) {
-    const int k = first + c + lane;
-    float m = -INFINITY;
-    if (c + lane < nwg && present(k)) {
-      const float* pr = base + k * stride;
-      if (pr[1] != 0.f) m = pr[0];
-    }
-    M = fmaxf(M, wave_max(m));
-  }
-  // Pass 2: weights e^(m_k - M), L = sum w_k l_k, acc = sum w_k acc_k.
-  float L = 0.f;
+  float M = -INFINITY, L = 0.f;
   float acc[kAcc];
 #pragma unroll
   for (int j = 0; j < kAcc; ++j) acc[j] = 0.f;
-  for (int c = 0; c < nwg; c += 64) {
-    const int n = min(64, nwg - c);
-    const int k = first + c + lane;
-    float wgt = 0.f, lw = 0.f;
-    if (lane < n && present(k)) {
-      const float* pr = base + k * stride;
-      const float l = pr[1];
-      if (l != 0.f) {
-        wgt = fast_exp2((pr[0] - M) * kLog2e);
-        lw = wgt * l;
-      }
-    }
-    L += wave_sum(lw);
-    for (int t0 = 0; t0 < n; t0 += kBatch) {
-      float v[kBatch][kAcc];
-      float wt[kBatch];
+  for (int c = 0; c < nwg; c += kBatch) {
+    float ms[kBatch], ls[kBatch], v[kBatch][kAcc];
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        wt[t] = t0 + t < n ? __shfl(wgt, t0 + t) : 0.f;
-        const float* pr = base + (first + c + min(t0 + t, n - 1)) * stride + 2;
+    for (int t = 0; t < kBatch; ++t) {
+      ms[t] = -INFINITY;
+      ls[t] = 0.f;
+#pragma unroll
+      for (int j = 0; j < kAcc; ++j) v[t][j] = 0.f;
+      const int k = first + c + t;
+      if (c + t < nwg && present(k)) {  // wave-uniform
+        const float* pr = base + k * stride;
+        ms[t] = pr[0];
+        ls[t] = pr[1];
 #pragma unroll
         for (int j = 0; j < kAcc; ++j) {
           const int d = lane + 64 * j;
-          v[t][j] = (wt[t] != 0.f && d < p.Dc) ? pr[d] : 0.f;
+          if (d < p.Dc) v[t][j] = pr[2 + d];
         }
       }
+    }
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t)
+    for (int t = 0; t < kBatch; ++t) {
+      if (ls[t] == 0.f) continue;  // absent or empty partial
+      const float mn = fmaxf(M, ms[t]);
+      const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
+      const float bw = fast_exp2((ms[t] - mn) * kLog2e);
+      L = a * L + bw * ls[t];
 #pragma unroll
-        for (int j = 0; j < kAcc; ++j) acc[j] = fmaf(wt[t], v[t][j], acc[j]);
+      for (int j = 0; j < kAcc; ++j) acc[j] = a * acc[j] + bw * v[t][j];
+      M = mn;
     }
   }
   S* orow = static_cast<S*>(p.out) + wid * p.Dc;
