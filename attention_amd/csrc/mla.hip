@@ -1974,10 +1974,12 @@ template <int DT>
 void launch_project(const ProjParams& prm, bool absorb, bool mfma, hipStream_t st) {
   if constexpr (DT != QD_DTYPE_F32) {
     if (mfma) {
-      // 64-row workgroups when they already fill the GPU twice over, else
-      // 16-row ones (grid.z stays within 65535: rows are few then).
+      // 64-row workgroups when they already fill the GPU twice over and
+      // their row tiles are full, else 16-row ones (grid.z stays within
+      // 65535: rows are few then).
       const int64_t col_tiles = (prm.dout + 127) / 128;
-      const bool small = col_tiles * prm.H * ((prm.rows + 63) / 64) < 2 * static_cast<int64_t>(device_cus()) &&
+      const bool small = (prm.rows < 64 ||
+                          col_tiles * prm.H * ((prm.rows + 63) / 64) < 2 * static_cast<int64_t>(device_cus())) &&
                          (prm.rows + 15) / 16 <= 65535;
       const bool long_k = prm.di / 32 >= 16;
       const dim3 grid(static_cast<unsigned>(col_tiles), prm.H,

@@ -198,6 +198,7 @@ PROJ_SHAPES = [
     ("rows70-fp16-value", False, (35, 2, 8, 96), 40, torch.float16),
     ("long-k-absorb", True, (4, 1, 8, 512), 64, torch.bfloat16),           # 16-row tiles, 4 chunks a wave
     ("big-value", False, (256, 1, 128, 512), 128, torch.bfloat16),         # 512 workgroups: 64-row tiles
+    ("big-absorb", True, (64, 1, 128, 128), 512, torch.bfloat16),          # 512 workgroups: 64-row tiles
     ("odd-generic", True, (2, 3, 4, 16), 32, torch.bfloat16),
     ("fp32", False, (1, 4, 4, 32), 16, torch.float32),
 ]
