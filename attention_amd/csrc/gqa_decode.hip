@@ -70,7 +70,6 @@ struct DecodeParams {
   int head_chunks;  // generic kernel: ceil(g / kGenericHeads)
   int64_t num_blocks;
   float sl2;  // scale * log2(e)
-  int* counters;  // stream-K path: control region (zero between calls)
   int* meta;      // stream-K path: per sequence {first workgroup, workgroups}
   int wg_waves;   // stream-K path: waves per workgroup
 };
@@ -115,30 +114,6 @@ __device__ __forceinline__ int clamp_page(int32_t phys, int64_t num_blocks) {
   return phys;
 }
 
-
-// Partials exchanged between workgroups inside one kernel are written and
-// read with agent-scope relaxed atomic accesses (the sc1 cache policy):
-// each access is coherent across the XCDs' separate L2s by itself, so no
-// cache-wide writeback or invalidate (an agent-scope fence) is needed.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_agent2(float* p, f32x2 v) {  // p 8-byte aligned
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT));
-}
-
-__device__ __forceinline__ f32x2 load_agent2(const float* p) {  // p 8-byte aligned
-  return __builtin_bit_cast(f32x2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
-}
 
 // Inclusive prefix sum over the 64 lanes.
 // ----------------------------------------------------------------------------
@@ -587,32 +562,20 @@ struct MfmaWave {
   }
 
   // Partial {m (natural-log units), l, acc[D]} of kv-head kvh0+jk, this
-  // lane's head, at w + head*head_stride (head_stride even).  AGENT:
-  // coherent stores for a reader in another workgroup of the same kernel.
-  template <bool AGENT>
+  // lane's head, at w + head*head_stride (head_stride even).
   __device__ void store_partial(const DecodeParams& p, int jk, float* w, int64_t head_stride, float l_tot) {
     if (r16 >= p.g) return;
     w += r16 * head_stride;
     if (q4 == 0) {
-      if constexpr (AGENT) {
-        store_agent(w, m_run[jk] * kLn2);
-        store_agent(w + 1, l_tot);
-      } else {
-        w[0] = m_run[jk] * kLn2;
-        w[1] = l_tot;
-      }
+      w[0] = m_run[jk] * kLn2;
+      w[1] = l_tot;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float* dst = w + 2 + DV * (4 * q4 + i);
 #pragma unroll
-      for (int j = 0; j < DV; j += 2) {
-        const f32x2 v = {acc[jk][j][i], acc[jk][j + 1][i]};
-        if constexpr (AGENT)
-          store_agent2(dst + j, v);
-        else
-          *reinterpret_cast<f32x2*>(dst + j) = v;
-      }
+      for (int j = 0; j < DV; j += 2)
+        *reinterpret_cast<f32x2*>(dst + j) = f32x2{acc[jk][j][i], acc[jk][j + 1][i]};
     }
   }
 };
@@ -640,7 +603,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
     wv.store_direct(p, b, kvh, 0, l_tot);
   } else {
     float* w = p.ws + ((static_cast<int64_t>(b) * p.Hq + kvh * p.g) * p.splits + z) * (D + 2);
-    wv.template store_partial<false>(p, 0, w, static_cast<int64_t>(p.splits) * (D + 2), l_tot);
+    wv.store_partial(p, 0, w, static_cast<int64_t>(p.splits) * (D + 2), l_tot);
   }
 }
 
@@ -910,7 +873,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
           if (whole)
             wv.store_direct(p, b, kvh0, j, l_tot);
           else
-            wv.template store_partial<false>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
+            wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
                                              D + 2, l_tot);
         }
       }
@@ -1238,8 +1201,9 @@ int sk_wg_waves(int kv_heads, int nkv, int head_dim) {
   return 1;
 }
 
-// Bytes of the automatic path's control region (per-sequence counters),
-// which must be zero when a call starts and is zero when it ends.
+// Bytes of the automatic path's control region, reserved for per-sequence
+// counters of an in-kernel merge (no current kernel writes it): it must be
+// zero when a call starts and is zero when it ends.
 size_t control_bytes(int batch) { return (static_cast<size_t>(batch) * sizeof(int) + 255) / 256 * 256; }
 
 struct AutoPlan {
@@ -1331,7 +1295,6 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.head_chunks = (prm.g + kGenericHeads - 1) / kGenericHeads;
   prm.num_blocks = num_blocks;
   prm.sl2 = scale * kLog2e;
-  prm.counters = nullptr;
   prm.meta = nullptr;
   prm.wg_waves = 1;
   return prm;
@@ -1559,7 +1522,6 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, scratch, batch,
                                  q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
                                  ap.wgs, 0);
-  prm.counters = static_cast<int*>(workspace);
   prm.meta = reinterpret_cast<int*>(scratch + ap.meta_offset);
   prm.wg_waves = ap.wg_waves;
   hipStream_t stm = static_cast<hipStream_t>(stream);

@@ -49,8 +49,8 @@ qd_tensor_desc describe(const at::Tensor& t) {
 
 // The automatic path's workspace, one per (device, stream), kept for the
 // life of the process like a BLAS handle's workspace.  It is zero-filled on
-// the stream when created or grown (the library needs its control region
-// zero on entry and leaves it zero), so only the first call on a stream, or
+// the stream when created or grown (the library's reserved control region
+// must be zero on entry and is left zero), so only the first call on a stream, or
 // one that needs a larger workspace, pays for an allocation and a fill.
 // Calls on one stream run in order and share it; calls on different
 // streams never share one.

@@ -143,16 +143,18 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  * kernel occupancy), never from context_lens on the host:
  *   - 16-bit caches with head_dim 64/128/256, block_size a multiple of 16,
  *     group size <= 16 and batch <= 4096: the (sequence, 16-token group)
- *     space is cut into one equal range per resident workgroup; a sequence
- *     split across workgroups is merged (log-sum-exp) by the last of them
- *     to finish, inside the same kernel;
+ *     space is cut into cost-balanced ranges, one per resident workgroup;
+ *     a sequence split across workgroups leaves one partial per workgroup,
+ *     which a second kernel on the same stream folds (log-sum-exp);
  *   - otherwise: the split layout of qd_gqa_decode_launch with the plan of
  *     qd_gqa_decode_plan.
  * The workspace is device memory, 16-byte aligned, of at least
  * qd_gqa_decode_auto_workspace_bytes() bytes.  Its first
- * qd_gqa_decode_auto_control_bytes(batch) bytes hold arrival counters: they
- * must be zero when a call starts, and every call leaves them zero (zero a
- * new workspace once, then reuse it).  The rest is scratch.  Calls that may
+ * qd_gqa_decode_auto_control_bytes(batch) bytes are a reserved control
+ * region (per-sequence counters for an in-kernel merge; the current kernels
+ * do not write it): it must be zero when a call starts, and every call
+ * leaves it zero (zero a new workspace once, then reuse it).  The rest is
+ * scratch.  Calls that may
  * run concurrently (different streams) need different workspaces.
  * Workspace size and partition depend on the current device (hipGetDevice),
  * so query and launch with the same device current.  Does not allocate or
