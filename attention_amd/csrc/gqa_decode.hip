@@ -1060,9 +1060,11 @@ bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int d
 }
 
 #ifndef QD_PREFETCH
-#define QD_PREFETCH 3
+#define QD_PREFETCH 2
 #endif
-// 16-token groups in flight per wave (D <= 128).
+// 16-token groups in flight per wave (D <= 128).  2 measured best for one
+// kv-head per wave on the stream-K path (cfg3's kernel 79.4 -> 78.7 us
+// against 3; 4 spills).
 constexpr int kPrefetch = QD_PREFETCH;
 
 // Stream-K path limits: each wave scans all lengths, so the batch is capped;
