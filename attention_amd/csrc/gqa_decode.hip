@@ -621,10 +621,10 @@ __device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
 // per head (head j4 = lane / 16), D/16 consecutive elements per lane (one
 // vector store).  Partials come from an earlier kernel on the same stream:
 // plain loads.
-template <int D>
+template <int D, int KB>
 struct MergeRows {
   static constexpr int EPL = D / 16;
-  static constexpr int kBatch = 16;  // rows loaded per memory round trip
+  static constexpr int kBatch = KB;  // rows loaded per memory round trip
   int c16;
   float M = -INFINITY, L = 0.f;
   float acc[EPL];
@@ -636,7 +636,7 @@ struct MergeRows {
   }
 
   // Loads row t < kBatch of the batch from `row` (the lane's head) when
-  // `present` (wave-uniform).
+  // `present` (uniform over the lane's 16-lane group).
   __device__ void load(int t, bool present, const float* row) {
     ms[t] = -INFINITY;
     ls[t] = 0.f;
@@ -677,6 +677,28 @@ struct MergeRows {
 #pragma unroll
       for (int t = 0; t < kBatch; ++t) load(t, s0 + t < nrows, base + static_cast<int64_t>(s0 + t) * row_stride);
       fold(nrows - s0);
+    }
+  }
+
+  // Folds the states of the four 16-lane groups (which hold the same head
+  // and columns, over different rows) into each lane: two butterfly
+  // exchanges, each a SoftmaxState::merge (online_softmax.cuh:17-24).
+  __device__ void combine_groups() {
+#pragma unroll
+    for (int off = 16; off <= 32; off *= 2) {
+      const float mo = __shfl_xor(M, off);
+      const float lo = __shfl_xor(L, off);
+      float ao[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) ao[e] = __shfl_xor(acc[e], off);
+      if (lo == 0.f) continue;
+      const float mn = fmaxf(M, mo);
+      const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
+      const float bb = fast_exp2((mo - mn) * kLog2e);
+      L = a * L + bb * lo;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] = a * acc[e] + bb * ao[e];
+      M = mn;
     }
   }
 
@@ -894,27 +916,40 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   }
 }
 
-// Stream-K merge: grid (Hkv * ceil(g/4), B), block 64; one wave merges up
-// to four heads of one kv-head of one sequence from slots first+b ..
-// first+b+nwg-1, so the heads of a kv-head merge in parallel.  Two
-// dependent memory round trips: the meta entry, then the partial rows.
-template <int D, int DT>
+// Stream-K merge of sequence b = blockIdx.y from slots first+b ..
+// first+b+nwg-1 (its meta entry), block 64.  Two dependent memory round
+// trips: the meta entry, then the partial rows.
+//   RG = 1: grid (ceil(Hq/4), B); one wave merges heads 4*blockIdx.x + j4
+//           (16 lanes per head), KB rows per round trip.  For batches whose
+//           sequences are split over few workgroups.
+//   RG = 4: grid (Hq, B); one wave merges head blockIdx.x, lane group j4
+//           folds rows j4, j4+4, ... (4*KB rows per round trip), then the
+//           four group states are combined.  For sequences split over many
+//           workgroups.
+template <int D, int DT, int KB, int RG>
 __global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
-  const int npass = (p.g + 3) >> 2;
-  const int kvh = blockIdx.x / npass;
-  const int pass = blockIdx.x - kvh * npass;
   const int b = blockIdx.y;
   const int first = p.meta[2 * b];
   const int nwg = p.meta[2 * b + 1];
   if (nwg <= 1) return;  // written directly, or an empty sequence (zero-filled)
   const int j4 = (threadIdx.x & 63) >> 4;
-  const bool active = j4 < min(4, p.g - 4 * pass);
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
-  const int64_t h = static_cast<int64_t>(kvh) * p.g + 4 * pass + (active ? j4 : 0);
-  MergeRows<D> mr;
-  mr.fold_rows(p.ws + static_cast<int64_t>(first + b) * slot_floats + h * (D + 2), slot_floats, nwg);
-  mr.template store<DT>(active, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
+  const float* slots = p.ws + static_cast<int64_t>(first + b) * slot_floats;
+  MergeRows<D, KB> mr;
+  if constexpr (RG == 1) {
+    const int hh = 4 * blockIdx.x + j4;
+    const bool active = hh < p.Hq;
+    const int64_t h = active ? hh : 0;
+    mr.fold_rows(slots + h * (D + 2), slot_floats, nwg);
+    mr.template store<DT>(active, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
+  } else {
+    const int64_t h = blockIdx.x;
+    const int nrows = nwg > j4 ? (nwg - j4 + RG - 1) / RG : 0;
+    mr.fold_rows(slots + (h + static_cast<int64_t>(j4) * p.Hq) * (D + 2), RG * slot_floats, nrows);
+    mr.combine_groups();
+    mr.template store<DT>(j4 == 0, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
+  }
 }
 
 // ----------------------------------------------------------------------------
@@ -1120,17 +1155,30 @@ KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv) {
   return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D, nkv) : pick_mfma_sk<QD_DTYPE_BF16>(D, nkv);
 }
 
-template <int DT>
+template <int DT, int KB, int RG>
 KernelFn pick_merge_sk(int D) {
   switch (D) {
-    case 64: return merge_sk_kernel<64, DT>;
-    case 128: return merge_sk_kernel<128, DT>;
-    default: return merge_sk_kernel<256, DT>;
+    case 64: return merge_sk_kernel<64, DT, KB, RG>;
+    case 128: return merge_sk_kernel<128, DT, KB, RG>;
+    default: return merge_sk_kernel<256, DT, KB, RG>;
   }
 }
 
-KernelFn pick_merge_sk_dt(int dtype, int D) {
-  return dtype == QD_DTYPE_F16 ? pick_merge_sk<QD_DTYPE_F16>(D) : pick_merge_sk<QD_DTYPE_BF16>(D);
+// Merge layout for a batch: one wave per head (four row groups, up to 64
+// rows per round trip) while the Hq*B waves fit the GPU at once at the
+// kernel's occupancy (2 waves per SIMD), else four heads per wave with 8
+// rows per round trip (fewer registers, 4 waves per SIMD).
+constexpr int64_t kMergeOneHeadWaves = 2048;
+
+bool merge_one_head_per_wave(int batch, int q_heads) {
+  return static_cast<int64_t>(batch) * q_heads <= kMergeOneHeadWaves;
+}
+
+KernelFn pick_merge_sk_dt(int dtype, int D, bool one_head) {
+  if (one_head)
+    return dtype == QD_DTYPE_F16 ? pick_merge_sk<QD_DTYPE_F16, 16, 4>(D)
+                                 : pick_merge_sk<QD_DTYPE_BF16, 16, 4>(D);
+  return dtype == QD_DTYPE_F16 ? pick_merge_sk<QD_DTYPE_F16, 8, 1>(D) : pick_merge_sk<QD_DTYPE_BF16, 8, 1>(D);
 }
 
 template <int DT>
@@ -1531,9 +1579,11 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   if (stages & QD_STAGE_DECODE)
     hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0,
                        stm, prm);
-  if (stages & QD_STAGE_MERGE)
-    hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim), dim3(kv_heads * ((prm.g + 3) / 4), batch), dim3(64), 0,
-                       stm, prm);
+  if (stages & QD_STAGE_MERGE) {
+    const bool one_head = merge_one_head_per_wave(batch, q_heads);
+    hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim, one_head),
+                       dim3(one_head ? q_heads : (q_heads + 3) / 4, batch), dim3(64), 0, stm, prm);
+  }
   return launch_error();
 }
 

@@ -438,6 +438,26 @@ def test_auto_tiny_items(gpu, lengths):
     assert_close(out, ref, "f16", rows, "tiny")
 
 
+@pytest.mark.parametrize("shape", [
+    # one head per wave (B*Hq <= 2048); the one sequence spans every
+    # workgroup, so each of a wave's four row groups folds 64 rows in
+    # several round trips
+    (torch.bfloat16, 8, 2, 128, 16, [20000]),
+    # four heads per wave (B*Hq > 2048); about 28 workgroups per sequence,
+    # more than one 8-row round trip per head
+    (torch.float16, 256, 16, 64, 16, [3000, 2900, 3100, 2999, 3001, 17, 2800, 3050, 2950]),
+], ids=["one-head-many-rows", "four-heads-many-rows"])
+def test_auto_merge_layouts(gpu, shape):
+    dt, hq, hkv, d, p, lengths = shape
+    say(f"merge layouts: {DT_NAME[dt]} Hq{hq} Hkv{hkv} D{d} lengths {lengths[:3]}... (B={len(lengths)})")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
+                                   dtype=dt, seed=23, exact_pool=True), gpu)
+    ref, rows = oracle_rows(case)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    assert_close(out, ref, DT_NAME[dt], rows, "merge layouts")
+
+
 def test_repeat_calls_deterministic(gpu):
     say("determinism across calls")
     case = to_dev(CONFIGS["cfg3"].make(device="cpu"), gpu)
