@@ -789,11 +789,15 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
     const int bb = c * 64 + lane;
     n_r[c] = bb < B ? seq_groups(p, p.lens[bb]) : 0;
   }
+  // Chunks past the batch hold zeros and are not scanned.
   int64_t carry = 0;
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
-    incl_r[c] = carry + wave_incl_scan_i64(seq_cost(n_r[c]), lane);
-    carry = __shfl(incl_r[c], 63);
+    incl_r[c] = carry;
+    if (c == 0 || c * 64 < B) {
+      incl_r[c] += wave_incl_scan_small(seq_cost(n_r[c]), lane);
+      carry = readlane_i64(incl_r[c], 63);
+    }
   }
   for (int c = 64 * kRegChunks; c < B; c += 64) {  // larger batches: re-read
     const int bb = c + lane;
@@ -838,28 +842,28 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   int64_t cs = 0;
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
-    if (b == B) {
+    if (b == B && c * 64 < B) {
       const int bb = c * 64 + lane;
       const int cnt = __popcll(__ballot(bb < B && incl_r[c] <= c0));
       if (cnt < min(64, B - c * 64)) {
         b = c * 64 + cnt;
-        cs = __shfl(incl_r[c] - seq_cost(n_r[c]), cnt);
+        cs = readlane_i64(incl_r[c] - seq_cost(n_r[c]), cnt);
       }
     }
   }
   if (b == B) {
-    carry = __shfl(incl_r[kRegChunks - 1], 63);
+    carry = readlane_i64(incl_r[kRegChunks - 1], 63);
     for (int c = 64 * kRegChunks; c < B; c += 64) {
       const int bb = c + lane;
       const int64_t n = bb < B ? seq_cost(seq_groups(p, p.lens[bb])) : 0;
-      const int64_t incl = carry + wave_incl_scan_i64(n, lane);
+      const int64_t incl = carry + wave_incl_scan_small(n, lane);
       const int cnt = __popcll(__ballot(bb < B && incl <= c0));
       if (cnt < min(64, B - c)) {
         b = c + cnt;
-        cs = __shfl(incl - n, cnt);
+        cs = readlane_i64(incl - n, cnt);
         break;
       }
-      carry = __shfl(incl, 63);
+      carry = readlane_i64(incl, 63);
     }
   }
   if (b >= B) return;  // unreachable when C is consistent
@@ -933,6 +937,7 @@ __global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
   const int first = p.meta[2 * b];
   const int nwg = p.meta[2 * b + 1];
   if (nwg <= 1) return;  // written directly, or an empty sequence (zero-filled)
+  if (first < 0 || first + nwg > p.splits) return;  // spans are always inside [0, W)
   const int j4 = (threadIdx.x & 63) >> 4;
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
   const float* slots = p.ws + static_cast<int64_t>(first + b) * slot_floats;

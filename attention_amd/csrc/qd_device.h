@@ -96,6 +96,38 @@ __device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t x, int lane) {
   return x;
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_add_i32(int x) {
+  // Lanes whose DPP source is outside the row (or whose row is masked off)
+  // add the `old` operand, 0.
+  return x + __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Inclusive prefix sum over the wave's 64 lanes of non-negative values.
+// When every lane's value is below 2^25 (the 64-lane total then fits in 31
+// bits) it is a 32-bit DPP scan: row_shr 1, 2, 4, 8 within each 16-lane
+// row, then row_bcast:15 (rows 1 and 3 add lane 15 of the row before) and
+// row_bcast:31 (rows 2 and 3 add lane 31); otherwise the shuffle scan.
+__device__ __forceinline__ int64_t wave_incl_scan_small(int64_t x, int lane) {
+  if (__ballot(x >= (int64_t{1} << 25)) != 0) return wave_incl_scan_i64(x, lane);
+  int y = static_cast<int>(x);
+  y = dpp_add_i32<0x111, 0xF>(y);  // row_shr:1
+  y = dpp_add_i32<0x112, 0xF>(y);  // row_shr:2
+  y = dpp_add_i32<0x114, 0xF>(y);  // row_shr:4
+  y = dpp_add_i32<0x118, 0xF>(y);  // row_shr:8
+  y = dpp_add_i32<0x142, 0xA>(y);  // row_bcast:15
+  y = dpp_add_i32<0x143, 0xC>(y);  // row_bcast:31
+  return y;
+}
+
+// Lane `src` (wave-uniform) of a 64-bit value, through v_readlane.
+__device__ __forceinline__ int64_t readlane_i64(int64_t x, int src) {
+  const uint64_t u = static_cast<uint64_t>(x);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(u), src);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), src);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // ----------------------------------------------------------------------------
 // MFMA wrappers
 // ----------------------------------------------------------------------------
