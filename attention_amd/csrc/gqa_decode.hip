@@ -370,9 +370,15 @@ struct MfmaWave {
     q4 = lane >> 4;
   }
 
-  __device__ void begin_item(const DecodeParams& p, int b, int kvh0, int valid_tokens) {
+  // Starts item (b, kvh0..) whose run() begins at group g_first.  The page
+  // table window of g_first is loaded before the query, so the first K/V
+  // loads wait for the table alone; the query is needed only at compute.
+  __device__ void begin_item(const DecodeParams& p, int b, int kvh0, int valid_tokens, int g_first) {
     const int g = p.g;
     const bool head_ok = r16 < g;
+    trow = p.table + static_cast<int64_t>(b) * p.maxP;
+    wbase = g_first / (p.P >> 4);
+    tblv = (lane < p.maxP - wbase) ? trow[wbase + lane] : 0;
 #pragma unroll
     for (int j = 0; j < NKV; ++j) {
       const char* qp = static_cast<const char*>(p.q) +
@@ -390,7 +396,6 @@ struct MfmaWave {
     }
     kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh0) * D * 2;
     vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh0) * D * 2;
-    trow = p.table + static_cast<int64_t>(b) * p.maxP;
     len = valid_tokens;
   }
 
@@ -496,10 +501,12 @@ struct MfmaWave {
   __device__ void run(const DecodeParams& p, int ga, int gb, char* ktile) {
     const int gpp = p.P >> 4;
     for (int g_lo = ga; g_lo < gb;) {
-      wbase = g_lo / gpp;
+      if (g_lo != ga) {  // the first window came with begin_item
+        wbase = g_lo / gpp;
+        tblv = (lane < p.maxP - wbase) ? trow[wbase + lane] : 0;
+      }
       const int g_hi = min(gb, (wbase + 64) * gpp);
       const int n = g_hi - g_lo;
-      tblv = (lane < p.maxP - wbase) ? trow[wbase + lane] : 0;
       Buf buf[PF];
       int i = 0;
       if (n >= 2 * PF - 1) {
@@ -596,7 +603,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
   __shared__ __align__(16) char ktile[KTile<D>::kBytes];
   MfmaWave<D, DT, PF, 1> wv;
   wv.init_lane();
-  wv.begin_item(p, b, kvh, ci.te);
+  wv.begin_item(p, b, kvh, ci.te, ci.tb >> 4);
   wv.run(p, ci.tb >> 4, (ci.te + 15) >> 4, ktile);  // tb is page aligned
   const float l_tot = wv.total_l(0);
   if (ci.nch <= 1) {
@@ -782,12 +789,14 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   // the lengths of sequences c*64 + lane, and the group counts and the
   // running sums of the costs stay in registers.
   constexpr int kRegChunks = 4;
+  int len_r[kRegChunks];
   int n_r[kRegChunks];
   int64_t incl_r[kRegChunks];
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
     const int bb = c * 64 + lane;
-    n_r[c] = bb < B ? seq_groups(p, p.lens[bb]) : 0;
+    len_r[c] = bb < B ? clamp_len(p, p.lens[bb]) : 0;
+    n_r[c] = (len_r[c] + 15) >> 4;
   }
   // Chunks past the batch hold zeros and are not scanned.
   int64_t carry = 0;
@@ -833,13 +842,15 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   const int64_t wu_cap = C / kSkGroupCost;
   const int Wu = static_cast<int>(wu_cap < W ? (wu_cap > 0 ? wu_cap : 1) : W);
   if (w >= Wu || C == 0) return;
-  const int64_t c0 = static_cast<int64_t>(w) * C / Wu;
-  const int64_t c1 = static_cast<int64_t>(w + 1) * C / Wu;
+  const int64_t c0 = div_nonneg(static_cast<int64_t>(w) * C, Wu);
+  const int64_t c1 = div_nonneg(static_cast<int64_t>(w + 1) * C, Wu);
 
   // The sequence whose unit range holds c0 (the first whose running cost
-  // end exceeds c0) and its first unit cs.
+  // end exceeds c0) and its first unit cs; its clamped length comes from the
+  // registers when the prologue holds it.
   int b = B;
   int64_t cs = 0;
+  int len_first = -1;
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
     if (b == B && c * 64 < B) {
@@ -848,6 +859,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
       if (cnt < min(64, B - c * 64)) {
         b = c * 64 + cnt;
         cs = readlane_i64(incl_r[c] - seq_cost(n_r[c]), cnt);
+        len_first = __builtin_amdgcn_readlane(len_r[c], cnt);
       }
     }
   }
@@ -869,7 +881,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   if (b >= B) return;  // unreachable when C is consistent
 
   // Workgroup whose unit range holds unit x.
-  auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * Wu - 1) / C); };
+  auto wg_of = [&](int64_t x) { return static_cast<int>(div_nonneg((x + 1) * Wu - 1, C)); };
   // Groups of the current sequence whose unit lies below x.
   auto groups_below = [&](int64_t x, int64_t x0, int nb) {
     if (x <= x0) return 0;
@@ -882,7 +894,8 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   wv.init_lane();
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
   while (true) {
-    const int len = clamp_len(p, p.lens[b]);
+    const int len = len_first >= 0 ? len_first : clamp_len(p, p.lens[b]);
+    len_first = -1;
     const int nb = (len + 15) >> 4;
     const int64_t x0 = cs + kSkSeqCost;  // unit of group 0
     const int i0 = groups_below(c0, x0, nb);
@@ -891,7 +904,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
       const bool whole = i0 == 0 && i1 == nb;
       float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
       for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
-        wv.begin_item(p, b, kvh0, len);
+        wv.begin_item(p, b, kvh0, len, i0);
         wv.run(p, i0, i1, ktile[wid]);
 #pragma unroll
         for (int j = 0; j < NKV; ++j) {

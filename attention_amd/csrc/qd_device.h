@@ -120,6 +120,14 @@ __device__ __forceinline__ int64_t wave_incl_scan_small(int64_t x, int lane) {
   return y;
 }
 
+// n / d for n >= 0, d > 0: a 32-bit division when both fit (the 64-bit one
+// expands to several times the instructions).
+__device__ __forceinline__ int64_t div_nonneg(int64_t n, int64_t d) {
+  if (static_cast<uint64_t>(n) <= 0xFFFFFFFFull && static_cast<uint64_t>(d) <= 0xFFFFFFFFull)
+    return static_cast<uint32_t>(n) / static_cast<uint32_t>(d);
+  return n / d;
+}
+
 // Lane `src` (wave-uniform) of a 64-bit value, through v_readlane.
 __device__ __forceinline__ int64_t readlane_i64(int64_t x, int src) {
   const uint64_t u = static_cast<uint64_t>(x);
