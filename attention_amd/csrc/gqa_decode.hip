@@ -1249,14 +1249,23 @@ int resident_blocks(KernelFn fn, int threads) {
   return blocks;
 }
 
-#ifndef QD_SK_DUAL_MIN_KV
-#define QD_SK_DUAL_MIN_KV 8
-#endif
-// Kv-heads per wave on the stream-K path: two when there are at least
-// QD_SK_DUAL_MIN_KV (an even number of) kv-heads and head_dim <= 128, so a
-// workgroup of one wave per SIMD still covers whole rows; else one.
-int sk_kv_per_wave(int kv_heads, int head_dim) {
-  return (head_dim <= 128 && kv_heads % 2 == 0 && kv_heads >= QD_SK_DUAL_MIN_KV) ? 2 : 1;
+// Kv-heads per wave on the stream-K path.  One (a workgroup of up to 8
+// waves holds two per SIMD) hides the start of each item behind the other
+// wave of its SIMD: it wins on short and ragged batches (cfg2 decode 54.9
+// against 56.9 us, cfg5 101.6 against 103.8 us).  Two (one wave per SIMD,
+// 512 registers, 8 or more kv-heads with head_dim <= 128) stream faster once
+// every workgroup has long runs (cfg4 333 against 342 us): chosen when the
+// batch's static token capacity, B * max_pages * block_size, is at least
+// kSkDualTokensPerWg per resident workgroup (cfg4: 4096, cfg5: 1024, cfg2:
+// 512 on 256 CUs).  Static shapes only, as gqa_decode_auto's heuristic
+// (core.py:80-96).
+constexpr int64_t kSkDualTokensPerWg = 2048;
+
+bool sk_dual_applies(int batch, int kv_heads, int head_dim, int block_size, int max_pages,
+                     int resident_wgs) {
+  if (head_dim > 128 || kv_heads % 2 != 0 || kv_heads < 8) return false;
+  const int64_t cap = static_cast<int64_t>(batch) * max_pages * block_size;
+  return cap >= kSkDualTokensPerWg * resident_wgs;
 }
 
 // Waves per stream-K workgroup: the largest divisor of kv_heads / nkv that
@@ -1294,12 +1303,17 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
   const size_t ctrl = control_bytes(batch);
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
-    const int nkv = sk_kv_per_wave(kv_heads, head_dim);
-    const int nw = sk_wg_waves(kv_heads, nkv, head_dim);
+    int nkv = 1;
+    int nw = sk_wg_waves(kv_heads, nkv, head_dim);
+    int resident = resident_blocks(pick_mfma_sk_dt(dtype, head_dim, nkv), 64 * nw);
+    if (sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
+      nkv = 2;
+      nw = sk_wg_waves(kv_heads, nkv, head_dim);
+      resident = resident_blocks(pick_mfma_sk_dt(dtype, head_dim, nkv), 64 * nw);
+    }
     const int64_t gmax = static_cast<int64_t>(batch) *
                          ((static_cast<int64_t>(max_pages) * block_size + 15) / 16);
-    int64_t w = static_cast<int64_t>(resident_blocks(pick_mfma_sk_dt(dtype, head_dim, nkv), 64 * nw)) *
-                kSkOversubscribe;
+    int64_t w = static_cast<int64_t>(resident) * kSkOversubscribe;
     const int64_t by_work = (gmax + kSkMinGroups - 1) / kSkMinGroups;
     if (w > by_work) w = by_work;
     if (w < 1) w = 1;

@@ -458,6 +458,29 @@ def test_auto_merge_layouts(gpu, shape):
     assert_close(out, ref, DT_NAME[dt], rows, "merge layouts")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_auto_wave_shapes_by_capacity(gpu, dtype):
+    """The automatic path serves two kv-heads per wave when the batch's
+    static capacity (B * max_pages * block_size) is large, else one.  The
+    same lengths under a narrow and under a wide (-1 padded) page table run
+    both wave shapes; each must match the oracle."""
+    hq, hkv, d, p = 32, 8, 128, 16
+    lengths = [3000, 1, 4097, 2000, 17, 0, 5000, 700]
+    B = len(lengths)
+    q, k, v, table, lens = make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
+                                            block_size=p, dtype=dtype, seed=19, exact_pool=True)
+    for maxp in (table.shape[1], 8192):
+        kind, waves, _, _ = cabi.auto_info(B, hq, hkv, d, p, maxp, cabi.DTYPE[dtype])
+        say(f"wave shapes: {DT_NAME[dtype]} max_pages={maxp} kind={kind} waves={waves}")
+        tpad = torch.full((B, maxp), -1, dtype=torch.int32)
+        tpad[:, :table.shape[1]] = table
+        case = to_dev((q, k, v, tpad, lens), gpu)
+        ref, rows = oracle_rows(case)
+        out = attention_amd.gqa_decode(*case)
+        torch.cuda.synchronize()
+        assert_close(out, ref, DT_NAME[dtype], rows, f"max_pages={maxp}")
+
+
 def test_repeat_calls_deterministic(gpu):
     say("determinism across calls")
     case = to_dev(CONFIGS["cfg3"].make(device="cpu"), gpu)
