@@ -619,15 +619,16 @@ __device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
   return (clamp_len(p, len_raw) + 15) >> 4;
 }
 
-// Merge of the partials of up to four heads of one kv-head, in place of the
-// reference's merge kernel (gqa_decode.cu:74-87).  Each partial row is
-// {m (natural log), l, acc[D]}; rows are folded in order with
-// SoftmaxState::merge (online_softmax.cuh:17-24): a row with l == 0 is
-// skipped, the running state is rescaled by exp(m - max).  Output acc/l
-// rounded once, zeros when l == 0 (gqa_decode.cu:84-86).  One wave: 16 lanes
-// per head (head j4 = lane / 16), D/16 consecutive elements per lane (one
-// vector store).  Partials come from an earlier kernel on the same stream:
-// plain loads.
+// Merge of partial rows, in place of the reference's merge kernel
+// (gqa_decode.cu:74-87).  Each partial row is {m (natural log), l, acc[D]};
+// a lane group folds its rows in order with SoftmaxState::merge
+// (online_softmax.cuh:17-24): a row with l == 0 is skipped, the running
+// state is rescaled by exp(m - max).  Output acc/l rounded once, zeros when
+// l == 0 (gqa_decode.cu:84-86).  Each 16-lane group (j4 = lane / 16) holds
+// one head's state, D/16 consecutive elements per lane (one vector store):
+// four heads per wave, or one head whose rows the four groups share
+// (combine_groups).  Partials come from an earlier kernel on the same
+// stream: plain loads.
 template <int D, int KB>
 struct MergeRows {
   static constexpr int EPL = D / 16;
