@@ -148,6 +148,29 @@ def test_plan_values_for_configs():
     assert cabi.plan(256, 40, 8, 128, 32, 32) == (1, 32)
 
 
+@pytest.mark.skipif(torch.cuda.is_available(),
+                    reason="wave counts assume the CPU-only occupancy fallback (256 CUs, one workgroup each)")
+def test_auto_wave_shape_by_capacity():
+    """The automatic path's wave shape follows the batch's static token
+    capacity B*max_pages*P: one kv-head per wave (8-wave workgroups for 8
+    kv-heads) below 2048 tokens per resident workgroup, two kv-heads per wave
+    (4-wave workgroups) at or above it.  Without a GPU the occupancy query
+    falls back to 256 CUs and one workgroup each, so 2048 tokens per
+    workgroup is a capacity of 524288 tokens."""
+    bf16 = cabi.DTYPE[torch.bfloat16]
+    # cfg2 (131072 tokens) and cfg5 (262144): one kv-head per wave.
+    assert cabi.auto_info(32, 32, 8, 128, 16, 256, bf16)[:2] == (1, 256 * 8)
+    assert cabi.auto_info(256, 40, 8, 128, 32, 32, cabi.DTYPE[torch.float16])[:2] == (1, 256 * 8)
+    # cfg4 (1048576 tokens): two kv-heads per wave.
+    assert cabi.auto_info(8, 64, 8, 128, 16, 8192, bf16)[:2] == (1, 256 * 4)
+    # The threshold itself, and just below it.
+    assert cabi.auto_info(8, 64, 8, 128, 16, 4096, bf16)[:2] == (1, 256 * 4)
+    assert cabi.auto_info(8, 64, 8, 128, 16, 4095, bf16)[:2] == (1, 256 * 8)
+    # Two kv-heads per wave needs 8+ (an even number of) kv-heads and D <= 128.
+    assert cabi.auto_info(8, 28, 4, 128, 16, 8192, bf16)[:2] == (1, 256 * 4)  # 4 kv-heads: 4 waves
+    assert cabi.auto_info(8, 64, 8, 256, 16, 8192, bf16)[:2] == (1, 256 * 4)  # D 256: 4 waves, one each
+
+
 def test_plan_rejects_bad_shapes():
     s, c = ctypes.c_int(), ctypes.c_int()
     assert cabi.lib().qd_gqa_decode_plan(1, 8, 0, 64, 16, 4, 1, 256, ctypes.byref(s), ctypes.byref(c)) != 0
