@@ -53,35 +53,72 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out, flush=True)
 
 
-def hip_library_cmd() -> list[str]:
-    return [_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
-            os.path.join(CSRC, "gqa_decode.hip"), os.path.join(CSRC, "kv_append.hip"),
-            os.path.join(CSRC, "validate.hip"), os.path.join(CSRC, "mla.hip"),
+HIP_SOURCES = ["gqa_decode", "kv_append", "validate", "mla"]
+OBJ_DIR = os.path.join(ROOT, "_build", "obj")
+
+
+def hip_object_cmd(name: str) -> list[str]:
+    return [_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", "-c", os.path.join(CSRC, f"{name}.hip"),
+            "-o", os.path.join(OBJ_DIR, f"{name}.o")]
+
+
+def hip_link_cmd() -> list[str]:
+    return [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC",
+            *[os.path.join(OBJ_DIR, f"{n}.o") for n in HIP_SOURCES],
             "-o", HIP_LIB + ".tmp", f"-Wl,-rpath,{ROCM}/lib"]
 
 
-def torch_binding_cmd() -> list[str]:
+def _stale(name: str) -> bool:
+    obj = os.path.join(OBJ_DIR, f"{name}.o")
+    if not os.path.exists(obj):
+        return True
+    deps = [os.path.join(CSRC, f"{name}.hip"), os.path.join(CSRC, "qd_device.h"),
+            os.path.join(INCLUDE, "qd_attention.h")]
+    return any(os.path.getmtime(d) > os.path.getmtime(obj) for d in deps)
+
+
+def _torch_flags() -> tuple[list[str], str]:
     import torch  # noqa: F401  (paths only)
     from torch.utils.cpp_extension import include_paths, library_paths
 
     abi = int(getattr(__import__("torch")._C, "_GLIBCXX_USE_CXX11_ABI", True))
     incs = [f"-I{p}" for p in include_paths()] + [f"-I{INCLUDE}", f"-I{ROCM}/include"]
-    torch_lib = library_paths()[0]
-    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared",
-            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
-            *incs, os.path.join(CSRC, "torch_ops.cpp"),
-            "-o", TORCH_LIB + ".tmp",
+    return (["-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", *incs],
+            library_paths()[0])
+
+
+def torch_object_cmd() -> list[str]:
+    flags, _ = _torch_flags()
+    return ["g++", "-O2", "-std=c++17", "-fPIC", *flags, "-c", os.path.join(CSRC, "torch_ops.cpp"),
+            "-o", os.path.join(OBJ_DIR, "torch_ops.o")]
+
+
+def torch_link_cmd() -> list[str]:
+    _, torch_lib = _torch_flags()
+    return ["g++", "-shared", os.path.join(OBJ_DIR, "torch_ops.o"), "-o", TORCH_LIB + ".tmp",
             f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-lamdhip64",
             f"-L{LIB_DIR}", "-l:libqd_attention.so",
             "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
 
 
-def build(verbose: bool = False) -> None:
-    """Compile both libraries (always; no up-to-date check)."""
+def build(verbose: bool = False, incremental: bool = False) -> None:
+    """Compile both libraries (every source unless ``incremental``, which
+    recompiles only sources newer than their object): one compiler process
+    per source file, concurrently, then the two links."""
     os.makedirs(LIB_DIR, exist_ok=True)
-    _run(hip_library_cmd(), verbose)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    cmds = [hip_object_cmd(n) for n in HIP_SOURCES if not incremental or _stale(n)]
+    torch_obj = os.path.join(OBJ_DIR, "torch_ops.o")
+    if (not incremental or not os.path.exists(torch_obj)
+            or os.path.getmtime(os.path.join(CSRC, "torch_ops.cpp")) > os.path.getmtime(torch_obj)
+            or os.path.getmtime(os.path.join(INCLUDE, "qd_attention.h")) > os.path.getmtime(torch_obj)):
+        cmds.append(torch_object_cmd())
+    with ThreadPoolExecutor(max_workers=max(1, len(cmds))) as ex:
+        for f in [ex.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    _run(hip_link_cmd(), verbose)
     os.replace(HIP_LIB + ".tmp", HIP_LIB)
-    _run(torch_binding_cmd(), verbose)
+    _run(torch_link_cmd(), verbose)
     os.replace(TORCH_LIB + ".tmp", TORCH_LIB)
 
 
@@ -97,5 +134,5 @@ def build_parallel(extra: list[list[str]] | None = None, verbose: bool = False) 
 
 
 if __name__ == "__main__":
-    build(verbose="-v" in sys.argv)
+    build(verbose="-v" in sys.argv, incremental="-i" in sys.argv)
     print("built", HIP_LIB, TORCH_LIB)

@@ -750,7 +750,11 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_mfma_kernel(MlaPara
   auto step = [&](int j, u32x4 (&stu)[CPT]) {
     stage(j, stu);
     // Tile j is in LDS for every wave, and every wave is past tile j-1 (so
-    // the buffer written next, tile j-2's, is free).
+    // the buffer written next, tile j-2's, is free).  This barrier also
+    // publishes wave 0's per-tile metadata: tile_row, flags and masks for
+    // slot j % kMetaSlots (and the row offsets the staging reads) are
+    // written by wave 0 ahead of the pipeline, and no other wave may read
+    // them before it.  Every wave reaches it once per step, live or not.
     lds_barrier();
     const bool live = j < ntiles;
     const int sl = j % kMetaSlots;

@@ -90,48 +90,70 @@ def copy_mode(args) -> None:
                       "ms_per_call": ms, "gbs": gbs}), flush=True)
 
 
-def cpu_baseline(case_cpu, cfg, repeats: int) -> dict:
-    """Times the reference CPU path (oracle/cpu_path.py) on the host cores."""
-    from oracle.cpu_path import reference_cpu_path
-    from attention_amd.cases import algorithmic_bytes
+def cpu_threads() -> tuple[int, dict]:
+    """Threads for the CPU baseline and what they were derived from.
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    q, k, v, table, lens = case_cpu
-    # Sample: the first sequences of the same batch, enough for ~1-3 s per call.
-    lens_l = lens.tolist()
-    nb, toks = 0, 0
-    for L in lens_l:
-        nb += 1
-        toks += L
-        if toks >= 40_000:
-            break
-    sample = (q[:nb], k, v, table[:nb], lens[:nb])
-    reference_cpu_path(*sample)  # warmup
-    # Repeat for about 10 s of CPU work (at least `repeats` calls, at most 30 s).
+    BASELINE.md's plan is one thread per host core (``os.cpu_count()``).  A
+    job on the GPU box is confined to its CPU share (its affinity mask) and
+    gets ``OMP_NUM_THREADS`` set to that share, so the thread count is the
+    smallest of the three: more threads than the cores the process may run
+    on would time oversubscription, not the reference path."""
+    counts = {"os_cpu_count": os.cpu_count() or 1}
+    try:
+        counts["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        counts["affinity_cpus"] = counts["os_cpu_count"]
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        counts["omp_num_threads"] = int(omp)
+    return min(counts.values()), counts
+
+
+def _time_cpu(fn, repeats: int, min_s: float, max_s: float) -> list[float]:
+    """1 warmup call, then timed calls until there are at least `repeats`
+    of them over at least `min_s` seconds, or `max_s` seconds have passed."""
+    fn()
     times = []
     t_start = time.perf_counter()
     while True:
         t0 = time.perf_counter()
-        reference_cpu_path(*sample)
+        fn()
         times.append(time.perf_counter() - t0)
         spent = time.perf_counter() - t_start
-        if (len(times) >= repeats and spent >= 10.0) or spent >= 30.0:
+        if (len(times) >= repeats and spent >= min_s) or spent >= max_s:
             break
+    return times
+
+
+def cpu_baseline(case_cpu, cfg, repeats: int) -> dict:
+    """Times the reference CPU path (oracle/cpu_path.py, the torch CPU ops of
+    reference attention/reference/gqa.py:21-44) on the host cores: the whole
+    batch of the benchmark config, and cfg1 (BASELINE.md's mandatory
+    CPU-path config)."""
+    from oracle.cpu_path import reference_cpu_path
+    from attention_amd.cases import CONFIGS, algorithmic_bytes
+
+    threads, counts = cpu_threads()
+    torch.set_num_threads(threads)
+    q, k, v, table, lens = case_cpu
+    lens_l = lens.tolist()
+    times = _time_cpu(lambda: reference_cpu_path(q, k, v, table, lens), max(5, repeats), 10.0, 30.0)
     t = statistics.median(times)
-    elem = q.element_size()
-    b_sample = algorithmic_bytes(lens_l[:nb], nb, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
-                                 cfg.block_size, elem)
     b_full = algorithmic_bytes(lens_l, len(lens_l), cfg.q_heads, cfg.kv_heads, cfg.head_dim,
-                               cfg.block_size, elem)
-    gbs = b_sample / t / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_call_full_batch_est": round(t * b_full / b_sample * 1e6, 1),
+                               cfg.block_size, q.element_size())
+    c1 = CONFIGS["cfg1"]
+    case1 = c1.make(device="cpu")
+    t1 = statistics.median(_time_cpu(lambda: reference_cpu_path(*case1), 50, 2.0, 10.0))
+    return {"value": round(b_full / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_call": round(t * 1e6, 1),
+            "cfg1_us_per_call": round(t1 * 1e6, 1),
             "sample": (f"oracle/cpu_path.reference_cpu_path (torch CPU ops of reference "
-                       f"attention/reference/gqa.py:21-44) on the first {nb} of {len(lens_l)} "
-                       f"sequences ({toks} tokens) of the same {cfg.name} input, median of "
-                       f"{len(times)} calls after 1 warmup ({sum(times):.1f} s of CPU time): "
-                       f"{t * 1e3:.1f} ms per call"),
+                       f"attention/reference/gqa.py:21-44) on the whole {cfg.name} batch "
+                       f"({len(lens_l)} sequences, {sum(lens_l)} tokens, the same input as the GPU "
+                       f"run), median of {len(times)} calls after 1 warmup ({sum(times):.1f} s): "
+                       f"{t * 1e3:.1f} ms per call; cfg1 (lens 17/100/255/512): "
+                       f"{t1 * 1e6:.0f} us per call"),
+            "threads_from": counts,
             "cpu": _cpu_model()}
 
 
@@ -318,7 +340,7 @@ def mla_mode(args) -> None:
     }
     if not args.no_cpu_baseline:
         from oracle.cpu_path import reference_mla_cpu_path
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        threads, counts = cpu_threads()
         torch.set_num_threads(threads)
         nb = 2
         sample = [c_cpu[k][:nb] for k in ("q_nope", "q_rope")] + [c_cpu["cache"], c_cpu["table"][:nb],
@@ -340,7 +362,7 @@ def mla_mode(args) -> None:
             "sample": (f"oracle/cpu_path.reference_mla_cpu_path (torch CPU ops of reference "
                        f"attention/reference/mla.py:6-34, absorbed) on the first {nb} of {B} sequences "
                        f"({sum(lengths[:nb])} tokens), median of {len(times)} calls: {t * 1e3:.1f} ms"),
-            "cpu": _cpu_model()}
+            "threads_from": counts, "cpu": _cpu_model()}
     print(json.dumps(result), flush=True)
 
 
@@ -516,8 +538,9 @@ def main() -> None:
             case_cpu = tuple(x.cpu() for x in case)
         log("timing the reference CPU path ...")
         result["cpu_baseline"] = cpu_baseline(case_cpu, cfg, args.cpu_repeats)
-        log(f"cpu baseline {result['cpu_baseline']['value']} GB/s on "
-            f"{result['cpu_baseline']['cores']} threads")
+        cb = result["cpu_baseline"]
+        log(f"cpu baseline {cb['value']} GB/s ({cb['us_per_call']} us/call) on {cb['cores']} threads "
+            f"{cb['threads_from']}; cfg1 {cb['cfg1_us_per_call']} us/call")
     print(json.dumps(result), flush=True)
 
 

@@ -94,16 +94,21 @@ def test_config_matches_oracle(gpu, name):
 
 
 def test_cfg4_long_context(gpu):
+    """cfg4 from the CPU-seeded recipe (the same q/K/V as the CPU path would
+    see), every sequence compared with the oracle, one at a time so the
+    fp32 copies stay near 1 GB of host memory."""
     cfg = CONFIGS["cfg4"]
-    say("config cfg4 (device-generated, oracle on 3 sequences)")
-    case = cfg.make(device=gpu, device_gen=True)
+    say("config cfg4 (CPU-seeded recipe, oracle on all 8 sequences)")
+    case_cpu = cfg.make(device="cpu")
+    case = to_dev(case_cpu, gpu)
+    del case_cpu
     out = attention_amd.gqa_decode(*case)
     torch.cuda.synchronize()
-    lens = case[4].cpu().tolist()
-    pick = [int(np.argmax(lens)), int(np.argmin(lens)), 3]
-    ref, rows = oracle_rows(case, pick)
-    assert_close(out, ref, "bf16", rows, "cfg4")
     assert torch.isfinite(out).all()
+    for b in range(cfg.batch):
+        say(f"cfg4 sequence {b} (len {int(case[4][b])})")
+        ref, rows = oracle_rows(case, [b])
+        assert_close(out, ref, "bf16", rows, f"cfg4 sequence {b}")
 
 
 # ----------------------------------------------------------------------------
@@ -196,17 +201,89 @@ def test_workspace_partials_match_oracle(gpu):
 # Bit-exact index handling
 # ----------------------------------------------------------------------------
 
-def _poisoned_case(dev, dtype=torch.bfloat16, lengths=(1, 17, 31, 300, 0, 64), hq=32, hkv=8, d=128, p=16):
+def _poisoned_case(dev, dtype=torch.bfloat16, lengths=(1, 17, 31, 300, 0, 64), hq=32, hkv=8, d=128, p=16,
+                   seed=5):
+    """A case on a pool larger than the used blocks (the recipe's
+    B*max_pages pool), and the same case with every cache slot no sequence
+    uses set to NaN (K) and Inf (V): unused blocks, and the slots past each
+    sequence's length in its last page."""
     q, k, v, table, lens = make_decode_case(lengths=list(lengths), q_heads=hq, kv_heads=hkv,
-                                            head_dim=d, block_size=p, dtype=dtype, seed=5)
+                                            head_dim=d, block_size=p, dtype=dtype, seed=seed)
     used = torch.zeros(k.shape[0], p, dtype=torch.bool)
     for b, L in enumerate(lengths):
-        for t in range(L):
-            used[table[b, t // p], t % p] = True
+        if L <= 0:
+            continue
+        t = torch.arange(L)
+        used[table[b, t // p].long(), t % p] = True
     kp, vp = k.clone(), v.clone()
     kp[~used] = float("nan")
     vp[~used] = float("inf")
     return (q, k, v, table, lens), (q, kp, vp, table, lens)
+
+
+def _ragged_lengths(n, hi, seed):
+    """cfg3-style ragged lengths: uniform in [1, hi], with lengths 1, 16,
+    17, a page boundary minus one and a zero mixed in."""
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in rng.integers(1, hi + 1, n)]
+    for i, x in enumerate((1, 16, 17, 255, 0)):
+        lens[(i * 7) % n] = x
+    return lens
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("wide", [False, True], ids=["narrow-table", "wide-table"])
+def test_poisoned_unused_slots_bitwise_product_path(gpu, dtype, wide):
+    """The product path (attention_amd.gqa_decode: decode_mfma_sk_kernel and
+    merge_sk_kernel) on ragged lengths whose sequences split across
+    workgroups: NaN/Inf in every unused slot and -1 table padding change no
+    output bit.  A narrow page table runs one kv-head per wave, a wide
+    -1-padded one (8192 pages) two kv-heads per wave; the C entry point
+    with a NaN-filled scratch must give the same bits."""
+    hq, hkv, d, p = 32, 8, 128, 16
+    lengths = _ragged_lengths(12, 3000, seed=17)
+    clean, poison = _poisoned_case("cpu", dtype=dtype, lengths=lengths, hq=hq, hkv=hkv, d=d, p=p, seed=27)
+    maxp = 8192 if wide else clean[3].shape[1]
+    kind, waves, _, _ = cabi.auto_info(len(lengths), hq, hkv, d, p, maxp, cabi.DTYPE[dtype])
+    say(f"poisoned slots, product path: {DT_NAME[dtype]} max_pages={maxp} kind={kind} waves={waves}")
+    assert kind == 1
+    outs = []
+    for case in (clean, poison):
+        q, k, v, table, lens = case
+        tpad = torch.full((len(lengths), maxp), -1, dtype=torch.int32)
+        tpad[:, :table.shape[1]] = table
+        dev_case = to_dev((q, k, v, tpad, lens), gpu)
+        out = attention_amd.gqa_decode(*dev_case)
+        nbytes = cabi.auto_workspace_bytes(len(lengths), hq, hkv, d, p, maxp, cabi.DTYPE[dtype])
+        ctrl = cabi.auto_control_bytes(len(lengths))
+        ws = torch.full((nbytes,), 0xFF, device=gpu, dtype=torch.uint8)
+        ws[:ctrl] = 0
+        out_c = torch.full_like(dev_case[0], float("nan"))
+        rc = cabi.auto_launch(*dev_case, out_c, scale=1 / math.sqrt(d), workspace=ws)
+        assert rc == 0, cabi.error_string(rc)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_c)
+        outs.append(out)
+    assert torch.isfinite(outs[1]).all()
+    assert torch.equal(outs[0], outs[1])
+    ref, rows = oracle_rows(to_dev(clean, gpu))
+    assert_close(outs[0], ref, DT_NAME[dtype], rows, "clean")
+
+
+def test_poisoned_cfg3_bitwise_product_path(gpu):
+    """cfg3's own lengths (B64, Hq28/Hkv4, up to 8192 tokens, many not a
+    multiple of 16) on a pool with unused blocks, poisoned versus clean
+    through attention_amd.gqa_decode."""
+    cfg = CONFIGS["cfg3"]
+    lengths = cfg.lengths()
+    say("poisoned slots, cfg3 lengths, product path")
+    clean, poison = _poisoned_case("cpu", dtype=cfg.dtype, lengths=lengths, hq=cfg.q_heads, hkv=cfg.kv_heads,
+                                   d=cfg.head_dim, p=cfg.block_size, seed=cfg.seed)
+    out0 = attention_amd.gqa_decode(*to_dev(clean, gpu))
+    out1 = attention_amd.gqa_decode(*to_dev(poison, gpu))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out1).all()
+    assert torch.equal(out0, out1)
 
 
 @pytest.mark.parametrize("flags", [0, cabi.QD_FLAG_FORCE_GENERIC], ids=["auto", "generic"])
