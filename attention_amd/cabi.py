@@ -75,8 +75,6 @@ def lib():
                ctypes.c_void_p])
         L.qd_gqa_decode_auto_workspace_bytes.restype = ctypes.c_size_t
         L.qd_gqa_decode_auto_workspace_bytes.argtypes = [ctypes.c_int] * 7
-        L.qd_gqa_decode_auto_control_bytes.restype = ctypes.c_size_t
-        L.qd_gqa_decode_auto_control_bytes.argtypes = [ctypes.c_int]
         L.qd_gqa_decode_auto.restype = ctypes.c_int
         L.qd_gqa_decode_auto.argtypes = (
             [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
@@ -172,10 +170,6 @@ def auto_workspace_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pag
                                                     max_pages, dtype)
 
 
-def auto_control_bytes(batch):
-    return lib().qd_gqa_decode_auto_control_bytes(batch)
-
-
 def auto_info(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype=2):
     """(kind, waves, splits, chunk_pages); kind 1 = balanced MFMA path, 0 = split path."""
     w, s, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
@@ -187,9 +181,8 @@ def auto_info(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype=2
 def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None, stages=QD_STAGE_ALL):
     """Calls qd_gqa_decode_auto on torch device tensors (no validation).
 
-    ``workspace`` (any dtype, contiguous) must hold auto_workspace_bytes(),
-    with its first auto_control_bytes(batch) bytes zero (a zeroed tensor;
-    every call leaves that region zero)."""
+    ``workspace`` (any dtype, contiguous) must hold auto_workspace_bytes();
+    its contents need no initialization."""
     B, Hq, D = q.shape
     _, P, Hkv, _ = k.shape
     if stream is None:

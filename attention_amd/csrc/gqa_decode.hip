@@ -70,13 +70,8 @@ struct DecodeParams {
   int head_chunks;  // generic kernel: ceil(g / kGenericHeads)
   int64_t num_blocks;
   float sl2;  // scale * log2(e)
-  int* meta;      // stream-K path: per sequence {first segment, segments}
+  int* meta;      // stream-K path: per sequence {first workgroup, workgroups}
   int wg_waves;   // stream-K path: waves per workgroup
-  unsigned* ctrl;  // stream-K path: claim counters (zero between calls)
-  int tail_pct;    // stream-K path: share of each workgroup's range left to claiming
-  int chunk_units;  // stream-K path: minimum claimable chunk, cost units
-  int max_chunks;   // stream-K path: claimable chunks per share at most
-  int nseg;         // stream-K path: segment slots the workspace holds
 };
 
 // Valid tokens of a sequence: lengths are clamped to the table capacity
@@ -369,7 +364,7 @@ struct MfmaWave {
   int wbase;  // first page of the table window held in tblv
   int tblv;   // table entry (wbase + lane)
 
-  __device__ __forceinline__ void init_lane() {
+  __device__ void init_lane() {
     lane = threadIdx.x & 63;  // lane within the wave (workgroups may hold several)
     r16 = lane & 15;
     q4 = lane >> 4;
@@ -378,7 +373,7 @@ struct MfmaWave {
   // Starts item (b, kvh0..) whose run() begins at group g_first.  The page
   // table window of g_first is loaded before the query, so the first K/V
   // loads wait for the table alone; the query is needed only at compute.
-  __device__ __forceinline__ void begin_item(const DecodeParams& p, int b, int kvh0, int valid_tokens, int g_first) {
+  __device__ void begin_item(const DecodeParams& p, int b, int kvh0, int valid_tokens, int g_first) {
     const int g = p.g;
     const bool head_ok = r16 < g;
     trow = p.table + static_cast<int64_t>(b) * p.maxP;
@@ -407,7 +402,7 @@ struct MfmaWave {
   // Issues the K/V loads of group gi (tokens 16*gi .. 16*gi+15 of the item).
   // The group lies inside one page (block_size is a multiple of 16); rows at
   // or past `len` re-read the last valid row and are masked in compute().
-  __device__ __forceinline__ void issue(const DecodeParams& p, Buf& buf, int gi) {
+  __device__ void issue(const DecodeParams& p, Buf& buf, int gi) {
     const int gpp = p.P >> 4;
     const int tg = 16 * gi;
     buf.tg = tg;
@@ -439,7 +434,7 @@ struct MfmaWave {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  __device__ __forceinline__ void compute(const DecodeParams& p, const Buf& buf, char* ktile) {
+  __device__ void compute(const DecodeParams& p, const Buf& buf, char* ktile) {
     const int last = len - 1 - buf.tg;
 #pragma unroll
     for (int j = 0; j < NKV; ++j) {
@@ -503,7 +498,7 @@ struct MfmaWave {
   // flight: the steady-state loop issues unconditionally (static buffer
   // slots, no branches around loads) so the compiler's wait counts cover
   // only the group being consumed.
-  __device__ __forceinline__ void run(const DecodeParams& p, int ga, int gb, char* ktile) {
+  __device__ void run(const DecodeParams& p, int ga, int gb, char* ktile) {
     const int gpp = p.P >> 4;
     for (int g_lo = ga; g_lo < gb;) {
       if (g_lo != ga) {  // the first window came with begin_item
@@ -543,13 +538,13 @@ struct MfmaWave {
 
   // Softmax denominator of this lane's head (lanes of one head hold partial
   // sums over their 4 tokens of every group).
-  __device__ __forceinline__ float total_l(int j) const {
+  __device__ float total_l(int j) const {
     float l = l_run[j] + __shfl_xor(l_run[j], 16);
     return l + __shfl_xor(l, 32);
   }
 
   // out[b, (kvh0+jk)*g + r16, :] = acc / l (zeros when l == 0), one rounding.
-  __device__ __forceinline__ void store_direct(const DecodeParams& p, int b, int kvh0, int jk, float l_tot) {
+  __device__ void store_direct(const DecodeParams& p, int b, int kvh0, int jk, float l_tot) {
     using S = typename Elem<DT>::S;
     if (r16 >= p.g) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -575,7 +570,7 @@ struct MfmaWave {
 
   // Partial {m (natural-log units), l, acc[D]} of kv-head kvh0+jk, this
   // lane's head, at w + head*head_stride (head_stride even).
-  __device__ __forceinline__ void store_partial(const DecodeParams& p, int jk, float* w, int64_t head_stride, float l_tot) {
+  __device__ void store_partial(const DecodeParams& p, int jk, float* w, int64_t head_stride, float l_tot) {
     if (r16 >= p.g) return;
     w += r16 * head_stride;
     if (q4 == 0) {
@@ -759,67 +754,6 @@ __device__ __forceinline__ int64_t seq_cost(int groups) {
   return groups > 0 ? kSkGroupCost * groups + kSkSeqCost : 0;
 }
 
-// Claim queues of the stream-K path: one per XCC, each with one counter per
-// wave index of a workgroup (64 bytes apart), then the workgroups' done
-// count.  They live in the control region at the start of the workspace.
-constexpr int kSkQueues = 8;
-constexpr int kSkQueueStride = 16;  // 32-bit words between counters
-__host__ __device__ constexpr int sk_queue_word(int q, int wave) { return (q * kMaxWgWaves + wave) * kSkQueueStride; }
-constexpr int kSkDoneWord = kSkQueues * kMaxWgWaves * kSkQueueStride;
-constexpr int kSkControlWords = kSkDoneWord + kSkQueueStride;
-
-// XCC (accelerator complex die) this wave runs on: HW_REG_XCC_ID bits
-// [3:0].  Only picks which claim queue a wave tries first.
-__device__ __forceinline__ int xcc_id() {
-  return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (kSkQueues - 1);
-}
-
-// The cost line [0, C) cut into segments.  Share w = [u_w, u_{w+1}) with
-// u_w = floor(w*C/Wu); its first part [u_w, h_w) is the static head of
-// workgroup w, the rest (tail_pct percent of the share, rounded down) is K
-// chunks [h_w + floor(j*T_w/K), h_w + floor((j+1)*T_w/K)) that any wave may
-// claim.  K is the same for every share: the largest count (at most
-// max_chunks) that keeps every chunk of the shortest share at least
-// chunk_units long.  Every segment is at least kSkGroupCost long (heads:
-// because tail_pct <= 20 and shares are >= kSkGroupCost; chunks: because
-// chunk_units >= kSkGroupCost), so any segment that lies between the units
-// of a sequence's first and last group holds at least one of its groups.
-// Segment ids: w*(1+K) for a head, w*(1+K) + 1 + j for chunk j.
-struct SkSegments {
-  int64_t C;
-  int Wu, K, tail_pct;
-
-  __device__ static SkSegments make(int64_t C, int Wu, int tail_pct, int chunk_units, int max_chunks) {
-    SkSegments s{C, Wu, 0, tail_pct};
-    if (C > 0 && tail_pct > 0 && chunk_units > 0) {
-      const int64_t tmin = (C / Wu) * tail_pct / 100;
-      const int64_t k = tmin / chunk_units;
-      s.K = static_cast<int>(k < max_chunks ? k : max_chunks);
-    }
-    return s;
-  }
-  __device__ int64_t share_start(int w) const { return div_nonneg(static_cast<int64_t>(w) * C, Wu); }
-  __device__ int64_t tail_len(int w) const {
-    return K > 0 ? (share_start(w + 1) - share_start(w)) * tail_pct / 100 : 0;
-  }
-  __device__ int64_t head_end(int w) const { return share_start(w + 1) - tail_len(w); }
-  __device__ int64_t chunk_start(int w, int j) const {
-    return head_end(w) + div_nonneg(static_cast<int64_t>(j) * tail_len(w), K);
-  }
-  __device__ int head_seg(int w) const { return w * (1 + K); }
-  __device__ int chunk_seg(int w, int j) const { return w * (1 + K) + 1 + j; }
-  // Chunks in the queue of XCC q: the tails of shares q, q+8, ...
-  __device__ int queue_len(int q) const { return q < Wu ? ((Wu - q + kSkQueues - 1) / kSkQueues) * K : 0; }
-  // Segment holding unit x (0 <= x < C).
-  __device__ int seg_of(int64_t x) const {
-    const int w = static_cast<int>(div_nonneg((x + 1) * Wu - 1, C));
-    const int64_t h = head_end(w);
-    if (x < h) return head_seg(w);
-    const int64_t t = tail_len(w);
-    return chunk_seg(w, static_cast<int>(div_nonneg((x - h + 1) * K - 1, t)));
-  }
-};
-
 // Balanced ("stream-K") layout.  grid: W = p.splits workgroups of
 // p.wg_waves waves; wave j of a workgroup serves kv-heads j*NKV .. j*NKV +
 // NKV-1, then the same plus wg_waves*NKV, ... so that a workgroup reads
@@ -853,26 +787,26 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   __shared__ __align__(16) char ktile[sk_max_waves<D, NKV>()][KTile<D>::kBytes];
 
   // Prologue, one memory round trip for B <= 64*kRegChunks: every lane loads
-  // the lengths of sequences c*64 + lane; the running sums of the costs stay
-  // in registers (32-bit, kept when the total fits) for the sequence
-  // lookups, the lengths until the first lookup.
+  // the lengths of sequences c*64 + lane, and the group counts and the
+  // running sums of the costs stay in registers.
   constexpr int kRegChunks = 4;
   int len_r[kRegChunks];
-  int incl_r[kRegChunks];
-  int64_t carry = 0;
+  int n_r[kRegChunks];
+  int64_t incl_r[kRegChunks];
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
     const int bb = c * 64 + lane;
     len_r[c] = bb < B ? clamp_len(p, p.lens[bb]) : 0;
+    n_r[c] = (len_r[c] + 15) >> 4;
   }
   // Chunks past the batch hold zeros and are not scanned.
+  int64_t carry = 0;
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
-    incl_r[c] = static_cast<int>(carry);
+    incl_r[c] = carry;
     if (c == 0 || c * 64 < B) {
-      const int64_t incl = carry + wave_incl_scan_small(seq_cost((len_r[c] + 15) >> 4), lane);
-      incl_r[c] = static_cast<int>(incl);
-      carry = readlane_i64(incl, 63);
+      incl_r[c] += wave_incl_scan_small(seq_cost(n_r[c]), lane);
+      carry = readlane_i64(incl_r[c], 63);
     }
   }
   for (int c = 64 * kRegChunks; c < B; c += 64) {  // larger batches: re-read
@@ -880,8 +814,6 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
     carry += wave_sum_i64(seq_cost(bb < B ? seq_groups(p, p.lens[bb]) : 0));
   }
   const int64_t C = carry;
-  // Register lookups need the whole batch in registers and 31-bit sums.
-  const bool regs_hold_all = B <= 64 * kRegChunks && C < (int64_t{1} << 31);
 
   // Empty sequences (no workgroup holds them): workgroup b % W writes their
   // zero rows and a meta entry that tells merge_sk_kernel to skip them.
@@ -900,7 +832,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
     const int bb = c * 64 + lane;
-    zero_fill(__ballot(bb < B && len_r[c] == 0 && bb % W == w), c * 64);
+    zero_fill(__ballot(bb < B && n_r[c] == 0 && bb % W == w), c * 64);
   }
   for (int c = 64 * kRegChunks; c < B; c += 64) {
     const int bb = c + lane;
@@ -910,167 +842,95 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   // Workgroups in use (uniform across the grid).
   const int64_t wu_cap = C / kSkGroupCost;
   const int Wu = static_cast<int>(wu_cap < W ? (wu_cap > 0 ? wu_cap : 1) : W);
-  const SkSegments sg = SkSegments::make(C, Wu, p.tail_pct, p.chunk_units, p.max_chunks);
+  if (w >= Wu || C == 0) return;
+  const int64_t c0 = div_nonneg(static_cast<int64_t>(w) * C, Wu);
+  const int64_t c1 = div_nonneg(static_cast<int64_t>(w + 1) * C, Wu);
 
-  // The sequence whose unit range holds unit x (the first whose running cost
-  // end exceeds x) and its first unit cs; B when none.
-  auto find_seq = [&](int64_t x, int& b, int64_t& cs) __attribute__((always_inline)) {
-    b = B;
-    cs = 0;
-    if (regs_hold_all) {
+  // The sequence whose unit range holds c0 (the first whose running cost
+  // end exceeds c0) and its first unit cs; its clamped length comes from the
+  // registers when the prologue holds it.
+  int b = B;
+  int64_t cs = 0;
+  int len_first = -1;
 #pragma unroll
-      for (int c = 0; c < kRegChunks; ++c) {
-        if (b == B && c * 64 < B) {
-          const int bb = c * 64 + lane;
-          const int cnt = __popcll(__ballot(bb < B && incl_r[c] <= x));
-          if (cnt < min(64, B - c * 64)) {
-            b = c * 64 + cnt;
-            const int prev = __builtin_amdgcn_readlane(incl_r[c], cnt > 0 ? cnt - 1 : 0);
-            cs = cnt > 0 ? prev : (c > 0 ? __builtin_amdgcn_readlane(incl_r[c - 1], 63) : 0);
-          }
-        }
+  for (int c = 0; c < kRegChunks; ++c) {
+    if (b == B && c * 64 < B) {
+      const int bb = c * 64 + lane;
+      const int cnt = __popcll(__ballot(bb < B && incl_r[c] <= c0));
+      if (cnt < min(64, B - c * 64)) {
+        b = c * 64 + cnt;
+        cs = readlane_i64(incl_r[c] - seq_cost(n_r[c]), cnt);
+        len_first = __builtin_amdgcn_readlane(len_r[c], cnt);
       }
-      return;
     }
-    int64_t run = 0;
-    for (int c = 0; c < B; c += 64) {
+  }
+  if (b == B) {
+    carry = readlane_i64(incl_r[kRegChunks - 1], 63);
+    for (int c = 64 * kRegChunks; c < B; c += 64) {
       const int bb = c + lane;
       const int64_t n = bb < B ? seq_cost(seq_groups(p, p.lens[bb])) : 0;
-      const int64_t incl = run + wave_incl_scan_small(n, lane);
-      const int cnt = __popcll(__ballot(bb < B && incl <= x));
+      const int64_t incl = carry + wave_incl_scan_small(n, lane);
+      const int cnt = __popcll(__ballot(bb < B && incl <= c0));
       if (cnt < min(64, B - c)) {
         b = c + cnt;
         cs = readlane_i64(incl - n, cnt);
-        return;
+        break;
       }
-      run = readlane_i64(incl, 63);
+      carry = readlane_i64(incl, 63);
     }
-  };
+  }
+  if (b >= B) return;  // unreachable when C is consistent
+
+  // Workgroup whose unit range holds unit x.
+  auto wg_of = [&](int64_t x) { return static_cast<int>(div_nonneg((x + 1) * Wu - 1, C)); };
   // Groups of the current sequence whose unit lies below x.
-  auto groups_below = [&](int64_t x, int64_t x0, int nb) __attribute__((always_inline)) {
+  auto groups_below = [&](int64_t x, int64_t x0, int nb) {
     if (x <= x0) return 0;
     const int64_t i = (x - x0 + kSkGroupCost - 1) / kSkGroupCost;
     return static_cast<int>(i < nb ? i : nb);
   };
 
+
   MfmaWave<D, DT, PF, NKV> wv;
   wv.init_lane();
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
-
-  // Processes segment `seg` = units [c0, c1): every group whose unit it
-  // holds, for this wave's kv-heads.  A sequence held whole is written
-  // directly; a piece of a split sequence goes to slot (seg + b), unique per
-  // (segment, sequence) because the segments of sequence b+1 start at or
-  // after the last segment of b.
-  auto process = [&](int seg, int64_t c0, int64_t c1, int b, int64_t cs, int len_first)
-      __attribute__((always_inline)) {
-    while (b < B) {
-      const int len = len_first >= 0 ? len_first : clamp_len(p, p.lens[b]);
-      len_first = -1;
-      const int nb = (len + 15) >> 4;
-      const int64_t x0 = cs + kSkSeqCost;  // unit of group 0
-      const int i0 = groups_below(c0, x0, nb);
-      const int i1 = groups_below(c1, x0, nb);
-      if (i1 > i0) {
-        const bool whole = i0 == 0 && i1 == nb;
-        float* slot = p.ws + static_cast<int64_t>(seg + b) * slot_floats;
-        for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
-          wv.begin_item(p, b, kvh0, len, i0);
-          wv.run(p, i0, i1, ktile[wid]);
-#pragma unroll
-          for (int j = 0; j < NKV; ++j) {
-            const float l_tot = wv.total_l(j);
-            if (whole)
-              wv.store_direct(p, b, kvh0, j, l_tot);
-            else
-              wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2), D + 2, l_tot);
-          }
-        }
-        // The holder of a sequence's first group records the segments that
-        // span it, for merge_sk_kernel (also for a whole sequence, so that
-        // nothing from an earlier call survives).  Wave 0 of a workgroup
-        // processes every segment it is given for kv-head 0.
-        if (i0 == 0 && wid == 0 && lane == 0) {
-          const int first = sg.seg_of(x0);
-          p.meta[2 * b] = first;
-          p.meta[2 * b + 1] = sg.seg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
-        }
-      }
-      cs += seq_cost(nb);
-      if (cs >= c1) break;
-      do {
-        ++b;
-      } while (b < B && p.lens[b] <= 0);
-    }
-  };
-
-  // The static head of this workgroup's share, then tail chunks claimed one
-  // at a time per wave: first from the queue of this XCC (the tails of the
-  // shares whose workgroups it runs), then from the others.  Chunk
-  // boundaries are fixed by the lengths alone, so the result does not depend
-  // on which wave takes a chunk.
-  int seg = 0;
-  int64_t c0 = 0, c1 = 0;
-  int b = B, len_first = -1;
-  int64_t cs = 0;
-  bool have = C > 0 && w < Wu;
-  if (have) {
-    seg = sg.head_seg(w);
-    c0 = sg.share_start(w);
-    c1 = sg.head_end(w);
-    find_seq(c0, b, cs);
-    // The head's first length from the prologue's registers (saves a round
-    // trip at the start).
-#pragma unroll
-    for (int c = 0; c < kRegChunks; ++c)
-      if (regs_hold_all && b >= c * 64 && b < c * 64 + 64) len_first = __builtin_amdgcn_readlane(len_r[c], b - c * 64);
-  }
-  const int q0 = xcc_id();
-  int qt = (C > 0 && sg.K > 0) ? 0 : kSkQueues;  // queues tried
   while (true) {
-    if (have) process(seg, c0, c1, b, cs, len_first);
-    have = false;
-    while (qt < kSkQueues) {
-      const int q = (q0 + qt) & (kSkQueues - 1);
-      const int qlen = sg.queue_len(q);
-      unsigned idx = ~0u;
-      if (qlen > 0) {
-        if (lane == 0)
-          idx = __hip_atomic_fetch_add(p.ctrl + sk_queue_word(q, wid), 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-        idx = __builtin_amdgcn_readfirstlane(idx);
+    const int len = len_first >= 0 ? len_first : clamp_len(p, p.lens[b]);
+    len_first = -1;
+    const int nb = (len + 15) >> 4;
+    const int64_t x0 = cs + kSkSeqCost;  // unit of group 0
+    const int i0 = groups_below(c0, x0, nb);
+    const int i1 = groups_below(c1, x0, nb);
+    if (i1 > i0) {
+      const bool whole = i0 == 0 && i1 == nb;
+      float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
+      for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
+        wv.begin_item(p, b, kvh0, len, i0);
+        wv.run(p, i0, i1, ktile[wid]);
+#pragma unroll
+        for (int j = 0; j < NKV; ++j) {
+          const float l_tot = wv.total_l(j);
+          if (whole)
+            wv.store_direct(p, b, kvh0, j, l_tot);
+          else
+            wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
+                                             D + 2, l_tot);
+        }
       }
-      if (idx < static_cast<unsigned>(qlen)) {
-        const int share = q + kSkQueues * static_cast<int>(idx / sg.K);
-        const int j = static_cast<int>(idx % sg.K);
-        seg = sg.chunk_seg(share, j);
-        c0 = sg.chunk_start(share, j);
-        c1 = sg.chunk_start(share, j + 1);
-        find_seq(c0, b, cs);
-        len_first = -1;
-        have = true;
-        break;
-      }
-      ++qt;
-    }
-    if (!have) break;
-  }
-  // Every workgroup counts itself out once all its waves are past their last
-  // claim; the last one leaves the claim counters at zero for the next call.
-  // No wave touches them after its workgroup's count (its claims returned
-  // before the barrier), so the reset races with nothing.
-  if (sg.K > 0) {
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const unsigned done =
-          __hip_atomic_fetch_add(p.ctrl + kSkDoneWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (done == gridDim.x - 1) {
-        for (int i = 0; i < kSkQueues * kMaxWgWaves; ++i)
-          __hip_atomic_store(p.ctrl + sk_queue_word(i / kMaxWgWaves, i % kMaxWgWaves), 0u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.ctrl + kSkDoneWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // The workgroup holding a sequence's first group records which
+      // workgroups span it, for merge_sk_kernel (also for a whole sequence,
+      // so that nothing from an earlier call survives).
+      if (i0 == 0 && threadIdx.x == 0) {
+        const int first = wg_of(x0);
+        p.meta[2 * b] = first;
+        p.meta[2 * b + 1] = wg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
       }
     }
+    cs += seq_cost(nb);
+    if (cs >= c1) break;
+    do {
+      if (++b >= B) return;  // unreachable when C is consistent
+    } while (p.lens[b] <= 0);
   }
 }
 
@@ -1091,7 +951,7 @@ __global__ __launch_bounds__(64) void merge_sk_kernel(DecodeParams p) {
   const int first = p.meta[2 * b];
   const int nwg = p.meta[2 * b + 1];
   if (nwg <= 1) return;  // written directly, or an empty sequence (zero-filled)
-  if (first < 0 || first + nwg > p.nseg) return;  // spans are always inside the segment slots
+  if (first < 0 || first + nwg > p.splits) return;  // spans are always inside [0, W)
   const int j4 = (threadIdx.x & 63) >> 4;
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
   const float* slots = p.ws + static_cast<int64_t>(first + b) * slot_floats;
@@ -1419,30 +1279,6 @@ int sk_wg_waves(int kv_heads, int nkv, int head_dim) {
   return 1;
 }
 
-// Bytes of the automatic path's control region: the stream-K path's claim
-// counters.  It must be zero when a call starts; every call leaves it zero.
-size_t control_bytes(int batch) {
-  (void)batch;
-  return (static_cast<size_t>(kSkControlWords) * sizeof(unsigned) + 255) / 256 * 256;
-}
-
-#ifndef QD_SK_TAIL_PCT
-#define QD_SK_TAIL_PCT 0
-#endif
-#ifndef QD_SK_CHUNK_UNITS
-#define QD_SK_CHUNK_UNITS 8
-#endif
-#ifndef QD_SK_MAX_CHUNKS
-#define QD_SK_MAX_CHUNKS 4
-#endif
-// Stream-K claiming: the last kSkTailPct percent of each workgroup's share
-// is cut into at most kSkMaxChunks chunks of at least kSkChunkUnits cost
-// units (two 16-token groups) that waves claim at run time, so the
-// workgroups of faster XCCs take over work from slower ones.
-constexpr int kSkTailPct = QD_SK_TAIL_PCT < 20 ? QD_SK_TAIL_PCT : 20;
-constexpr int kSkChunkUnits = QD_SK_CHUNK_UNITS > 4 ? QD_SK_CHUNK_UNITS : 4;
-constexpr int kSkMaxChunks = QD_SK_MAX_CHUNKS;
-
 struct AutoPlan {
   bool stream_k;
   int wgs;          // stream-K grid (workgroups)
@@ -1450,18 +1286,16 @@ struct AutoPlan {
   int kv_per_wave;  // stream-K kv-heads per wave
   int splits;       // explicit-split path
   int chunk_pages;
-  size_t ws_bytes;  // control region + scratch
+  size_t ws_bytes;  // scratch bytes
   size_t meta_offset;  // stream-K: byte offset of the meta table in the scratch
-  int nseg;            // stream-K: segment slots (workgroups x (1 + claimable chunks))
 };
 
 // Chooses the automatic path from static shapes only.  `aligned` says
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
               int dtype, bool aligned, AutoPlan* ap) {
-  *ap = AutoPlan{false, 0, 1, 1, 1, 0, 0, 0, 0};
+  *ap = AutoPlan{false, 0, 1, 1, 1, 0, 0, 0};
   if (batch <= 0) return QD_OK;
-  const size_t ctrl = control_bytes(batch);
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
     int nkv = 1;
@@ -1482,9 +1316,8 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     ap->wgs = static_cast<int>(w);
     ap->wg_waves = nw;
     ap->kv_per_wave = nkv;
-    ap->nseg = static_cast<int>(w) * (1 + kSkMaxChunks);
-    ap->meta_offset = static_cast<size_t>(ap->nseg + batch) * q_heads * (head_dim + 2) * sizeof(float);
-    ap->ws_bytes = ctrl + ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
+    ap->meta_offset = static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
+    ap->ws_bytes = ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
     return QD_OK;
   }
   int s = 1, c = 0;
@@ -1493,7 +1326,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
   if (st != QD_OK) return st;
   ap->splits = s;
   ap->chunk_pages = c;
-  ap->ws_bytes = ctrl + qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, s);
+  ap->ws_bytes = qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, s);
   return QD_OK;
 }
 
@@ -1541,11 +1374,6 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.sl2 = scale * kLog2e;
   prm.meta = nullptr;
   prm.wg_waves = 1;
-  prm.ctrl = nullptr;
-  prm.tail_pct = 0;
-  prm.chunk_units = kSkChunkUnits;
-  prm.max_chunks = 0;
-  prm.nseg = 0;
   return prm;
 }
 
@@ -1724,8 +1552,6 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
   return launch_error();
 }
 
-size_t qd_gqa_decode_auto_control_bytes(int batch) { return batch > 0 ? control_bytes(batch) : 0; }
-
 size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
                                           int block_size, int max_pages, int dtype) {
   if (check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, 1, dtype, 1.f) !=
@@ -1759,12 +1585,12 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   if (st != QD_OK) return st;
   if (!workspace || workspace_bytes < ap.ws_bytes || !aligned16(workspace))
     return fail(QD_ERR_INVALID_VALUE, "workspace smaller than qd_gqa_decode_auto_workspace_bytes()");
-  char* scratch = static_cast<char*>(workspace) + control_bytes(batch);
+  char* scratch = static_cast<char*>(workspace);
   if (!ap.stream_k) {
     if (stages != QD_STAGE_ALL)
       return fail(QD_ERR_INVALID_VALUE, "stages apply to the balanced MFMA path only");
     return qd_gqa_decode_launch(q, k_cache, v_cache, block_table, context_lens, out,
-                                reinterpret_cast<float*>(scratch), ap.ws_bytes - control_bytes(batch),
+                                reinterpret_cast<float*>(scratch), ap.ws_bytes,
                                 batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
                                 dtype, scale, ap.splits, ap.chunk_pages, 0, stream);
   }
@@ -1773,10 +1599,6 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
                                  ap.wgs, 0);
   prm.meta = reinterpret_cast<int*>(scratch + ap.meta_offset);
   prm.wg_waves = ap.wg_waves;
-  prm.ctrl = static_cast<unsigned*>(workspace);
-  prm.tail_pct = kSkTailPct;
-  prm.max_chunks = kSkMaxChunks;
-  prm.nseg = ap.nseg;
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (stages & QD_STAGE_DECODE)

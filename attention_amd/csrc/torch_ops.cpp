@@ -47,28 +47,6 @@ qd_tensor_desc describe(const at::Tensor& t) {
   return d;
 }
 
-// The automatic path's workspace, one per (device, stream), kept for the
-// life of the process like a BLAS handle's workspace.  It is zero-filled on
-// the stream when created or grown (the library's reserved control region
-// must be zero on entry and is left zero), so only the first call on a stream, or
-// one that needs a larger workspace, pays for an allocation and a fill.
-// Calls on one stream run in order and share it; calls on different
-// streams never share one.
-at::Tensor stream_workspace(const at::Tensor& like, hipStream_t stream, size_t bytes) {
-  static std::mutex mu;
-  // Never destroyed: tensors must not be freed after the allocator is gone
-  // at process exit.
-  static auto* cache = new std::map<std::pair<int, hipStream_t>, at::Tensor>();
-  const std::pair<int, hipStream_t> key{like.get_device(), stream};
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache->find(key);
-  if (it != cache->end() && static_cast<size_t>(it->second.numel()) >= bytes) return it->second;
-  at::Tensor ws = at::zeros({static_cast<int64_t>(std::max<size_t>(bytes, 256))},
-                            like.options().dtype(at::kByte));
-  (*cache)[key] = ws;
-  return ws;
-}
-
 // Explicit-split path (gqa_decode.cu:96-183 with splits >= 1).
 at::Tensor decode_impl(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                        const at::Tensor& table, const at::Tensor& lens, double scale,
@@ -115,8 +93,10 @@ at::Tensor decode_impl(const at::Tensor& q, const at::Tensor& k, const at::Tenso
 
 // The reference's gqa_decode (gqa_decode.cu:186-188): same validation and
 // output, body replaced by the library's automatic path (balanced MFMA
-// partition or planned splits), with a per-call workspace from the caching
-// allocator.
+// partition or planned splits).  The workspace is allocated per call from
+// the caching allocator, as the reference allocates its split partials
+// (gqa_decode.cu:154): it needs no initialization, so under stream capture
+// it comes from the graph's private pool like any other tensor of the call.
 at::Tensor gqa_decode_hip(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                           const at::Tensor& table, const at::Tensor& lens, double scale) {
   const qd_tensor_desc dq = describe(q), dk = describe(k), dv = describe(v), dt = describe(table),
@@ -135,7 +115,7 @@ at::Tensor gqa_decode_hip(const at::Tensor& q, const at::Tensor& k, const at::Te
   const int maxP = static_cast<int>(table.size(1));
   const size_t ws_bytes = qd_gqa_decode_auto_workspace_bytes(B, Hq, Hkv, D, P, maxP, dq.dtype);
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  const at::Tensor ws = stream_workspace(q, stream, ws_bytes);
+  const at::Tensor ws = at::empty({static_cast<int64_t>(std::max<size_t>(ws_bytes, 16))}, q.options().dtype(at::kByte));
   st = qd_gqa_decode_auto(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr<int32_t>(),
                           lens.data_ptr<int32_t>(), out.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv, D,
                           P, maxP, k.size(0), dq.dtype, static_cast<float>(scale), stream);

@@ -15,7 +15,7 @@
  *   qd_gqa_decode_workspace_bytes     csrc/cuda/dense/gqa_decode.cu:152-154
  *   qd_gqa_decode_launch              csrc/cuda/dense/gqa_decode.cu:140-183,
  *                                     kernels :18-87 (explicit splits)
- *   qd_gqa_decode_auto(+_stages, _workspace_bytes, _control_bytes, _info)
+ *   qd_gqa_decode_auto(+_stages, _workspace_bytes, _info)
  *                                     csrc/cuda/dense/gqa_decode.cu:186-188
  *                                     and attention/core.py:80-96
  *
@@ -148,23 +148,16 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  *     which a second kernel on the same stream folds (log-sum-exp);
  *   - otherwise: the split layout of qd_gqa_decode_launch with the plan of
  *     qd_gqa_decode_plan.
- * The workspace is device memory, 16-byte aligned, of at least
- * qd_gqa_decode_auto_workspace_bytes() bytes.  Its first
- * qd_gqa_decode_auto_control_bytes(batch) bytes are a reserved control
- * region (per-sequence counters for an in-kernel merge; the current kernels
- * do not write it): it must be zero when a call starts, and every call
- * leaves it zero (zero a new workspace once, then reuse it).  The rest is
- * scratch.  Calls that may
- * run concurrently (different streams) need different workspaces.
- * Workspace size and partition depend on the current device (hipGetDevice),
- * so query and launch with the same device current.  Does not allocate or
- * synchronize. */
+ * The workspace is device scratch, 16-byte aligned, of at least
+ * qd_gqa_decode_auto_workspace_bytes() bytes.  Its contents need no
+ * initialization: every call writes what it reads (the partial slots and,
+ * for every sequence, its span entry).  Calls that may run concurrently
+ * (different streams, or replays of captured graphs on different streams)
+ * need different workspaces.  Workspace size and partition depend on the
+ * current device (hipGetDevice), so query and launch with the same device
+ * current.  Does not allocate or synchronize. */
 size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
                                           int block_size, int max_pages, int dtype);
-
-/* Bytes at the start of the automatic path's workspace that must be zero
- * between calls (0 when batch <= 0). */
-size_t qd_gqa_decode_auto_control_bytes(int batch);
 
 int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
                        const int32_t* block_table, const int32_t* context_lens, void* out,

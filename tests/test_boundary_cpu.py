@@ -233,15 +233,6 @@ def test_launch_batch_zero_is_a_no_op():
 # Automatic path (qd_gqa_decode_auto*): plan, workspace layout, argument errors
 # ----------------------------------------------------------------------------
 
-def test_auto_control_bytes():
-    # The claim counters of the stream-K path: 8 queues x 8 wave counters 64
-    # bytes apart, then the done count, rounded up to 256 bytes; independent
-    # of the batch.
-    assert cabi.auto_control_bytes(0) == 0
-    for batch in (1, 64, 65, 4096):
-        assert cabi.auto_control_bytes(batch) == 4352
-
-
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_auto_plan_for_configs(name):
     cfg = CONFIGS[name]
@@ -254,8 +245,8 @@ def test_auto_plan_for_configs(name):
     nbytes = cabi.auto_workspace_bytes(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
                                        cfg.block_size, max_pages, dt)
     wgs = waves // min(cfg.kv_heads, 8)
-    slots = (wgs + cfg.batch) * cfg.q_heads * (cfg.head_dim + 2) * 4   # at least one segment per workgroup
-    assert nbytes >= cabi.auto_control_bytes(cfg.batch) + slots + 8 * cfg.batch
+    slots = (wgs + cfg.batch) * cfg.q_heads * (cfg.head_dim + 2) * 4
+    assert nbytes >= slots + 8 * cfg.batch
 
 
 def test_auto_plan_falls_back_to_splits():
