@@ -79,6 +79,11 @@ def lib():
         L.qd_gqa_decode_auto.argtypes = (
             [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
             + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p])
+        L.qd_gqa_decode_noalloc_scratch_bytes.restype = ctypes.c_size_t
+        L.qd_gqa_decode_noalloc_scratch_bytes.argtypes = []
+        L.qd_gqa_decode_auto_noalloc.restype = ctypes.c_int
+        L.qd_gqa_decode_auto_noalloc.argtypes = (
+            [ctypes.c_void_p] * 6 + [ctypes.c_int] * 6 + [ctypes.c_int64] + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p])
         L.qd_gqa_decode_auto_stages.restype = ctypes.c_int
         L.qd_gqa_decode_auto_stages.argtypes = (
             [ctypes.c_void_p] * 7 + [ctypes.c_size_t] + [ctypes.c_int] * 6 + [ctypes.c_int64]
@@ -193,6 +198,18 @@ def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None
         q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), lens.data_ptr(), out.data_ptr(),
         ws_ptr, ws_bytes, B, Hq, Hkv, D, P, table.shape[1], k.shape[0], DTYPE[q.dtype], float(scale),
         stages, stream)
+
+
+def auto_noalloc_launch(q, k, v, table, lens, out, *, scale, stream=None):
+    """Calls qd_gqa_decode_auto_noalloc (the library's own scratch, no
+    workspace argument) on torch device tensors (no validation)."""
+    B, Hq, D = q.shape
+    _, P, Hkv, _ = k.shape
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else 0
+    return lib().qd_gqa_decode_auto_noalloc(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), lens.data_ptr(), out.data_ptr(),
+        B, Hq, Hkv, D, P, table.shape[1], k.shape[0], DTYPE[q.dtype], float(scale), stream)
 
 
 def validate_kv_append(key, value, kc, vc, table, pos):

@@ -1384,6 +1384,41 @@ int launch_error() {
   return QD_OK;
 }
 
+// Scratch of the no-allocation entry point: one array per GPU the library
+// runs on, held until the process ends.  In host code `scratch` names a
+// host-side stand-in, not device memory: the device address comes from
+// hipGetSymbolAddress, once per device (no_alloc_scratch below).
+constexpr size_t kNoAllocScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on the current device (looked up on the first
+// call on that device, with it current), or null with *status set.
+void* no_alloc_scratch(int* status) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *status = fail(e != hipSuccess ? static_cast<int>(e) : QD_ERR_INVALID_VALUE,
+                   "no current device for the no-allocation scratch");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      *status = fail(e != hipSuccess ? static_cast<int>(e) : QD_ERR_INVALID_VALUE,
+                     std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev] = ptr;
+  }
+  *status = QD_OK;
+  return addr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -1620,6 +1655,29 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
   return qd_gqa_decode_auto_stages(q, k_cache, v_cache, block_table, context_lens, out, workspace,
                                    workspace_bytes, batch, q_heads, kv_heads, head_dim, block_size,
                                    max_pages, num_blocks, dtype, scale, QD_STAGE_ALL, stream);
+}
+
+size_t qd_gqa_decode_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int qd_gqa_decode_auto_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                               const int32_t* block_table, const int32_t* context_lens, void* out, int batch,
+                               int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
+                               int64_t num_blocks, int dtype, float scale, void* stream) {
+  int st = check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, dtype,
+                               scale);
+  if (st != QD_OK) return st;
+  if (batch == 0) return QD_OK;
+  const size_t need =
+      qd_gqa_decode_auto_workspace_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype);
+  if (need > kNoAllocScratchBytes)
+    return fail(QD_ERR_INVALID_VALUE, "shapes need " + std::to_string(need) +
+                                          " bytes of scratch, more than the no-allocation scratch holds (" +
+                                          std::to_string(kNoAllocScratchBytes) + ")");
+  void* ws = no_alloc_scratch(&st);
+  if (!ws) return st;
+  return qd_gqa_decode_auto_stages(q, k_cache, v_cache, block_table, context_lens, out, ws, kNoAllocScratchBytes,
+                                   batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, dtype,
+                                   scale, QD_STAGE_ALL, stream);
 }
 
 int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, int block_size,

@@ -178,6 +178,24 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
                               int kv_heads, int head_dim, int block_size, int max_pages,
                               int64_t num_blocks, int dtype, float scale, int stages, void* stream);
 
+/* ---- Automatic path without allocation ------------------------------
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same as qd_gqa_decode_auto, but its scratch is a
+ * file-scope device array of qd_gqa_decode_noalloc_scratch_bytes() bytes
+ * (16 MiB) per GPU, held until the process ends; shapes whose
+ * qd_gqa_decode_auto_workspace_bytes() exceed it are rejected with
+ * QD_ERR_INVALID_VALUE before anything is enqueued.  Nothing is allocated
+ * (the array's address is looked up once per device).  Every call on a GPU
+ * uses that GPU's one array: calls that may overlap on one GPU (different
+ * streams, host threads) race and must be serialized by the caller. */
+size_t qd_gqa_decode_noalloc_scratch_bytes(void);
+
+int qd_gqa_decode_auto_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                               const int32_t* block_table, const int32_t* context_lens, void* out, int batch,
+                               int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
+                               int64_t num_blocks, int dtype, float scale, void* stream);
+
 /* Describes the automatic path's choice (assuming aligned pointers):
  * returns 1 for the balanced MFMA path (*waves = its total wave count), 0 for
  * the split path (*splits, *chunk_pages), -1 for invalid shapes.  Any
