@@ -21,6 +21,7 @@ DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.int32: 3, 
 QD_FLAG_FORCE_GENERIC = 1
 QD_FLAG_MLA_STAGED = 2
 QD_STAGE_DECODE, QD_STAGE_MERGE, QD_STAGE_ALL = 1, 2, 3
+QD_STAGE_VALU = 4   # measurement option: VALU math in the balanced decode kernel
 
 
 class TensorDesc(ctypes.Structure):

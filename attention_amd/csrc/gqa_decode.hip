@@ -50,6 +50,7 @@
 
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "qd_attention.h"
 #include "qd_device.h"
@@ -587,6 +588,225 @@ struct MfmaWave {
   }
 };
 
+// VALU compute of the same per-wave pipeline, for comparison with the MFMA
+// one (head_dim 128, one kv-head per wave, at most GV heads per group).
+// Same loads, table windows and partition as MfmaWave; only the math
+// differs.  Lane l, a = l % 16, r = l / 16:
+//   K  from the coalesced load: rows 4c + r (c = 0..3), elements 8a .. 8a+7
+//   Q  the same 8 elements of every head, packed 16-bit pairs
+//   S  4 dot2 per (row, head), then a sum over the 16 lanes of the row (DPP):
+//      every lane of row r holds S[4c + r][h] for c = 0..3
+//   P  written to LDS as P[token][head], read back as P[4*q4 + i][h]
+//   V  rows 4*q4 + i (i = 0..3), elements 8a .. 8a+7: fp32 FMAs into
+//      acc[h][e], a partial over the lane's 4 tokens, summed over q4 at the
+//      end of the item.
+// The softmax state is the same (exact running max, base 2, scale folded in).
+template <int D, int DT, int PF, int GV>
+struct ValuWave : MfmaWave<D, DT, PF, 1> {
+  using Base = MfmaWave<D, DT, PF, 1>;
+  using Buf = typename Base::Buf;
+  using Ops = MfmaOps<DT>;
+  static_assert(D == 128, "the VALU comparison kernel serves head_dim 128");
+  uint32_t qk[GV][4];
+  float vm[GV], vl[GV];
+  float vacc[GV][8];
+
+  __device__ __forceinline__ static float dot2(uint32_t x, uint32_t y, float c) {
+    if constexpr (DT == QD_DTYPE_BF16)
+      return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), __builtin_bit_cast(bf16x2, y), c, false);
+    else
+      return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), __builtin_bit_cast(f16x2, y), c, false);
+  }
+  __device__ __forceinline__ static void unpack2(uint32_t w, float& lo, float& hi) {
+    if constexpr (DT == QD_DTYPE_BF16) {
+      lo = __uint_as_float(w << 16);
+      hi = __uint_as_float(w & 0xFFFF0000u);
+    } else {
+      const f32x2 v = __builtin_convertvector(__builtin_bit_cast(f16x2, w), f32x2);
+      lo = v[0];
+      hi = v[1];
+    }
+  }
+
+  __device__ __forceinline__ void begin_item(const DecodeParams& p, int b, int kvh, int valid_tokens, int g_first) {
+    const int a = this->r16;
+    this->trow = p.table + static_cast<int64_t>(b) * p.maxP;
+    this->wbase = g_first / (p.P >> 4);
+    this->tblv = (this->lane < p.maxP - this->wbase) ? this->trow[this->wbase + this->lane] : 0;
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      const bool ok = h < p.g;
+      const char* qp = static_cast<const char*>(p.q) +
+                       (static_cast<int64_t>(b) * p.Hq + kvh * p.g + (ok ? h : 0)) * D * 2 + 16 * a;
+      const u32x4 x = *reinterpret_cast<const u32x4*>(qp);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) qk[h][w] = ok ? x[w] : 0u;
+      vm[h] = -INFINITY;
+      vl[h] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vacc[h][e] = 0.f;
+    }
+    this->kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh) * D * 2;
+    this->vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh) * D * 2;
+    this->len = valid_tokens;
+  }
+
+  // ptile: this wave's LDS area (KTile<D>::kBytes >= 16 x 16 floats).
+  __device__ __forceinline__ void compute(const DecodeParams& p, const Buf& buf, char* ptile) {
+    const int a = this->r16, r = this->q4;
+    const int last = this->len - 1 - buf.tg;
+    float s[4][GV];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 kv = buf.k[0][c];
+#pragma unroll
+      for (int h = 0; h < GV; ++h) {
+        float d = dot2(kv[0], qk[h][0], 0.f);
+        d = dot2(kv[1], qk[h][1], d);
+        d = dot2(kv[2], qk[h][2], d);
+        s[c][h] = row16_sum(dot2(kv[3], qk[h][3], d));
+      }
+    }
+    float* P = reinterpret_cast<float*>(ptile);
+    bool rescale = false;
+    float alpha[GV];
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[c][h] = (4 * c + r <= last) ? s[c][h] * p.sl2 : -INFINITY;
+        mx = fmaxf(mx, s[c][h]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(vm[h], mx);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      alpha[h] = fast_exp2(vm[h] - mref);
+      rescale |= alpha[h] != 1.f;
+      float lsum = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[c][h] = fast_exp2(s[c][h] - mref);
+        lsum += s[c][h];
+      }
+      vl[h] = fmaf(vl[h], alpha[h], lsum);
+      vm[h] = mn;
+    }
+    // P[token][head]: lane a < GV of row r writes its head's 4 weights.
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float w = 0.f;
+#pragma unroll
+      for (int h = 0; h < GV; ++h) w = (a == h) ? s[c][h] : w;
+      if (a < GV) P[(4 * c + r) * 16 + a] = w;
+    }
+    if (__builtin_amdgcn_read_exec() & __ballot(rescale)) {
+#pragma unroll
+      for (int h = 0; h < GV; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vacc[h][e] *= alpha[h];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) unpack2(buf.v[0][i].w[w], v[2 * w], v[2 * w + 1]);
+      const float* prow = P + (4 * r + i) * 16;
+#pragma unroll
+      for (int h = 0; h < GV; ++h) {
+        const float ph = prow[h];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vacc[h][e] = fmaf(ph, v[e], vacc[h][e]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Same structure as MfmaWave::run, with this compute.
+  __device__ __forceinline__ void run(const DecodeParams& p, int ga, int gb, char* ptile) {
+    const int gpp = p.P >> 4;
+    for (int g_lo = ga; g_lo < gb;) {
+      if (g_lo != ga) {
+        this->wbase = g_lo / gpp;
+        this->tblv = (this->lane < p.maxP - this->wbase) ? this->trow[this->wbase + this->lane] : 0;
+      }
+      const int g_hi = min(gb, (this->wbase + 64) * gpp);
+      const int n = g_hi - g_lo;
+      Buf buf[PF];
+      int i = 0;
+      if (n >= 2 * PF - 1) {
+#pragma unroll
+        for (int u = 0; u < PF - 1; ++u) this->issue(p, buf[u], g_lo + u);
+        for (; i + 2 * PF - 2 < n; i += PF) {
+#pragma unroll
+          for (int u = 0; u < PF; ++u) {
+            this->issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
+            compute(p, buf[u], ptile);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < PF - 1; ++u)
+          if (u < n) this->issue(p, buf[u], g_lo + u);
+      }
+      for (; i < n; i += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+          if (i + u + PF - 1 < n) this->issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
+          if (i + u < n) compute(p, buf[u], ptile);
+        }
+      }
+      g_lo = g_hi;
+    }
+  }
+
+  // Sums the lane partials over the four token rows (q4) and, for head h,
+  // returns the softmax denominator; acc becomes the full output slice.
+  __device__ __forceinline__ void finish_item() {
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      vl[h] += __shfl_xor(vl[h], 16);
+      vl[h] += __shfl_xor(vl[h], 32);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vacc[h][e] += __shfl_xor(vacc[h][e], 16);
+        vacc[h][e] += __shfl_xor(vacc[h][e], 32);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store_direct(const DecodeParams& p, int b, int kvh) {
+    using S = typename Elem<DT>::S;
+    if (this->q4 != 0) return;
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      if (h >= p.g) break;
+      const float inv = vl[h] > 0.f ? 1.f / vl[h] : 0.f;
+      uint32_t wv[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        wv[e / 2] = Ops::pack2(vl[h] > 0.f ? vacc[h][e] * inv : 0.f, vl[h] > 0.f ? vacc[h][e + 1] * inv : 0.f);
+      S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + kvh * p.g + h) * D + 8 * this->r16;
+      *reinterpret_cast<u32x4*>(o) = u32x4{wv[0], wv[1], wv[2], wv[3]};
+    }
+  }
+
+  // Partial rows {m (natural log), l, acc[D]} of the kv-head's heads, head h at w + h*(D+2).
+  __device__ __forceinline__ void store_partial(const DecodeParams& p, float* w) {
+    if (this->q4 != 0) return;
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      if (h >= p.g) break;
+      float* row = w + static_cast<int64_t>(h) * (D + 2);
+      if (this->r16 == 0) *reinterpret_cast<f32x2*>(row) = f32x2{vm[h] * kLn2, vl[h]};
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        *reinterpret_cast<f32x2*>(row + 2 + 8 * this->r16 + e) = f32x2{vacc[h][e], vacc[h][e + 1]};
+    }
+  }
+};
+
 // Explicit split layout.  grid: (splits, Hkv, B), block 64 (one wave per
 // (sequence, kv-head, split)).  Split z of a sequence covers whole pages
 // (chunk_info); a sequence with a single non-empty split is written
@@ -735,8 +955,24 @@ constexpr int kMaxWgWaves = 8;
 // Waves per stream-K workgroup at most: 8 serving one kv-head each, or 4
 // (one per SIMD, so each may use 512 registers) serving two each or with
 // head_dim 256.
-template <int D, int NKV>
+#ifndef QD_VALU_WAVES
+#define QD_VALU_WAVES 8
+#endif
+#ifndef QD_VALU_PF
+#define QD_VALU_PF 1
+#endif
+// The VALU comparison variant holds more state per wave (scores for every
+// head, fp32 output slices): QD_VALU_WAVES waves per workgroup at most and
+// QD_VALU_PF groups in flight.  Measured on cfg2/cfg5/cfg3 and a group-8
+// shape, 8 waves with one group in flight was its fastest form (4 waves with
+// 2 or 3 groups, one wave per SIMD and 512 registers, were 9-32% slower; 8
+// waves with 2 groups spill).
+constexpr int kValuMaxWaves = QD_VALU_WAVES;
+constexpr int kValuPrefetch = QD_VALU_PF;
+
+template <int D, int NKV, int GV = 0>
 constexpr int sk_max_waves() {
+  if (GV > 0) return kValuMaxWaves;
   return (NKV == 1 && D <= 128) ? kMaxWgWaves : kMaxWgWaves / 2;
 }
 
@@ -775,8 +1011,8 @@ __device__ __forceinline__ int64_t seq_cost(int groups) {
 // sequence b+1 start at or after the last one of b, so W + B slots
 // suffice).  merge_sk_kernel combines the slots of every split sequence.
 // Rows of empty sequences are zero-filled by workgroup b % W.
-template <int D, int DT, int PF, int NKV>
-__global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_kernel(DecodeParams p) {
+template <int D, int DT, int PF, int NKV, int GV = 0>
+__global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV>())) void decode_mfma_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -784,7 +1020,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   const int w = blockIdx.x;
   const int W = p.splits;
   const int B = p.B;
-  __shared__ __align__(16) char ktile[sk_max_waves<D, NKV>()][KTile<D>::kBytes];
+  __shared__ __align__(16) char ktile[sk_max_waves<D, NKV, GV>()][KTile<D>::kBytes];
 
   // Prologue, one memory round trip for B <= 64*kRegChunks: every lane loads
   // the lengths of sequences c*64 + lane, and the group counts and the
@@ -891,7 +1127,9 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
   };
 
 
-  MfmaWave<D, DT, PF, NKV> wv;
+  // GV > 0: the VALU comparison variant (ValuWave, GV heads per group).
+  using Wave = std::conditional_t<GV == 0, MfmaWave<D, DT, PF, NKV>, ValuWave<D, DT, PF, (GV > 0 ? GV : 4)>>;
+  Wave wv;
   wv.init_lane();
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
   while (true) {
@@ -907,14 +1145,22 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV>())) void decode_mfma_sk_
       for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
         wv.begin_item(p, b, kvh0, len, i0);
         wv.run(p, i0, i1, ktile[wid]);
+        if constexpr (GV == 0) {
 #pragma unroll
-        for (int j = 0; j < NKV; ++j) {
-          const float l_tot = wv.total_l(j);
+          for (int j = 0; j < NKV; ++j) {
+            const float l_tot = wv.total_l(j);
+            if (whole)
+              wv.store_direct(p, b, kvh0, j, l_tot);
+            else
+              wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
+                                               D + 2, l_tot);
+          }
+        } else {
+          wv.finish_item();
           if (whole)
-            wv.store_direct(p, b, kvh0, j, l_tot);
+            wv.store_direct(p, b, kvh0);
           else
-            wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
-                                             D + 2, l_tot);
+            wv.store_partial(p, slot + static_cast<int64_t>(kvh0) * p.g * (D + 2));
         }
       }
       // The workgroup holding a sequence's first group records which
@@ -1174,6 +1420,21 @@ KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv) {
   return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D, nkv) : pick_mfma_sk<QD_DTYPE_BF16>(D, nkv);
 }
 
+// The VALU comparison variant of the balanced kernel: head_dim 128, one
+// kv-head per wave, group size <= 8.
+bool valu_sk_applies(int q_heads, int kv_heads, int head_dim, int dtype) {
+  return head_dim == 128 && (dtype == QD_DTYPE_F16 || dtype == QD_DTYPE_BF16) && kv_heads > 0 &&
+         q_heads % kv_heads == 0 && q_heads / kv_heads <= 8;
+}
+
+KernelFn pick_valu_sk_dt(int dtype, int g) {
+  if (dtype == QD_DTYPE_F16)
+    return g <= 4 ? decode_mfma_sk_kernel<128, QD_DTYPE_F16, kValuPrefetch, 1, 4>
+                  : decode_mfma_sk_kernel<128, QD_DTYPE_F16, kValuPrefetch, 1, 8>;
+  return g <= 4 ? decode_mfma_sk_kernel<128, QD_DTYPE_BF16, kValuPrefetch, 1, 4>
+                : decode_mfma_sk_kernel<128, QD_DTYPE_BF16, kValuPrefetch, 1, 8>;
+}
+
 template <int DT, int KB, int RG>
 KernelFn pick_merge_sk(int D) {
   switch (D) {
@@ -1272,9 +1533,10 @@ bool sk_dual_applies(int batch, int kv_heads, int head_dim, int block_size, int 
 // Waves per stream-K workgroup: the largest divisor of kv_heads / nkv that
 // fits the kernel's bound, so every wave serves the same number of
 // kv-heads.
-int sk_wg_waves(int kv_heads, int nkv, int head_dim) {
+int sk_wg_waves(int kv_heads, int nkv, int head_dim, bool valu = false) {
   const int units = kv_heads / nkv;
-  for (int n = (nkv == 1 && head_dim <= 128) ? kMaxWgWaves : kMaxWgWaves / 2; n > 1; --n)
+  const int cap = valu ? kValuMaxWaves : (nkv == 1 && head_dim <= 128) ? kMaxWgWaves : kMaxWgWaves / 2;
+  for (int n = cap; n > 1; --n)
     if (units % n == 0) return n;
   return 1;
 }
@@ -1293,15 +1555,17 @@ struct AutoPlan {
 // Chooses the automatic path from static shapes only.  `aligned` says
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
-              int dtype, bool aligned, AutoPlan* ap) {
+              int dtype, bool aligned, AutoPlan* ap, bool valu = false) {
   *ap = AutoPlan{false, 0, 1, 1, 1, 0, 0, 0};
   if (batch <= 0) return QD_OK;
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
     int nkv = 1;
-    int nw = sk_wg_waves(kv_heads, nkv, head_dim);
-    int resident = resident_blocks(pick_mfma_sk_dt(dtype, head_dim, nkv), 64 * nw);
-    if (sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
+    int nw = sk_wg_waves(kv_heads, nkv, head_dim, valu);
+    int resident = resident_blocks(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads)
+                                        : pick_mfma_sk_dt(dtype, head_dim, nkv),
+                                   64 * nw);
+    if (!valu && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
       nkv = 2;
       nw = sk_wg_waves(kv_heads, nkv, head_dim);
       resident = resident_blocks(pick_mfma_sk_dt(dtype, head_dim, nkv), 64 * nw);
@@ -1606,6 +1870,8 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
                               void* workspace, size_t workspace_bytes, int batch, int q_heads,
                               int kv_heads, int head_dim, int block_size, int max_pages,
                               int64_t num_blocks, int dtype, float scale, int stages, void* stream) {
+  const bool valu = (stages & QD_STAGE_VALU) != 0;
+  stages &= ~QD_STAGE_VALU;
   if ((stages & ~QD_STAGE_ALL) != 0 || stages == 0)
     return fail(QD_ERR_INVALID_VALUE, "stages must be a non-empty mask of QD_STAGE_*");
   int st = check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
@@ -1615,8 +1881,11 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   if (!q || !k_cache || !v_cache || !block_table || !context_lens || !out)
     return fail(QD_ERR_INVALID_VALUE, "null tensor pointer");
   const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out);
+  if (valu && !(aligned && valu_sk_applies(q_heads, kv_heads, head_dim, dtype) &&
+                mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) && batch <= kSkMaxBatch))
+    return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_VALU needs the balanced path with head_dim 128 and group size <= 8");
   AutoPlan ap;
-  st = auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, aligned, &ap);
+  st = auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, aligned, &ap, valu);
   if (st != QD_OK) return st;
   if (!workspace || workspace_bytes < ap.ws_bytes || !aligned16(workspace))
     return fail(QD_ERR_INVALID_VALUE, "workspace smaller than qd_gqa_decode_auto_workspace_bytes()");
@@ -1637,8 +1906,8 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (stages & QD_STAGE_DECODE)
-    hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave), dim3(ap.wgs), dim3(64 * ap.wg_waves), 0,
-                       stm, prm);
+    hipLaunchKernelGGL(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads) : pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave),
+                       dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
   if (stages & QD_STAGE_MERGE) {
     const bool one_head = merge_one_head_per_wave(batch, q_heads);
     hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim, one_head),

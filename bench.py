@@ -61,6 +61,9 @@ def parse():
                          "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config")
     ap.add_argument("--mla-config", default="mla-h128")
     ap.add_argument("--device-gen", action="store_true", help="draw inputs on the GPU")
+    ap.add_argument("--compute", choices=["mfma", "valu"], default="mfma",
+                    help="valu: the balanced kernel with VALU math in place of MFMA (QD_STAGE_VALU, "
+                         "C ABI path), for the MFMA-versus-VALU comparison")
     return ap.parse_args()
 
 
@@ -432,7 +435,22 @@ def main() -> None:
                                                           cfg.head_dim, cfg.block_size, table.shape[1],
                                                           cabi.DTYPE[q.dtype])
 
-    if args.kernel == "auto" and args.splits == 0:
+    valu_stage = cabi.QD_STAGE_VALU if args.compute == "valu" else 0
+    if args.compute == "valu":
+        if args.kernel != "auto" or args.splits:
+            raise SystemExit("--compute valu applies to the automatic balanced path only")
+        path = "C ABI qd_gqa_decode_auto_stages with QD_STAGE_VALU (VALU math, comparison)"
+        vws = torch.empty(cabi.auto_workspace_bytes(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                                                    cfg.block_size, table.shape[1], cabi.DTYPE[q.dtype]),
+                          device=dev, dtype=torch.uint8)
+        vout = torch.empty_like(q)
+
+        def step(i):
+            rc = cabi.auto_launch(q, ks[i % pools], vs[i % pools], table, lens, vout, scale=scale, workspace=vws,
+                                  stream=stream.cuda_stream, stages=cabi.QD_STAGE_ALL | valu_stage)
+            if rc:
+                raise RuntimeError(cabi.error_string(rc))
+    elif args.kernel == "auto" and args.splits == 0:
         path = "torch.ops.qd_attention.gqa_decode (automatic path)"
 
         def step(i):
@@ -477,7 +495,7 @@ def main() -> None:
 
         def decode_stage(i):
             rc = cabi.auto_launch(q, ks[i % pools], vs[i % pools], table, lens, rout, scale=scale,
-                                  workspace=rws, stream=stream.cuda_stream, stages=cabi.QD_STAGE_DECODE)
+                                  workspace=rws, stream=stream.cuda_stream, stages=cabi.QD_STAGE_DECODE | valu_stage)
             if rc:
                 raise RuntimeError(cabi.error_string(rc))
 
@@ -514,7 +532,7 @@ def main() -> None:
             "context_lens": (list(cfg.fixed_lengths) if cfg.fixed_lengths else
                              f"U{list(cfg.len_range)} seed {10_000 + cfg.seed}: sum {sum(lengths)}, "
                              f"min {min(lengths)}, max {max(lengths)}"),
-            "kv_pools_rotated": pools, "path": path, "kernels": kernels,
+            "kv_pools_rotated": pools, "path": path, "kernels": kernels, "compute": args.compute,
             "waves": auto_waves if auto_kind == 1 else None, "splits": splits, "chunk_pages": chunk,
             "algorithmic_bytes_per_call": alg_bytes,
             "flops_per_call": algorithmic_flops(lengths, cfg.q_heads, cfg.head_dim),

@@ -171,6 +171,11 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
  * a following QD_STAGE_MERGE call with the same arguments and workspace on
  * the same stream completes the output. */
 enum { QD_STAGE_DECODE = 1, QD_STAGE_MERGE = 2, QD_STAGE_ALL = 3 };
+/* OR'ed into `stages` for measurement only: run the balanced path's decode
+ * kernel with VALU math (packed dot products and fp32 FMAs) in place of the
+ * MFMA instructions, same loads and partition.  Head_dim 128, group size
+ * <= 8, one kv-head per wave; other shapes are rejected. */
+enum { QD_STAGE_VALU = 4 };
 
 int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_table, const int32_t* context_lens, void* out,

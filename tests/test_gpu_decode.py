@@ -603,3 +603,26 @@ def test_graph_capture_replays_match_eager(gpu):
         assert torch.equal(out, ref), f"replay {i}"
         attention_amd.gqa_decode(*other)   # eager work on the same stream between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("hq,hkv,dtype", [(32, 8, torch.bfloat16), (40, 8, torch.float16), (28, 4, torch.bfloat16),
+                                          (64, 8, torch.bfloat16)], ids=["g4-bf16", "g5-f16", "g7-bf16", "g8-bf16"])
+def test_valu_comparison_variant_matches_oracle(gpu, hq, hkv, dtype):
+    """The VALU math variant of the balanced decode kernel (QD_STAGE_VALU,
+    kept for the MFMA-versus-VALU measurement) on group sizes 4, 5, 7 and 8,
+    with ragged lengths, a zero length and sequences split across
+    workgroups."""
+    lengths = [1, 17, 300, 0, 2049, 1000, 16, 4000]
+    say(f"VALU variant g={hq // hkv} {DT_NAME[dtype]}")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=128, block_size=16,
+                                   dtype=dtype, seed=29), gpu)
+    q, k, v, table, lens = case
+    ref, rows = oracle_rows(case)
+    nbytes = cabi.auto_workspace_bytes(len(lengths), hq, hkv, 128, 16, table.shape[1], cabi.DTYPE[dtype])
+    ws = torch.full((nbytes,), 0xFF, device=gpu, dtype=torch.uint8)
+    out = torch.full_like(q, float("nan"))
+    rc = cabi.auto_launch(q, k, v, table, lens, out, scale=1 / math.sqrt(128), workspace=ws,
+                          stages=cabi.QD_STAGE_ALL | cabi.QD_STAGE_VALU)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert_close(out, ref, DT_NAME[dtype], rows, "VALU variant")
