@@ -499,7 +499,15 @@ struct MfmaWave {
   // flight: the steady-state loop issues unconditionally (static buffer
   // slots, no branches around loads) so the compiler's wait counts cover
   // only the group being consumed.
-  __device__ void run(const DecodeParams& p, int ga, int gb, char* ktile) {
+  //
+  // lockstep: a workgroup barrier every PF groups, for workgroups whose
+  // waves all stream the same groups (one item each, same [ga, gb)).  Two
+  // waves sharing a SIMD are not issued evenly: without it the older wave
+  // of each pair ran ahead and the other finished its range alone with half
+  // the loads in flight (per-wave timestamps: waves of one workgroup ended
+  // 4-8 us apart).  gfx950's barrier does not wait for outstanding loads,
+  // so the prefetched groups stay in flight across it.
+  __device__ void run(const DecodeParams& p, int ga, int gb, char* ktile, bool lockstep = false) {
     const int gpp = p.P >> 4;
     for (int g_lo = ga; g_lo < gb;) {
       if (g_lo != ga) {  // the first window came with begin_item
@@ -514,6 +522,7 @@ struct MfmaWave {
 #pragma unroll
         for (int u = 0; u < PF - 1; ++u) issue(p, buf[u], g_lo + u);
         for (; i + 2 * PF - 2 < n; i += PF) {
+          if (lockstep) __builtin_amdgcn_s_barrier();
 #pragma unroll
           for (int u = 0; u < PF; ++u) {
             issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
@@ -724,7 +733,7 @@ struct ValuWave : MfmaWave<D, DT, PF, 1> {
   }
 
   // Same structure as MfmaWave::run, with this compute.
-  __device__ __forceinline__ void run(const DecodeParams& p, int ga, int gb, char* ptile) {
+  __device__ __forceinline__ void run(const DecodeParams& p, int ga, int gb, char* ptile, bool = false) {
     const int gpp = p.P >> 4;
     for (int g_lo = ga; g_lo < gb;) {
       if (g_lo != ga) {
@@ -970,10 +979,10 @@ constexpr int kMaxWgWaves = 8;
 constexpr int kValuMaxWaves = QD_VALU_WAVES;
 constexpr int kValuPrefetch = QD_VALU_PF;
 
-template <int D, int NKV, int GV = 0>
+template <int D, int NKV, int GV = 0, int PF = 2>
 constexpr int sk_max_waves() {
   if (GV > 0) return kValuMaxWaves;
-  return (NKV == 1 && D <= 128) ? kMaxWgWaves : kMaxWgWaves / 2;
+  return (NKV == 1 && D <= 128 && PF <= 2) ? kMaxWgWaves : kMaxWgWaves / 2;
 }
 
 #ifndef QD_SK_SEQ_COST
@@ -1012,7 +1021,7 @@ __device__ __forceinline__ int64_t seq_cost(int groups) {
 // suffice).  merge_sk_kernel combines the slots of every split sequence.
 // Rows of empty sequences are zero-filled by workgroup b % W.
 template <int D, int DT, int PF, int NKV, int GV = 0>
-__global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV>())) void decode_mfma_sk_kernel(DecodeParams p) {
+__global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_mfma_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -1020,7 +1029,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV>())) void decode_mfma
   const int w = blockIdx.x;
   const int W = p.splits;
   const int B = p.B;
-  __shared__ __align__(16) char ktile[sk_max_waves<D, NKV, GV>()][KTile<D>::kBytes];
+  __shared__ __align__(16) char ktile[sk_max_waves<D, NKV, GV, PF>()][KTile<D>::kBytes];
 
   // Prologue, one memory round trip for B <= 64*kRegChunks: every lane loads
   // the lengths of sequences c*64 + lane, and the group counts and the
@@ -1144,7 +1153,9 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV>())) void decode_mfma
       float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
       for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
         wv.begin_item(p, b, kvh0, len, i0);
-        wv.run(p, i0, i1, ktile[wid]);
+        // Every wave runs exactly one item here when the workgroup's waves
+        // cover the kv-heads once, so all reach the same barriers.
+        wv.run(p, i0, i1, ktile[wid], p.Hkv == nw * NKV);
         if constexpr (GV == 0) {
 #pragma unroll
           for (int j = 0; j < NKV; ++j) {
@@ -1401,8 +1412,17 @@ KernelFn pick_mfma(int D) {
 // bytes per group).
 constexpr int kPrefetchDual = QD_PREFETCH_DUAL;
 
+// Groups in flight per wave for 4 kv-heads at head_dim 128 (sk_wide_applies):
+// one workgroup of 4 waves per CU, one wave per SIMD with up to 512
+// registers.  4-wave workgroups of the 2-in-flight kernel sit two per CU,
+// and the older workgroup of each pair ran ahead of the other as the older
+// wave of a SIMD does (cfg3's decode kernel: 78.8 us, against 76.7-77.1 us
+// with 3 or 4 in flight and one workgroup per CU).
+constexpr int kSkWidePrefetch = 3;
+
 template <int DT>
-KernelFn pick_mfma_sk(int D, int nkv) {
+KernelFn pick_mfma_sk(int D, int nkv, bool wide) {
+  if (wide) return decode_mfma_sk_kernel<128, DT, kSkWidePrefetch, 1>;
   if (nkv == 2) {
     switch (D) {
       case 64: return decode_mfma_sk_kernel<64, DT, kPrefetchDual, 2>;
@@ -1416,9 +1436,13 @@ KernelFn pick_mfma_sk(int D, int nkv) {
   }
 }
 
-KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv) {
-  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D, nkv) : pick_mfma_sk<QD_DTYPE_BF16>(D, nkv);
+KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv, bool wide = false) {
+  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D, nkv, wide) : pick_mfma_sk<QD_DTYPE_BF16>(D, nkv, wide);
 }
+
+// One wave per SIMD needs exactly 4 single-kv-head waves per workgroup;
+// fewer kv-heads would leave SIMDs idle.
+bool sk_wide_applies(int kv_heads, int head_dim) { return kv_heads == 4 && head_dim == 128; }
 
 // The VALU comparison variant of the balanced kernel: head_dim 128, one
 // kv-head per wave, group size <= 8.
@@ -1533,9 +1557,9 @@ bool sk_dual_applies(int batch, int kv_heads, int head_dim, int block_size, int 
 // Waves per stream-K workgroup: the largest divisor of kv_heads / nkv that
 // fits the kernel's bound, so every wave serves the same number of
 // kv-heads.
-int sk_wg_waves(int kv_heads, int nkv, int head_dim, bool valu = false) {
+int sk_wg_waves(int kv_heads, int nkv, int head_dim, bool valu = false, bool wide = false) {
   const int units = kv_heads / nkv;
-  const int cap = valu ? kValuMaxWaves : (nkv == 1 && head_dim <= 128) ? kMaxWgWaves : kMaxWgWaves / 2;
+  const int cap = valu ? kValuMaxWaves : (nkv == 1 && head_dim <= 128 && !wide) ? kMaxWgWaves : kMaxWgWaves / 2;
   for (int n = cap; n > 1; --n)
     if (units % n == 0) return n;
   return 1;
@@ -1546,6 +1570,7 @@ struct AutoPlan {
   int wgs;          // stream-K grid (workgroups)
   int wg_waves;     // stream-K waves per workgroup
   int kv_per_wave;  // stream-K kv-heads per wave
+  bool wide;        // stream-K: one wave per SIMD, kSkWidePrefetch groups in flight
   int splits;       // explicit-split path
   int chunk_pages;
   size_t ws_bytes;  // scratch bytes
@@ -1556,14 +1581,15 @@ struct AutoPlan {
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
               int dtype, bool aligned, AutoPlan* ap, bool valu = false) {
-  *ap = AutoPlan{false, 0, 1, 1, 1, 0, 0, 0};
+  *ap = AutoPlan{false, 0, 1, 1, false, 1, 0, 0, 0};
   if (batch <= 0) return QD_OK;
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
     int nkv = 1;
-    int nw = sk_wg_waves(kv_heads, nkv, head_dim, valu);
+    const bool wide = !valu && sk_wide_applies(kv_heads, head_dim);
+    int nw = sk_wg_waves(kv_heads, nkv, head_dim, valu, wide);
     int resident = resident_blocks(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads)
-                                        : pick_mfma_sk_dt(dtype, head_dim, nkv),
+                                        : pick_mfma_sk_dt(dtype, head_dim, nkv, wide),
                                    64 * nw);
     if (!valu && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
       nkv = 2;
@@ -1580,6 +1606,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     ap->wgs = static_cast<int>(w);
     ap->wg_waves = nw;
     ap->kv_per_wave = nkv;
+    ap->wide = wide && nkv == 1;
     ap->meta_offset = static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
     ap->ws_bytes = ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
     return QD_OK;
@@ -1639,6 +1666,26 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.meta = nullptr;
   prm.wg_waves = 1;
   return prm;
+}
+
+// Scratch bytes the automatic path needs for these shapes: the larger of
+// the aligned and unaligned plans, so that the size does not depend on
+// pointer alignment, and with_valu: also QD_STAGE_VALU's plan (its
+// partition may have more workgroups).  0 for invalid shapes.
+size_t auto_scratch_bytes(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
+                          int dtype, bool with_valu) {
+  if (check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, 1, dtype, 1.f) != QD_OK)
+    return 0;
+  AutoPlan a, b, c;
+  if (auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &a) != QD_OK ||
+      auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, false, &b) != QD_OK)
+    return 0;
+  size_t bytes = a.ws_bytes > b.ws_bytes ? a.ws_bytes : b.ws_bytes;
+  if (with_valu && valu_sk_applies(q_heads, kv_heads, head_dim, dtype) &&
+      auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &c, true) == QD_OK &&
+      c.ws_bytes > bytes)
+    bytes = c.ws_bytes;
+  return bytes;
 }
 
 int launch_error() {
@@ -1853,16 +1900,7 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
 
 size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
                                           int block_size, int max_pages, int dtype) {
-  if (check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, 1, dtype, 1.f) !=
-      QD_OK)
-    return 0;
-  // The larger of the two paths, so that the size does not depend on
-  // pointer alignment.
-  AutoPlan a, b;
-  if (auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &a) != QD_OK ||
-      auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, false, &b) != QD_OK)
-    return 0;
-  return a.ws_bytes > b.ws_bytes ? a.ws_bytes : b.ws_bytes;
+  return auto_scratch_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true);
 }
 
 int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_cache,
@@ -1906,7 +1944,7 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (stages & QD_STAGE_DECODE)
-    hipLaunchKernelGGL(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads) : pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave),
+    hipLaunchKernelGGL(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads) : pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide),
                        dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
   if (stages & QD_STAGE_MERGE) {
     const bool one_head = merge_one_head_per_wave(batch, q_heads);
@@ -1937,7 +1975,7 @@ int qd_gqa_decode_auto_noalloc(const void* q, const void* k_cache, const void* v
   if (st != QD_OK) return st;
   if (batch == 0) return QD_OK;
   const size_t need =
-      qd_gqa_decode_auto_workspace_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype);
+      auto_scratch_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, false);
   if (need > kNoAllocScratchBytes)
     return fail(QD_ERR_INVALID_VALUE, "shapes need " + std::to_string(need) +
                                           " bytes of scratch, more than the no-allocation scratch holds (" +

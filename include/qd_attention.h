@@ -149,7 +149,8 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  *   - otherwise: the split layout of qd_gqa_decode_launch with the plan of
  *     qd_gqa_decode_plan.
  * The workspace is device scratch, 16-byte aligned, of at least
- * qd_gqa_decode_auto_workspace_bytes() bytes.  Its contents need no
+ * qd_gqa_decode_auto_workspace_bytes() bytes (which also covers
+ * QD_STAGE_VALU below).  Its contents need no
  * initialization: every call writes what it reads (the partial slots and,
  * for every sequence, its span entry).  Calls that may run concurrently
  * (different streams, or replays of captured graphs on different streams)

@@ -548,6 +548,21 @@ def test_auto_wave_shapes_by_capacity(gpu, dtype):
         assert_close(out, ref, DT_NAME[dtype], rows, f"max_pages={maxp}")
 
 
+def test_auto_wave_layout_on_device(gpu):
+    """Resident waves of the automatic path on the device: one workgroup per
+    CU in every layout.  8 kv-heads: 8 one-kv-head waves (two per SIMD), or
+    4 two-kv-head waves for large capacities; 4 kv-heads at head_dim 128: 4
+    waves with one per SIMD (3 groups in flight), not two 4-wave workgroups
+    per CU."""
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    bf16 = cabi.DTYPE[torch.bfloat16]
+    say(f"wave layout on device: {cus} CUs")
+    assert cabi.auto_info(32, 32, 8, 128, 16, 256, bf16)[:2] == (1, cus * 8)     # cfg2
+    assert cabi.auto_info(8, 64, 8, 128, 16, 8192, bf16)[:2] == (1, cus * 4)     # cfg4
+    assert cabi.auto_info(64, 28, 4, 128, 16, 512, bf16)[:2] == (1, cus * 4)     # cfg3
+    assert cabi.auto_info(64, 28, 4, 64, 16, 512, bf16)[1] > cus * 4             # D 64: 4-wave groups share CUs
+
+
 def test_repeat_calls_deterministic(gpu):
     say("determinism across calls")
     case = to_dev(CONFIGS["cfg3"].make(device="cpu"), gpu)
