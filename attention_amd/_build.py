@@ -56,10 +56,16 @@ def _run(cmd: list[str], verbose: bool) -> None:
 HIP_SOURCES = ["gqa_decode", "kv_append", "validate", "mla"]
 OBJ_DIR = os.path.join(ROOT, "_build", "obj")
 
+# Per-source flags.  mla: MFMA accumulators in VGPRs where the register
+# budget allows (one wave per SIMD gives 512); with the default AGPR form the
+# attention kernels moved hundreds of registers between the two files per
+# cache tile.
+SOURCE_FLAGS = {"mla": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def hip_object_cmd(name: str) -> list[str]:
-    return [_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", "-c", os.path.join(CSRC, f"{name}.hip"),
-            "-o", os.path.join(OBJ_DIR, f"{name}.o")]
+    return [_hipcc(), *HIP_FLAGS, *SOURCE_FLAGS.get(name, []), f"-I{INCLUDE}", "-c",
+            os.path.join(CSRC, f"{name}.hip"), "-o", os.path.join(OBJ_DIR, f"{name}.o")]
 
 
 def hip_link_cmd() -> list[str]:

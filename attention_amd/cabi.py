@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(PKG, "lib", "libqd_attention.so")
 DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.int32: 3, torch.int64: 4}
 QD_FLAG_FORCE_GENERIC = 1
 QD_FLAG_MLA_STAGED = 2
+QD_FLAG_MLA_WAVE = 4
 QD_STAGE_DECODE, QD_STAGE_MERGE, QD_STAGE_ALL = 1, 2, 3
 QD_STAGE_VALU = 4   # measurement option: VALU math in the balanced decode kernel
 

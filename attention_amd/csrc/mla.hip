@@ -37,6 +37,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <type_traits>
 #include <string>
 
 #include "qd_attention.h"
@@ -1475,6 +1476,459 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
   merge_before(rows);
 }
 
+// ----------------------------------------------------------------------------
+// Paged latent attention, pair kernel: dense rows, Dc 512, Dr 64, 32*NHB
+// heads per workgroup of four waves (two pairs), cache tiles fed to LDS by
+// DMA
+// ----------------------------------------------------------------------------
+
+constexpr int kPairThreads = 256;                       // four waves: two pairs
+constexpr int kPairBufs = 7;                            // LDS tile ring
+constexpr int kPairRowBytes = 2 * 576;                  // cache row: 512 latent + 64 rope, 16-bit
+constexpr int kPairLatStride = 1024 + 16;              // LDS bytes per latent row (padded)
+constexpr int kPairLatBytes = 16 * kPairLatStride;      // latent part of a 16-row tile
+constexpr int kPairTileBytes = kPairLatBytes + 2 * 1024;  // + rope rows (8 per KB)
+constexpr int kPairRows = 1024;                         // query rows (prologue arrays in the ring)
+constexpr int kPairListTiles = 1024;                    // tiles of one workgroup's range
+constexpr int kPairDma = 5;                             // DMA instructions per wave per tile
+#ifndef QD_MLA_PAIR_ROW_COST
+#define QD_MLA_PAIR_ROW_COST 8
+#endif
+// Partition cost of a row's start, in tile units: the query load drains the
+// tile pipeline once, and the row's output or partial is stored.
+constexpr int kPairRowCost = QD_MLA_PAIR_ROW_COST;
+
+template <int NHB>
+__host__ __device__ constexpr size_t mla_pair_lds_bytes() {
+  return static_cast<size_t>(kPairBufs) * kPairTileBytes  // tile ring (prologue arrays before the first tile)
+         + 4 * NHB * 64 * 16                              // score exchange
+         + static_cast<size_t>(kPairListTiles) * 16;      // tile list
+}
+
+// The prologue's arrays fit in the ring, which the first DMA overwrites.
+static_assert(kPairRows * (4 + 4 + 8) + kPairListTiles * 16 <= kPairBufs * kPairTileBytes,
+              "pair kernel prologue arrays exceed the tile ring");
+
+// LDS wait for the DMA ring: all but the last kVm vector-memory operations of
+// this wave done (loads into LDS included), this wave's LDS operations done,
+// then the workgroup barrier.  The empty asm statements keep the compiler
+// from moving memory accesses across.
+template <int kVm>
+__device__ __forceinline__ void pair_dma_barrier() {
+  static_assert(kVm >= 0 && kVm < 64, "vmcnt is 6 bits");
+  constexpr int imm = (kVm & 0xF) | ((kVm >> 4) << 14) | (0x7 << 4) | (0x0 << 8);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(imm);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Stream-K over (query row, 16-token tile) like mla_attend_wave_kernel (same
+// grid mapping, meta, slots and merge kernel), one workgroup per CU with
+// 32*NHB heads and every wave on every tile of the workgroup's range.  Wave
+// v belongs to pair v / 2 (heads 16*NHB*(v/2) .. of the workgroup's) and
+// takes latent half hv = v % 2:
+//   load     each wave DMAs a quarter of the tile's 16 cache rows (latent
+//            rows 4v .. 4v + 3, 1 KB per instruction, and their rope bytes)
+//            into one of kPairBufs LDS buffers (global_load_lds),
+//            kPairBufs - 1 tiles ahead; no registers hold tiles in flight.
+//            Latent rows are 1 KB apart plus 16 bytes (each instruction has
+//            its own LDS base), so the operand reads below meet no LDS bank
+//            conflict and take immediate offsets from one lane address; rope
+//            chunk c of row R sits at c ^ (R/2 % 8).  Rows past the tile's
+//            visible count re-read its last visible row and get weight 0.
+//   QK       wave hv takes the 9 chunks 9 hv .. 9 hv + 8 of the 18
+//            32-element chunks of [latent | rope]: S^T partial = K chunk x
+//            [q | q_rope] chunk for its pair's NHB blocks of 16 heads (query
+//            in registers, loaded when a row segment starts); the two
+//            partial scores of a pair meet through LDS and both waves add
+//            them (the same sum in both: IEEE addition commutes).
+//   softmax  fp32 with the lazy reference max of the wave kernel; both
+//            waves of a pair compute the same weights.
+//   PV       wave hv: latent columns 256 hv .. +255 for its pair's heads
+//            (A = C^T from 4 LDS rows, 8x8 byte-permute transposes, as in the
+//            wave kernel; one A feeds NHB head blocks).
+// At the end of a row segment each wave stores its half of the columns:
+// the output (whole row) or the partial {m, l, acc} in slot (w + row).
+// NT: nontemporal cache loads (one head group); with several head groups
+// the tiles stay in L2 for the other groups' workgroups on the XCD.
+template <int DT, int NHB, bool NT>
+__global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams p) {
+  using E = Elem<DT>;
+  using Ops = MfmaOps<DT>;
+  using S = typename E::S;
+  constexpr int kDc = 512;
+  constexpr int kW = 576;
+  extern __shared__ __align__(16) char smem[];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hv = wv & 1;
+  const int r16 = lane & 15, q4 = lane >> 4;
+
+  const int L = blockIdx.x;
+  const int hg = (L >> 3) % p.head_groups;
+  const int w = ((L >> 3) / p.head_groups) * 8 + (L & 7);
+  if (w >= p.wgs) return;  // whole workgroup: uniform
+
+  char* ring = smem;
+  f32x4* xch = reinterpret_cast<f32x4*>(smem + kPairBufs * kPairTileBytes);            // [4][NHB][64]
+  i32x4* ctl = reinterpret_cast<i32x4*>(smem + kPairBufs * kPairTileBytes + 4 * NHB * 64 * 16);
+  // Prologue arrays, inside the ring.
+  int* rt = reinterpret_cast<int*>(ring);                 // [rows] tiles
+  int* re = rt + kPairRows;                               // [rows] visible end
+  int64_t* incl = reinterpret_cast<int64_t*>(re + kPairRows);  // [rows] prefix of costs
+  i32x4* tl = reinterpret_cast<i32x4*>(incl + kPairRows);    // [positions]
+
+  const int rows = p.B * p.T;  // <= kPairRows (host check)
+  constexpr int kHeads = 32 * NHB;   // per workgroup
+  const int h0 = kHeads * hg;
+  const int hp = h0 + 16 * NHB * (wv >> 1);  // this pair's first head
+  const char* cache = static_cast<const char*>(p.cache);
+
+  // --- Prologue -----------------------------------------------------------
+  for (int r = tid; r < rows; r += kPairThreads) {
+    const int end = row_end(p, r / p.T, r);
+    re[r] = end;
+    rt[r] = (end + kSubTokens - 1) / kSubTokens;
+  }
+  __syncthreads();
+  auto row_cost = [&](int tiles) { return tiles > 0 ? tiles + kPairRowCost : 0; };
+  if (wv == 0) {
+    int64_t carry = 0;
+    for (int base = 0; base < rows; base += 64) {
+      const int r = base + lane;
+      const int64_t n = r < rows ? row_cost(rt[r]) : 0;
+      const int64_t v = carry + wave_incl_scan_i64(n, lane);
+      if (r < rows) incl[r] = v;
+      carry = __shfl(v, 63);
+    }
+  }
+  __syncthreads();
+  const int64_t G = incl[rows - 1];
+  const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
+  const int64_t g1 = static_cast<int64_t>(w + 1) * G / p.wgs;
+  const int npos = static_cast<int>(g1 - g0);  // <= kPairListTiles (host check)
+  if (w == 0 && hg == 0 && tid == 0) *p.gtotal = G;
+  auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * p.wgs - 1) / G); };
+  // Positions of this range: the first kPairRowCost positions of a row hold
+  // no tile (row -1); the others tile i of the row: element offset of its
+  // first cache row, visible rows | whole-row flag << 16, row.
+  for (int t = tid; t < npos; t += kPairThreads) {
+    const int64_t g = g0 + t;
+    int lo = 0, hi = rows - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (incl[mid] > g) hi = mid; else lo = mid + 1;
+    }
+    const int r = lo;
+    const int64_t first = incl[r] - rt[r];
+    const int tir = static_cast<int>(g - first);
+    if (tir < 0) {
+      tl[t] = i32x4{0, 0, 0, -1};
+      continue;
+    }
+    const int tok0 = kSubTokens * tir;
+    const int pg = tok0 / p.P;
+    int32_t phys = p.table[static_cast<int64_t>(r / p.T) * p.maxP + pg];
+    if (phys < 0) phys = 0;
+    if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
+    const int64_t base = (static_cast<int64_t>(phys) * p.P + (tok0 - pg * p.P)) * kW;
+    const int whole = (first >= g0 && incl[r] <= g1) ? 1 : 0;
+    tl[t] = i32x4{static_cast<int>(base & 0xFFFFFFFF), static_cast<int>(base >> 32),
+                  min(kSubTokens, re[r] - tok0) | (whole << 16), r};
+    if (tir == 0 && hg == 0) {
+      // This workgroup holds the row's first tile: record its span.
+      p.meta[2 * r] = w;
+      p.meta[2 * r + 1] = wg_of(incl[r] - 1) - w + 1;
+    }
+  }
+  // Rows with no tile: zeros from workgroup (row % wgs), meta {0, 0}.
+  for (int r = w; r < rows; r += p.wgs) {
+    if (rt[r] != 0) continue;
+    for (int i = tid; i < kHeads * kDc / 8; i += kPairThreads) {
+      const int h = h0 + i / (kDc / 8);
+      if (h < p.H)
+        *reinterpret_cast<u32x4*>(static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * kDc +
+                                  8 * (i % (kDc / 8))) = u32x4{0u, 0u, 0u, 0u};
+    }
+    if (hg == 0 && tid == 0) {
+      p.meta[2 * r] = 0;
+      p.meta[2 * r + 1] = 0;
+    }
+  }
+  __syncthreads();
+  // Compact the tiles (wave 0); their count goes through the exchange area.
+  if (wv == 0) {
+    int count = 0;
+    for (int base = 0; base < npos; base += 64) {
+      const int t = base + lane;
+      const i32x4 e = t < npos ? tl[t] : i32x4{0, 0, 0, -1};
+      const bool real = e[3] >= 0;
+      const uint64_t bal = __ballot(real);
+      const int before = __popcll(bal & ((uint64_t{1} << lane) - 1));
+      if (real) ctl[count + before] = e;
+      count += __popcll(bal);
+    }
+    if (lane == 0) reinterpret_cast<int*>(xch)[0] = count;
+  }
+  __syncthreads();
+  const int n = reinterpret_cast<const int*>(xch)[0];
+  if (n == 0) return;  // whole workgroup: uniform
+
+  // --- Main loop ------------------------------------------------------------
+  // The rest is instantiated per latent half (wave-uniform hv), so every
+  // chunk and column index is a compile-time constant.
+  auto body = [&](auto half) {
+    constexpr int HV = decltype(half)::value;
+    // DMA of tile t (past the end: a re-read of the cache's first row into
+    // the unused slot, so every step issues the same loads).
+    auto dma = [&](int t) {
+      char* slot = ring + (t % kPairBufs) * kPairTileBytes;
+      int64_t base = 0;
+      int nv = 1;
+      if (t < n) {
+        const i32x4 e = ctl[t];
+        base = static_cast<int64_t>(static_cast<uint32_t>(e[0])) | (static_cast<int64_t>(e[1]) << 32);
+        nv = e[2] & 0xFFFF;
+      }
+      const char* tb = cache + 2 * base;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int R = 4 * wv + k;
+        const int Rc = R < nv ? R : nv - 1;
+        const char* src = tb + Rc * kPairRowBytes + 16 * lane;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)(slot + R * kPairLatStride), 16,
+                                         0, NT ? 2 : 0);
+      }
+      // Rope bytes of the same 4 rows: 32 lanes, 512 bytes.
+      if (lane < 32) {
+        const int R = 4 * wv + (lane >> 3);
+        const int Rc = R < nv ? R : nv - 1;
+        const int c = (lane & 7) ^ ((R >> 1) & 7);
+        const char* src = tb + Rc * kPairRowBytes + 2 * kDc + 16 * c;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)(slot + kPairLatBytes + wv * 512),
+                                         16, 0, NT ? 2 : 0);
+      }
+    };
+    // Query chunks 9 HV .. 9 HV + 8 of this pair's heads for row r.  Heads
+    // past H read head 0's query (never stored; no select on the loaded
+    // values, which would wait for every load in flight).
+    u32x4 qv[NHB][9];
+    auto load_q = [&](int r) {
+#pragma unroll
+      for (int j = 0; j < NHB; ++j) {
+        const int h = hp + 16 * j + r16;
+        const int64_t hr = static_cast<int64_t>(r) * p.H + (h < p.H ? h : 0);
+        const char* qrow = static_cast<const char*>(p.q) + hr * kDc * 2;
+        const char* rrow = static_cast<const char*>(p.qr) + hr * (kW - kDc) * 2;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+          const int c = 9 * HV + k;
+          qv[j][k] = c < 16 ? *reinterpret_cast<const u32x4*>(qrow + (32 * c + 8 * q4) * 2)
+                            : *reinterpret_cast<const u32x4*>(rrow + (32 * (c - 16) + 8 * q4) * 2);
+        }
+      }
+    };
+
+    float m_run[NHB], l_run[NHB];
+    f32x4 acc[NHB][2][8];
+    auto reset = [&]() {
+#pragma unroll
+      for (int j = 0; j < NHB; ++j) {
+        m_run[j] = -INFINITY;
+        l_run[j] = 0.f;
+#pragma unroll
+        for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j][b2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+
+#pragma unroll
+    for (int t = 0; t < kPairBufs - 1; ++t) dma(t);
+    // The first query completes here (with the first tiles), so no register
+    // load is pending when the loop starts (see the wait after the next
+    // row's query below).
+    load_q(ctl[0][3]);
+    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0)
+    int row = -1;
+    for (int t = 0; t < n; ++t) {
+      pair_dma_barrier<(kPairBufs - 2) * kPairDma>();  // tile t in LDS; tile t-1 done by both waves
+      dma(t + kPairBufs - 1);
+      const i32x4 e = ctl[t];
+      const int nv = e[2] & 0xFFFF;
+      const bool whole = (e[2] >> 16) != 0;
+      const int r = e[3];
+      const bool last = t + 1 == n || ctl[t + 1][3] != r;
+      if (r != row) {
+        row = r;
+        reset();
+      }
+      const char* slot = ring + (t % kPairBufs) * kPairTileBytes;
+
+      // QK partial over this wave's 9 chunks, operands read kAhead chunks
+      // before their MFMAs; the scheduling barriers keep that distance (left
+      // free, the scheduler sinks each read next to its MFMA).
+      const char* lat = slot + r16 * kPairLatStride + 16 * q4;
+      const char* rop = slot + kPairLatBytes + r16 * 128;
+      auto a_chunk = [&](int k) {
+        const int c = 9 * HV + k;
+        if (c < 16) return *reinterpret_cast<const u32x4*>(lat + 64 * c);
+        return *reinterpret_cast<const u32x4*>(rop + 16 * ((4 * (c - 16) + q4) ^ ((r16 >> 1) & 7)));
+      };
+      constexpr int kAhead = 4;
+      u32x4 a[kAhead];
+#pragma unroll
+      for (int k = 0; k < kAhead; ++k) a[k] = a_chunk(k);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 s[NHB], s2[NHB];
+#pragma unroll
+      for (int j = 0; j < NHB; ++j) s[j] = s2[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        const u32x4 ak = a[k % kAhead];
+        if (k + kAhead < 9) a[k % kAhead] = a_chunk(k + kAhead);
+#pragma unroll
+        for (int j = 0; j < NHB; ++j) {
+          if (k & 1)
+            s2[j] = Ops::mma32(ak, qv[j][k], s2[j]);
+          else
+            s[j] = Ops::mma32(ak, qv[j][k], s[j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // The next row's query, once this row's last scores are issued.  The
+      // explicit wait keeps the load from being pending at the loop's back
+      // edge: the compiler would otherwise wait for every load in flight
+      // (the whole DMA ring) before the QK of every tile.
+      if (last && t + 1 < n) {
+        load_q(ctl[t + 1][3]);
+        __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0), expcnt and lgkmcnt free
+      }
+#pragma unroll
+      for (int j = 0; j < NHB; ++j) {
+        s[j] += s2[j];
+        xch[(wv * NHB + j) * 64 + lane] = s[j];
+      }
+      lds_barrier();  // the partner's partial scores
+#pragma unroll
+      for (int j = 0; j < NHB; ++j) s[j] += xch[((wv ^ 1) * NHB + j) * 64 + lane];
+
+      // PV operands (tokens 4 q4 + i, columns 256 HV + 128 b2 + 8 r16 ..).
+      const char* pv0 = slot + 4 * q4 * kPairLatStride + 256 * (2 * HV) + 16 * r16;
+      u32x4 raw[2][4];
+#pragma unroll
+      for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          raw[b2][i] = *reinterpret_cast<const u32x4*>(pv0 + i * kPairLatStride + 256 * b2);
+
+      // Softmax per head block (lazy reference max, as the wave kernel).
+      u32x4 pbl[NHB];
+      u32x2 pb[NHB];
+#pragma unroll
+      for (int j = 0; j < NHB; ++j) {
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = 4 * q4 + i < nv ? s[j][i] * p.sl2 : -INFINITY;
+        float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        mx = max_over_lane_groups(mx);
+        const bool move = mx > m_run[j] + kWaveLazyLog2;
+        if (__ballot(move)) {
+          const float mn = fmaxf(m_run[j], mx);
+          const float alpha = mn == m_run[j] ? 1.f : fast_exp2(m_run[j] - mn);  // m_run = -inf: 0
+          m_run[j] = mn;
+          l_run[j] *= alpha;
+#pragma unroll
+          for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+            for (int ee = 0; ee < 8; ++ee) acc[j][b2][ee] *= alpha;
+        }
+        const float m_use = m_run[j] == -INFINITY ? 0.f : m_run[j];
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - m_use);
+        pb[j] = u32x2{Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
+        pbl[j] = u32x4{pb[j][0], pb[j][1], 0u, 0u};
+        if constexpr (Ops::kSplitWeights) {
+          pbl[j][2] = Ops::rest2(pr[0], pr[1], pb[j][0]);
+          pbl[j][3] = Ops::rest2(pr[2], pr[3], pb[j][1]);
+          l_run[j] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        } else {
+          l_run[j] += Ops::sum2(pb[j][0]) + Ops::sum2(pb[j][1]);
+        }
+      }
+
+      // PV: C tile (b2, ee) row m <-> latent column 256 HV + 128 b2 + 8 m + ee.
+#pragma unroll
+      for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+        for (int ee = 0; ee < 8; ++ee) {
+          const int wd = ee >> 1;
+          const uint32_t sel = (ee & 1) ? 0x07060302u : 0x05040100u;
+          const u32x2 av = {__builtin_amdgcn_perm(raw[b2][1][wd], raw[b2][0][wd], sel),
+                            __builtin_amdgcn_perm(raw[b2][3][wd], raw[b2][2][wd], sel)};
+#pragma unroll
+          for (int j = 0; j < NHB; ++j) {
+            if constexpr (Ops::kSplitWeights)
+              acc[j][b2][ee] = Ops::mma32(u32x4{av[0], av[1], av[0], av[1]}, pbl[j], acc[j][b2][ee]);
+            else
+              acc[j][b2][ee] = Ops::pv(av, pb[j], acc[j][b2][ee]);
+          }
+        }
+
+      if (last) {
+        // This wave's columns 256 HV .. +255 of the row segment.
+#pragma unroll
+        for (int j = 0; j < NHB; ++j) {
+          const int h = hp + 16 * j + r16;
+          const float Lt = sum_over_lane_groups(l_run[j]);
+          if (h >= p.H) continue;
+          if (whole) {
+            const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+            S* orow = static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * kDc;
+#pragma unroll
+            for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                uint32_t wd[4];
+#pragma unroll
+                for (int ee = 0; ee < 8; ee += 2)
+                  wd[ee / 2] = Ops::pack2(acc[j][b2][ee][i] * inv, acc[j][b2][ee + 1][i] * inv);
+                *reinterpret_cast<u32x4*>(orow + 128 * (2 * HV + b2) + 32 * q4 + 8 * i) =
+                    u32x4{wd[0], wd[1], wd[2], wd[3]};
+              }
+          } else {
+            float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kDc + 2);
+            if (HV == 0 && q4 == 0) {
+              pr[0] = m_run[j] == -INFINITY ? -INFINITY : m_run[j] * kLn2;
+              pr[1] = Lt;
+            }
+            // Rows are Dc+2 floats: the accumulator starts 8 bytes in.
+#pragma unroll
+            for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int ee = 0; ee < 8; ee += 2)
+                  *reinterpret_cast<f32x2*>(pr + 2 + 128 * (2 * HV + b2) + 32 * q4 + 8 * i + ee) =
+                      f32x2{acc[j][b2][ee][i], acc[j][b2][ee + 1][i]};
+          }
+        }
+      }
+    }
+    // Drain the placeholder loads before the workgroup's LDS is released.
+    __builtin_amdgcn_s_waitcnt(0);
+  };
+  if (hv == 0)
+    body(std::integral_constant<int, 0>{});
+  else
+    body(std::integral_constant<int, 1>{});
+}
+
 // Merge of the stream-K partials: one wave per (row, head) of a row split
 // across workgroups (meta[row] = {first, count >= 2}); the partial of
 // workgroup k is in slot k + row, for the k in [first, first + count) whose
@@ -1748,6 +2202,7 @@ struct AttendPlan {
   size_t lds;
   int splits;  // VALU kernel
   bool wave;   // MFMA path through mla_attend_wave_kernel
+  bool pair;   // MFMA path through mla_attend_pair_kernel
 };
 
 // Smallest instantiated DMA-chunk count covering ceil(W/64), 0 if none.
@@ -1791,8 +2246,26 @@ AttendPlan plan_attend(const AttendShape& a, int forced, int flags) {
     const int64_t gmax =
         rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens + kWaveRowCost);
     const size_t wlds = mla_wave_lds_bytes(4, 2);
-    if ((flags & QD_FLAG_MLA_STAGED) == 0 && a.Dc == 512 && a.Dr == 64 && a.nk < 0 && a.P % kSubTokens == 0 &&
-        rows <= kWaveRows && wlds <= static_cast<size_t>(device_max_lds())) {
+    // The pair kernel: the same dense shapes with 64 heads or more, 64 heads
+    // per workgroup of four waves, one workgroup per CU.
+    const size_t plds = mla_pair_lds_bytes<2>();
+    const bool dense512 = a.Dc == 512 && a.Dr == 64 && a.nk < 0 && a.P % kSubTokens == 0;
+    if ((flags & (QD_FLAG_MLA_STAGED | QD_FLAG_MLA_WAVE)) == 0 && dense512 && a.H >= 64 && rows <= kPairRows &&
+        plds <= static_cast<size_t>(device_max_lds())) {
+      const int groups = (a.H + 63) / 64;
+      const int wgs = forced > 0 ? forced : std::max(1, device_cus() / groups);
+      const int64_t pmax =
+          rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens + kPairRowCost);
+      if ((pmax + wgs - 1) / wgs + 1 <= kPairListTiles) {
+        pl.pair = true;
+        pl.nht = 1;
+        pl.head_groups = groups;
+        pl.wgs = wgs;
+        pl.lds = plds;
+      }
+    }
+    if (!pl.pair && (flags & QD_FLAG_MLA_STAGED) == 0 && dense512 && rows <= kWaveRows &&
+        wlds <= static_cast<size_t>(device_max_lds())) {
       const int groups = ht;
       const int wgs = forced > 0 ? forced : std::max(1, device_cus() / groups);
       if ((gmax + wgs - 1) / wgs + 1 <= kWaveListTiles) {
@@ -1860,6 +2333,20 @@ hipError_t launch_attend_wave(const MlaParams& prm, const AttendPlan& pl, int64_
   return hipSuccess;
 }
 
+template <int DT, bool NT>
+hipError_t launch_attend_pair(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
+  auto fn = mla_attend_pair_kernel<DT, 2, NT>;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [&] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(mla_pair_lds_bytes<2>()));
+  });
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kPairThreads), pl.lds, st, prm);
+  return hipSuccess;
+}
+
 template <int DT>
 hipError_t dispatch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
   switch (pl.cpt * 8 + pl.ds) {
@@ -1921,7 +2408,13 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   if (pl.mfma) {
     const int64_t grid = (static_cast<int64_t>(pl.wgs) + 7) / 8 * 8 * pl.head_groups;
     if (grid > 2147483647LL) return mla_fail(nullptr, 0, "mla_attend grid exceeds launch limits");
-    if (pl.wave && pl.head_groups == 1)
+    if (pl.pair && pl.head_groups == 1)
+      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_pair<QD_DTYPE_BF16, true>(prm, pl, grid, st)
+                                     : launch_attend_pair<QD_DTYPE_F16, true>(prm, pl, grid, st);
+    else if (pl.pair)
+      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_pair<QD_DTYPE_BF16, false>(prm, pl, grid, st)
+                                     : launch_attend_pair<QD_DTYPE_F16, false>(prm, pl, grid, st);
+    else if (pl.wave && pl.head_groups == 1)
       err = a.dtype == QD_DTYPE_BF16 ? launch_attend_wave<QD_DTYPE_BF16, true>(prm, pl, grid, st)
                                      : launch_attend_wave<QD_DTYPE_F16, true>(prm, pl, grid, st);
     else if (pl.wave)
@@ -2183,7 +2676,7 @@ int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope
   const AttendPlan pl = plan_attend(a, splits, flags);
   if (out_splits) *out_splits = pl.mfma ? pl.wgs : pl.splits;
   if (head_groups) *head_groups = pl.mfma ? pl.head_groups : 0;
-  return pl.mfma ? (pl.wave ? 2 : 1) : 0;
+  return pl.mfma ? (pl.pair ? 3 : pl.wave ? 2 : 1) : 0;
 }
 
 int qd_mla_attend(const void* q, const void* q_rope, const void* cache, const int32_t* block_table,

@@ -60,6 +60,8 @@ def parse():
                     help="kv_append: time the paged cache append on the config's shapes instead; "
                          "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config")
     ap.add_argument("--mla-config", default="mla-h128")
+    ap.add_argument("--mla-kernel", choices=["auto", "wave", "staged"], default="auto",
+                    help="--op mla: attention kernel of the timed attention stage (comparison)")
     ap.add_argument("--device-gen", action="store_true", help="draw inputs on the GPU")
     ap.add_argument("--compute", choices=["mfma", "valu"], default="mfma",
                     help="valu: the balanced kernel with VALU math in place of MFMA (QD_STAGE_VALU, "
@@ -294,17 +296,19 @@ def mla_mode(args) -> None:
     log(f"mla_decode: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s algorithmic")
 
     # Latent attention alone, on the absorbed query.
+    mflags = {"auto": 0, "wave": cabi.QD_FLAG_MLA_WAVE, "staged": cabi.QD_FLAG_MLA_STAGED}[args.mla_kernel]
     kind, splits, groups = cabi.mla_attend_info(B, 1, H, Dc, Dr, P, table.shape[1], -1, cabi.DTYPE[cfg.dtype],
-                                                args.splits)
+                                                args.splits, mflags)
     qa = attention_amd.mla_query_absorb(c["q_nope"], c["w_uk"])
     lat = torch.empty(B, 1, H, Dc, dtype=cfg.dtype, device=dev)
     need = cabi.lib().qd_mla_attend_workspace_bytes(B, 1, H, Dc, Dr, P, table.shape[1], -1,
-                                                    cabi.DTYPE[cfg.dtype], args.splits, 0)
+                                                    cabi.DTYPE[cfg.dtype], args.splits, mflags)
     ws = torch.empty(max(16, need), dtype=torch.uint8, device=dev)
 
     def attend(i):
         rc = cabi.mla_attend(qa, c["q_rope"], caches[i % pools], table, lens,
-                             pos, lat, scale=scale, splits=args.splits, workspace=ws, stream=stream.cuda_stream)
+                             pos, lat, scale=scale, splits=args.splits, workspace=ws, flags=mflags,
+                             stream=stream.cuda_stream)
         if rc:
             raise RuntimeError(cabi.error_string(rc))
     a_ms = time_loop(attend, args.steps, args.warmup, stream)
@@ -312,7 +316,8 @@ def mla_mode(args) -> None:
     a_gbs = a_bytes / (a_ms * 1e-3) / 1e9
     a_flops = 2 * rows * H * (Dc + Dr + Dc)
     a_tflops = a_flops / (a_ms * 1e-3) / 1e12
-    kname = {2: "mla_attend_wave_kernel", 1: "mla_attend_mfma_kernel"}.get(kind, "mla_attend_generic_kernel")
+    kname = {3: "mla_attend_pair_kernel", 2: "mla_attend_wave_kernel",
+             1: "mla_attend_mfma_kernel"}.get(kind, "mla_attend_generic_kernel")
     if kind >= 1:
         kernels = kname + "+mla_merge_sk_kernel"
     else:

@@ -22,6 +22,7 @@ pytestmark = pytest.mark.gpu
 
 QD_FLAG_FORCE_GENERIC = 1
 QD_FLAG_MLA_STAGED = 2
+QD_FLAG_MLA_WAVE = 4
 TOL = {torch.bfloat16: (2e-3, 1e-2), torch.float16: (2e-3, 1e-2), torch.float32: (1e-4, 1e-4)}
 ODT = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
 
@@ -78,7 +79,7 @@ ATTEND_SHAPES = [
 
 
 @pytest.mark.parametrize("name,kw", ATTEND_SHAPES, ids=[s[0] for s in ATTEND_SHAPES])
-@pytest.mark.parametrize("variant", ["auto", "split1", "split3", "generic", "staged"])   # split<n>: forced partition
+@pytest.mark.parametrize("variant", ["auto", "split1", "split3", "generic", "staged", "wave"])   # split<n>: forced partition
 def test_mla_attend_matches_oracle(gpu, name, kw, variant):
     say(f"mla_attend {name} {variant}")
     dtype = kw["dtype"]
@@ -87,8 +88,8 @@ def test_mla_attend_matches_oracle(gpu, name, kw, variant):
     B, T, H, Dc = qa.shape
     scale = default_mla_scale(c["q_nope"].shape[-1], c["q_rope"].shape[-1])
     out = torch.empty_like(qa)
-    splits = {"auto": 0, "split1": 1, "split3": 3, "generic": 0, "staged": 0}[variant]
-    flags = {"generic": QD_FLAG_FORCE_GENERIC, "staged": QD_FLAG_MLA_STAGED}.get(variant, 0)
+    splits = {"auto": 0, "split1": 1, "split3": 3, "generic": 0, "staged": 0, "wave": 0}[variant]
+    flags = {"generic": QD_FLAG_FORCE_GENERIC, "staged": QD_FLAG_MLA_STAGED, "wave": QD_FLAG_MLA_WAVE}.get(variant, 0)
     rc = cabi.mla_attend(qa, c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"], out, scale=scale,
                          splits=splits, flags=flags)
     assert rc == 0, cabi.error_string(rc)
@@ -98,7 +99,13 @@ def test_mla_attend_matches_oracle(gpu, name, kw, variant):
 
 def test_mla_attend_kernel_choice(gpu):
     say("mla_attend plan on the device")
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64)
+    assert kind == 3 and groups == 2 and wgs * groups == cus      # pair kernel: 2 groups of 64 heads, 1 per CU
+    kind, wgs, groups = cabi.mla_attend_info(32, 1, 64, 512, 64, 16, 64)
+    assert kind == 3 and groups == 1
+    assert cabi.mla_attend_info(32, 1, 32, 512, 64, 16, 64)[0] == 2   # 32 heads: wave-streamed kernel
+    kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64, flags=QD_FLAG_MLA_WAVE)
     assert kind == 2 and groups == 8 and wgs * groups <= 256      # wave-streamed kernel, 8 head groups
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 20, 512, 64, 64, 64)
     assert kind == 2 and groups == 2 and wgs * groups <= 256      # 2 head groups, the second of 4 heads
@@ -134,15 +141,15 @@ def test_mla_attend_sparse_and_causal(gpu, causal, kernel):
 
 
 @pytest.mark.parametrize("seed", range(1, 9))
-@pytest.mark.parametrize("flags", [0, QD_FLAG_MLA_STAGED], ids=["wave", "staged"])
-def test_mla_attend_bf16_accuracy_over_seeds(gpu, flags, seed):
+@pytest.mark.parametrize("heads,flags", [(16, 0), (16, QD_FLAG_MLA_STAGED), (64, 0)], ids=["wave", "staged", "pair"])
+def test_mla_attend_bf16_accuracy_over_seeds(gpu, heads, flags, seed):
     """Random DeepSeek-shaped inputs with short rows in bf16: with one bf16
     rounding of the softmax weights in the PV product, 3 of these 8 seeds
     landed past the 16-bit bar (worst 1.23x); the kernels carry the weights
     as hi + lo and stay under 0.5x."""
-    say(f"mla_attend bf16 accuracy seed {seed} flags {flags}")
+    say(f"mla_attend bf16 accuracy seed {seed} heads {heads} flags {flags}")
     dtype = torch.bfloat16
-    c = _case(gpu, lengths=[3, 300, 1031, 2500], q_len=1, heads=16, block_size=64, dtype=dtype, seed=seed)
+    c = _case(gpu, lengths=[3, 300, 1031, 2500], q_len=1, heads=heads, block_size=64, dtype=dtype, seed=seed)
     qa = _absorbed(c, dtype).to(dtype).to(gpu)
     scale = default_mla_scale(c["q_nope"].shape[-1], c["q_rope"].shape[-1])
     out = torch.empty_like(qa)
@@ -153,8 +160,8 @@ def test_mla_attend_bf16_accuracy_over_seeds(gpu, flags, seed):
     _close(out, _oracle_attend(c, qa, scale, dtype=dtype), dtype, f"seed {seed}")
 
 
-@pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_STAGED), (16, 0)],
-                         ids=["wave-h64", "staged-h64", "wave-h16"])
+@pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_WAVE), (64, QD_FLAG_MLA_STAGED), (16, 0)],
+                         ids=["pair-h64", "wave-h64", "staged-h64", "wave-h16"])
 def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads, flags):
     """Physical page order and unreferenced cache contents do not change a bit
     of the output (index handling is exact)."""
