@@ -241,7 +241,7 @@ struct MlaParams {
   const int32_t* idx;  // [R, nk] when nk >= 0
   void* out;           // [R, H, Dc]
   float* part;         // VALU kernel: [R, H, splits, Dc + 2] (splits > 1);
-                       // MFMA kernel: [wgs + R, H, Dc + 2] stream-K partials
+                       // MFMA kernel: [wgs + R, H, pst] stream-K partials
   int B, T, H, Dc, Dr, W, P, maxP;
   int nk;  // indices per row, -1 = all tokens (dense)
   int causal, splits;
@@ -250,6 +250,7 @@ struct MlaParams {
   int nht, ds;      // MFMA kernel: head tiles per workgroup, latent slices per head tile
   int wgs;          // MFMA kernel: workgroups per head group (stream-K ranges)
   int* meta;        // MFMA kernel: [rows][2] {first workgroup, workgroups} per row
+  int pst;          // MFMA kernel: floats per partial row {m, l, pad.., acc[Dc]} (acc at pst - Dc)
   int64_t* gtotal;  // MFMA kernel: tiles G of the batch (merge: skips empty ranges)
   int64_t num_blocks;
   float sl2;        // scale * log2(e)
@@ -1477,44 +1478,46 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
 }
 
 // ----------------------------------------------------------------------------
-// Paged latent attention, pair kernel: dense rows, Dc 512, Dr 64, 32*NHB
-// heads per workgroup of four waves (two pairs), cache tiles fed to LDS by
-// DMA
+// Paged latent attention, shared-tile kernel: dense rows, Dc 512, Dr 64,
+// 64 heads per workgroup of four waves, 32-token cache tiles fed to LDS by
+// DMA and shared by all four waves
 // ----------------------------------------------------------------------------
 
-constexpr int kPairThreads = 256;                       // four waves: two pairs
-constexpr int kPairBufs = 7;                            // LDS tile ring
-constexpr int kPairRowBytes = 2 * 576;                  // cache row: 512 latent + 64 rope, 16-bit
-constexpr int kPairLatStride = 1024 + 16;              // LDS bytes per latent row (padded)
-constexpr int kPairLatBytes = 16 * kPairLatStride;      // latent part of a 16-row tile
-constexpr int kPairTileBytes = kPairLatBytes + 2 * 1024;  // + rope rows (8 per KB)
-constexpr int kPairRows = 1024;                         // query rows (prologue arrays in the ring)
-constexpr int kPairListTiles = 1024;                    // tiles of one workgroup's range
-constexpr int kPairDma = 5;                             // DMA instructions per wave per tile
-#ifndef QD_MLA_PAIR_ROW_COST
-#define QD_MLA_PAIR_ROW_COST 8
+constexpr int kShThreads = 256;                         // four waves, 16 heads each
+constexpr int kShTokens = 32;                           // tokens per tile
+constexpr int kShBufs = 4;                              // LDS tile ring
+constexpr int kShRowBytes = 2 * 576;                    // cache row: 512 latent + 64 rope, 16-bit
+constexpr int kShLatStride = 1024 + 16;                 // LDS bytes per latent row (padded)
+constexpr int kShLatBytes = kShTokens * kShLatStride;   // latent part of a tile
+constexpr int kShTileBytes = kShLatBytes + kShTokens * 128;  // + rope rows
+constexpr int kShRows = 1024;                           // query rows (prologue arrays in the ring)
+constexpr int kShListTiles = 512;                       // tiles of one workgroup's range
+constexpr int kShDma = 9;                               // DMA instructions per wave per tile
+constexpr int kShPartialPad = 4;                        // partial row: {m, l, pad, pad, acc[Dc]}
+#ifndef QD_MLA_SHARED_ROW_COST
+#define QD_MLA_SHARED_ROW_COST 4
 #endif
-// Partition cost of a row's start, in tile units: the query load drains the
-// tile pipeline once, and the row's output or partial is stored.
-constexpr int kPairRowCost = QD_MLA_PAIR_ROW_COST;
+// Partition cost of a row's start, in tile units: the row's query load and
+// output stores drain the tile pipeline once.
+constexpr int kShRowCost = QD_MLA_SHARED_ROW_COST;
+#ifndef QD_MLA_SHARED_QK_AHEAD
+#define QD_MLA_SHARED_QK_AHEAD 6
+#endif
 
-template <int NHB>
-__host__ __device__ constexpr size_t mla_pair_lds_bytes() {
-  return static_cast<size_t>(kPairBufs) * kPairTileBytes  // tile ring (prologue arrays before the first tile)
-         + 4 * NHB * 64 * 16                              // score exchange
-         + static_cast<size_t>(kPairListTiles) * 16;      // tile list
+__host__ __device__ constexpr size_t mla_shared_lds_bytes() {
+  return static_cast<size_t>(kShBufs) * kShTileBytes    // tile ring (prologue arrays before the first tile)
+         + static_cast<size_t>(kShListTiles) * 16;      // tile list
 }
 
-// The prologue's arrays fit in the ring, which the first DMA overwrites.
-static_assert(kPairRows * (4 + 4 + 8) + kPairListTiles * 16 <= kPairBufs * kPairTileBytes,
-              "pair kernel prologue arrays exceed the tile ring");
+static_assert(kShRows * (4 + 4 + 8) + kShListTiles * 16 <= kShBufs * kShTileBytes,
+              "shared-tile kernel prologue arrays exceed the tile ring");
 
-// LDS wait for the DMA ring: all but the last kVm vector-memory operations of
-// this wave done (loads into LDS included), this wave's LDS operations done,
-// then the workgroup barrier.  The empty asm statements keep the compiler
-// from moving memory accesses across.
+// Wait for all but the last kVm vector-memory operations of this wave (loads
+// into LDS included) and for its LDS operations, then the workgroup
+// barrier.  The empty asm statements keep the compiler from moving memory
+// accesses across.
 template <int kVm>
-__device__ __forceinline__ void pair_dma_barrier() {
+__device__ __forceinline__ void dma_ring_barrier() {
   static_assert(kVm >= 0 && kVm < 64, "vmcnt is 6 bits");
   constexpr int imm = (kVm & 0xF) | ((kVm >> 4) << 14) | (0x7 << 4) | (0x0 << 8);  // lgkmcnt(0)
   asm volatile("" ::: "memory");
@@ -1523,47 +1526,50 @@ __device__ __forceinline__ void pair_dma_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Stream-K over (query row, 16-token tile) like mla_attend_wave_kernel (same
-// grid mapping, meta, slots and merge kernel), one workgroup per CU with
-// 32*NHB heads and every wave on every tile of the workgroup's range.  Wave
-// v belongs to pair v / 2 (heads 16*NHB*(v/2) .. of the workgroup's) and
-// takes latent half hv = v % 2:
-//   load     each wave DMAs a quarter of the tile's 16 cache rows (latent
-//            rows 4v .. 4v + 3, 1 KB per instruction, and their rope bytes)
-//            into one of kPairBufs LDS buffers (global_load_lds),
-//            kPairBufs - 1 tiles ahead; no registers hold tiles in flight.
-//            Latent rows are 1 KB apart plus 16 bytes (each instruction has
-//            its own LDS base), so the operand reads below meet no LDS bank
-//            conflict and take immediate offsets from one lane address; rope
-//            chunk c of row R sits at c ^ (R/2 % 8).  Rows past the tile's
-//            visible count re-read its last visible row and get weight 0.
-//   QK       wave hv takes the 9 chunks 9 hv .. 9 hv + 8 of the 18
-//            32-element chunks of [latent | rope]: S^T partial = K chunk x
-//            [q | q_rope] chunk for its pair's NHB blocks of 16 heads (query
-//            in registers, loaded when a row segment starts); the two
-//            partial scores of a pair meet through LDS and both waves add
-//            them (the same sum in both: IEEE addition commutes).
-//   softmax  fp32 with the lazy reference max of the wave kernel; both
-//            waves of a pair compute the same weights.
-//   PV       wave hv: latent columns 256 hv .. +255 for its pair's heads
-//            (A = C^T from 4 LDS rows, 8x8 byte-permute transposes, as in the
-//            wave kernel; one A feeds NHB head blocks).
-// At the end of a row segment each wave stores its half of the columns:
-// the output (whole row) or the partial {m, l, acc} in slot (w + row).
+// vmcnt(0) alone (expcnt and lgkmcnt left free).
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
+
+// Stream-K over (query row, 32-token tile) like mla_attend_wave_kernel (same
+// grid mapping, meta and merge kernel; partial rows padded to Dc + 4 floats
+// so their stores are 16-byte), one workgroup per CU with 64 heads, every
+// wave on every tile of the workgroup's range.  Wave v serves heads
+// 16 v .. 16 v + 15 of the workgroup's:
+//   load     each wave DMAs a quarter of the tile's 32 cache rows (latent
+//            rows 8v .. 8v + 7, 1 KB per instruction, and their rope bytes)
+//            into one of kShBufs LDS buffers (global_load_lds), kShBufs - 1
+//            tiles ahead; no registers hold tiles in flight.  Latent rows are
+//            1 KB apart plus 16 bytes (each instruction has its own LDS
+//            base), so the operand reads meet no LDS bank conflict and take
+//            immediate offsets from one lane address; rope chunk c of row R
+//            sits at c ^ (R/2 % 8).  Rows past the tile's visible count
+//            re-read its last visible row and get weight 0.
+//   QK       per 16-row block of the tile: S^T = K chunk x [q | q_rope]
+//            chunk over the 18 32-element chunks (query in registers, loaded
+//            when a row segment starts).
+//   softmax  fp32 over the tile's 32 tokens, with the lazy reference max of
+//            the wave kernel.
+//   PV       16x16x16 per row block with A = C^T from 4 LDS rows (8x8
+//            byte-permute transposes, as in the wave kernel); bf16 weights
+//            as hi + lo in one 16x16x32.
+// No per-tile exchange between waves: one barrier per tile, for the ring.
+// At the end of a row segment each wave stores its heads: the output (whole
+// row) or the partial {m, l, acc} in slot (w + row); the next row's query is
+// loaded there too, and one wait for every load in flight covers both (the
+// stores would otherwise hold the tile waits behind them).
 // NT: nontemporal cache loads (one head group); with several head groups
 // the tiles stay in L2 for the other groups' workgroups on the XCD.
-template <int DT, int NHB, bool NT>
-__global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams p) {
+template <int DT, bool NT>
+__global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams p) {
   using E = Elem<DT>;
   using Ops = MfmaOps<DT>;
   using S = typename E::S;
   constexpr int kDc = 512;
   constexpr int kW = 576;
+  constexpr int kPst = kDc + kShPartialPad;
   extern __shared__ __align__(16) char smem[];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hv = wv & 1;
   const int r16 = lane & 15, q4 = lane >> 4;
 
   const int L = blockIdx.x;
@@ -1572,28 +1578,28 @@ __global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams
   if (w >= p.wgs) return;  // whole workgroup: uniform
 
   char* ring = smem;
-  f32x4* xch = reinterpret_cast<f32x4*>(smem + kPairBufs * kPairTileBytes);            // [4][NHB][64]
-  i32x4* ctl = reinterpret_cast<i32x4*>(smem + kPairBufs * kPairTileBytes + 4 * NHB * 64 * 16);
+  i32x4* ctl = reinterpret_cast<i32x4*>(smem + kShBufs * kShTileBytes);
   // Prologue arrays, inside the ring.
-  int* rt = reinterpret_cast<int*>(ring);                 // [rows] tiles
-  int* re = rt + kPairRows;                               // [rows] visible end
-  int64_t* incl = reinterpret_cast<int64_t*>(re + kPairRows);  // [rows] prefix of costs
-  i32x4* tl = reinterpret_cast<i32x4*>(incl + kPairRows);    // [positions]
+  int* rt = reinterpret_cast<int*>(ring);                      // [rows] tiles
+  int* re = rt + kShRows;                                      // [rows] visible end
+  int64_t* incl = reinterpret_cast<int64_t*>(re + kShRows);   // [rows] prefix of costs
+  i32x4* tl = reinterpret_cast<i32x4*>(incl + kShRows);       // [positions]
+  int* nreal = reinterpret_cast<int*>(tl + kShListTiles);     // real tiles of the range
 
-  const int rows = p.B * p.T;  // <= kPairRows (host check)
-  constexpr int kHeads = 32 * NHB;   // per workgroup
+  const int rows = p.B * p.T;  // <= kShRows (host check)
+  constexpr int kHeads = 64;   // per workgroup
   const int h0 = kHeads * hg;
-  const int hp = h0 + 16 * NHB * (wv >> 1);  // this pair's first head
+  const int h = h0 + 16 * wv + r16;  // this lane's head
   const char* cache = static_cast<const char*>(p.cache);
 
   // --- Prologue -----------------------------------------------------------
-  for (int r = tid; r < rows; r += kPairThreads) {
+  for (int r = tid; r < rows; r += kShThreads) {
     const int end = row_end(p, r / p.T, r);
     re[r] = end;
-    rt[r] = (end + kSubTokens - 1) / kSubTokens;
+    rt[r] = (end + kShTokens - 1) / kShTokens;
   }
   __syncthreads();
-  auto row_cost = [&](int tiles) { return tiles > 0 ? tiles + kPairRowCost : 0; };
+  auto row_cost = [&](int tiles) { return tiles > 0 ? tiles + kShRowCost : 0; };
   if (wv == 0) {
     int64_t carry = 0;
     for (int base = 0; base < rows; base += 64) {
@@ -1608,13 +1614,13 @@ __global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams
   const int64_t G = incl[rows - 1];
   const int64_t g0 = static_cast<int64_t>(w) * G / p.wgs;
   const int64_t g1 = static_cast<int64_t>(w + 1) * G / p.wgs;
-  const int npos = static_cast<int>(g1 - g0);  // <= kPairListTiles (host check)
+  const int npos = static_cast<int>(g1 - g0);  // <= kShListTiles (host check)
   if (w == 0 && hg == 0 && tid == 0) *p.gtotal = G;
   auto wg_of = [&](int64_t x) { return static_cast<int>(((x + 1) * p.wgs - 1) / G); };
-  // Positions of this range: the first kPairRowCost positions of a row hold
-  // no tile (row -1); the others tile i of the row: element offset of its
-  // first cache row, visible rows | whole-row flag << 16, row.
-  for (int t = tid; t < npos; t += kPairThreads) {
+  // Positions of this range: the first kShRowCost positions of a row hold no
+  // tile (row -1); the others tile i of the row: element offset of its first
+  // cache row, visible rows | whole-row flag << 16, row.
+  for (int t = tid; t < npos; t += kShThreads) {
     const int64_t g = g0 + t;
     int lo = 0, hi = rows - 1;
     while (lo < hi) {
@@ -1628,15 +1634,15 @@ __global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams
       tl[t] = i32x4{0, 0, 0, -1};
       continue;
     }
-    const int tok0 = kSubTokens * tir;
-    const int pg = tok0 / p.P;
+    const int tok0 = kShTokens * tir;
+    const int pg = tok0 / p.P;  // the tile lies in one page (P % 32 == 0)
     int32_t phys = p.table[static_cast<int64_t>(r / p.T) * p.maxP + pg];
     if (phys < 0) phys = 0;
     if (phys >= p.num_blocks) phys = static_cast<int32_t>(p.num_blocks - 1);
     const int64_t base = (static_cast<int64_t>(phys) * p.P + (tok0 - pg * p.P)) * kW;
     const int whole = (first >= g0 && incl[r] <= g1) ? 1 : 0;
     tl[t] = i32x4{static_cast<int>(base & 0xFFFFFFFF), static_cast<int>(base >> 32),
-                  min(kSubTokens, re[r] - tok0) | (whole << 16), r};
+                  min(kShTokens, re[r] - tok0) | (whole << 16), r};
     if (tir == 0 && hg == 0) {
       // This workgroup holds the row's first tile: record its span.
       p.meta[2 * r] = w;
@@ -1646,10 +1652,10 @@ __global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams
   // Rows with no tile: zeros from workgroup (row % wgs), meta {0, 0}.
   for (int r = w; r < rows; r += p.wgs) {
     if (rt[r] != 0) continue;
-    for (int i = tid; i < kHeads * kDc / 8; i += kPairThreads) {
-      const int h = h0 + i / (kDc / 8);
-      if (h < p.H)
-        *reinterpret_cast<u32x4*>(static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * kDc +
+    for (int i = tid; i < kHeads * kDc / 8; i += kShThreads) {
+      const int hh = h0 + i / (kDc / 8);
+      if (hh < p.H)
+        *reinterpret_cast<u32x4*>(static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + hh) * kDc +
                                   8 * (i % (kDc / 8))) = u32x4{0u, 0u, 0u, 0u};
     }
     if (hg == 0 && tid == 0) {
@@ -1658,7 +1664,7 @@ __global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams
     }
   }
   __syncthreads();
-  // Compact the tiles (wave 0); their count goes through the exchange area.
+  // Compact the tiles (wave 0).
   if (wv == 0) {
     int count = 0;
     for (int base = 0; base < npos; base += 64) {
@@ -1670,265 +1676,245 @@ __global__ __launch_bounds__(kPairThreads) void mla_attend_pair_kernel(MlaParams
       if (real) ctl[count + before] = e;
       count += __popcll(bal);
     }
-    if (lane == 0) reinterpret_cast<int*>(xch)[0] = count;
+    if (lane == 0) *nreal = count;
   }
   __syncthreads();
-  const int n = reinterpret_cast<const int*>(xch)[0];
+  const int n = *nreal;
+  __syncthreads();  // every wave has read the count before the ring is written
   if (n == 0) return;  // whole workgroup: uniform
 
   // --- Main loop ------------------------------------------------------------
-  // The rest is instantiated per latent half (wave-uniform hv), so every
-  // chunk and column index is a compile-time constant.
-  auto body = [&](auto half) {
-    constexpr int HV = decltype(half)::value;
-    // DMA of tile t (past the end: a re-read of the cache's first row into
-    // the unused slot, so every step issues the same loads).
-    auto dma = [&](int t) {
-      char* slot = ring + (t % kPairBufs) * kPairTileBytes;
-      int64_t base = 0;
-      int nv = 1;
-      if (t < n) {
-        const i32x4 e = ctl[t];
-        base = static_cast<int64_t>(static_cast<uint32_t>(e[0])) | (static_cast<int64_t>(e[1]) << 32);
-        nv = e[2] & 0xFFFF;
-      }
-      const char* tb = cache + 2 * base;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int R = 4 * wv + k;
-        const int Rc = R < nv ? R : nv - 1;
-        const char* src = tb + Rc * kPairRowBytes + 16 * lane;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                         (__attribute__((address_space(3))) void*)(slot + R * kPairLatStride), 16,
-                                         0, NT ? 2 : 0);
-      }
-      // Rope bytes of the same 4 rows: 32 lanes, 512 bytes.
-      if (lane < 32) {
-        const int R = 4 * wv + (lane >> 3);
-        const int Rc = R < nv ? R : nv - 1;
-        const int c = (lane & 7) ^ ((R >> 1) & 7);
-        const char* src = tb + Rc * kPairRowBytes + 2 * kDc + 16 * c;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                         (__attribute__((address_space(3))) void*)(slot + kPairLatBytes + wv * 512),
-                                         16, 0, NT ? 2 : 0);
-      }
-    };
-    // Query chunks 9 HV .. 9 HV + 8 of this pair's heads for row r.  Heads
-    // past H read head 0's query (never stored; no select on the loaded
-    // values, which would wait for every load in flight).
-    u32x4 qv[NHB][9];
-    auto load_q = [&](int r) {
-#pragma unroll
-      for (int j = 0; j < NHB; ++j) {
-        const int h = hp + 16 * j + r16;
-        const int64_t hr = static_cast<int64_t>(r) * p.H + (h < p.H ? h : 0);
-        const char* qrow = static_cast<const char*>(p.q) + hr * kDc * 2;
-        const char* rrow = static_cast<const char*>(p.qr) + hr * (kW - kDc) * 2;
-#pragma unroll
-        for (int k = 0; k < 9; ++k) {
-          const int c = 9 * HV + k;
-          qv[j][k] = c < 16 ? *reinterpret_cast<const u32x4*>(qrow + (32 * c + 8 * q4) * 2)
-                            : *reinterpret_cast<const u32x4*>(rrow + (32 * (c - 16) + 8 * q4) * 2);
-        }
-      }
-    };
-
-    float m_run[NHB], l_run[NHB];
-    f32x4 acc[NHB][2][8];
-    auto reset = [&]() {
-#pragma unroll
-      for (int j = 0; j < NHB; ++j) {
-        m_run[j] = -INFINITY;
-        l_run[j] = 0.f;
-#pragma unroll
-        for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[j][b2][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    };
-
-#pragma unroll
-    for (int t = 0; t < kPairBufs - 1; ++t) dma(t);
-    // The first query completes here (with the first tiles), so no register
-    // load is pending when the loop starts (see the wait after the next
-    // row's query below).
-    load_q(ctl[0][3]);
-    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0)
-    int row = -1;
-    for (int t = 0; t < n; ++t) {
-      pair_dma_barrier<(kPairBufs - 2) * kPairDma>();  // tile t in LDS; tile t-1 done by both waves
-      dma(t + kPairBufs - 1);
+  // DMA of tile t (past the end: a re-read of the cache's first row into the
+  // unused slot, so every step issues the same loads).
+  auto dma = [&](int t) {
+    char* slot = ring + (t % kShBufs) * kShTileBytes;
+    int64_t base = 0;
+    int nv = 1;
+    if (t < n) {
       const i32x4 e = ctl[t];
-      const int nv = e[2] & 0xFFFF;
-      const bool whole = (e[2] >> 16) != 0;
-      const int r = e[3];
-      const bool last = t + 1 == n || ctl[t + 1][3] != r;
-      if (r != row) {
-        row = r;
-        reset();
-      }
-      const char* slot = ring + (t % kPairBufs) * kPairTileBytes;
+      base = static_cast<int64_t>(static_cast<uint32_t>(e[0])) | (static_cast<int64_t>(e[1]) << 32);
+      nv = e[2] & 0xFFFF;
+    }
+    const char* tb = cache + 2 * base;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int R = 8 * wv + k;
+      const int Rc = R < nv ? R : nv - 1;
+      const char* src = tb + Rc * kShRowBytes + 16 * lane;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(slot + R * kShLatStride), 16, 0,
+                                       NT ? 2 : 0);
+    }
+    {
+      const int R = 8 * wv + (lane >> 3);
+      const int Rc = R < nv ? R : nv - 1;
+      const int c = (lane & 7) ^ ((R >> 1) & 7);
+      const char* src = tb + Rc * kShRowBytes + 2 * kDc + 16 * c;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(slot + kShLatBytes + wv * 1024), 16,
+                                       0, NT ? 2 : 0);
+    }
+  };
+  // This lane's head's query, 18 chunks of 32 elements ([q | q_rope]).
+  // Heads past H read head 0's query (never stored; no select on the loaded
+  // values, which would wait for every load in flight).
+  u32x4 qv[18];
+  auto load_q = [&](int r) {
+    const int64_t hr = static_cast<int64_t>(r) * p.H + (h < p.H ? h : 0);
+    const char* qrow = static_cast<const char*>(p.q) + hr * kDc * 2;
+    const char* rrow = static_cast<const char*>(p.qr) + hr * (kW - kDc) * 2;
+#pragma unroll
+    for (int c = 0; c < 18; ++c)
+      qv[c] = c < 16 ? *reinterpret_cast<const u32x4*>(qrow + (32 * c + 8 * q4) * 2)
+                     : *reinterpret_cast<const u32x4*>(rrow + (32 * (c - 16) + 8 * q4) * 2);
+  };
 
-      // QK partial over this wave's 9 chunks, operands read kAhead chunks
-      // before their MFMAs; the scheduling barriers keep that distance (left
-      // free, the scheduler sinks each read next to its MFMA).
-      const char* lat = slot + r16 * kPairLatStride + 16 * q4;
-      const char* rop = slot + kPairLatBytes + r16 * 128;
-      auto a_chunk = [&](int k) {
-        const int c = 9 * HV + k;
-        if (c < 16) return *reinterpret_cast<const u32x4*>(lat + 64 * c);
-        return *reinterpret_cast<const u32x4*>(rop + 16 * ((4 * (c - 16) + q4) ^ ((r16 >> 1) & 7)));
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 acc[4][8];
+  auto reset = [&]() {
+    m_run = -INFINITY;
+    l_run = 0.f;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[bb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  // The first tiles in flight and the first query, waited for here so that
+  // no register load is pending when the loop starts (the compiler would
+  // otherwise wait for every load in flight, the whole ring, in every step).
+#pragma unroll
+  for (int t = 0; t < kShBufs - 1; ++t) dma(t);
+  load_q(ctl[0][3]);
+  wait_vm_all();
+  int row = -1;
+  for (int t = 0; t < n; ++t) {
+    dma_ring_barrier<(kShBufs - 2) * kShDma>();  // tile t in LDS; tile t-1 done by every wave
+    dma(t + kShBufs - 1);                         // into tile t-1's slot
+    const i32x4 e = ctl[t];
+    const int nv = e[2] & 0xFFFF;
+    const bool whole = (e[2] >> 16) != 0;
+    const int r = e[3];
+    const int r1 = t + 1 < n ? ctl[t + 1][3] : -1;
+    const bool last = r1 != r;
+    if (r != row) {
+      row = r;
+      reset();
+    }
+    const char* slot = ring + (t % kShBufs) * kShTileBytes;
+
+    // QK for both 16-row blocks together (two MFMAs per chunk, one per
+    // block), operands read kAhead chunks ahead: one chunk's MFMAs take 32
+    // cycles, an LDS read under this load well over 100.  The scheduling
+    // barriers keep that distance (left free, the scheduler sinks each read
+    // next to its MFMA).
+    f32x4 s[2];
+    {
+      const char* lat = slot + r16 * kShLatStride + 16 * q4;
+      const char* rop = slot + kShLatBytes + r16 * 128;
+      auto a_chunk = [&](int c, int tb) {
+        if (c < 16) return *reinterpret_cast<const u32x4*>(lat + 16 * kShLatStride * tb + 64 * c);
+        return *reinterpret_cast<const u32x4*>(rop + 16 * 128 * tb + 16 * ((4 * (c - 16) + q4) ^ ((r16 >> 1) & 7)));
       };
-      constexpr int kAhead = 4;
-      u32x4 a[kAhead];
+      constexpr int kAhead = QD_MLA_SHARED_QK_AHEAD;
+      u32x4 a[kAhead][2];
 #pragma unroll
-      for (int k = 0; k < kAhead; ++k) a[k] = a_chunk(k);
+      for (int c = 0; c < kAhead; ++c) {
+        a[c][0] = a_chunk(c, 0);
+        a[c][1] = a_chunk(c, 1);
+      }
       __builtin_amdgcn_sched_barrier(0);
-      f32x4 s[NHB], s2[NHB];
+      s[0] = s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < NHB; ++j) s[j] = s2[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k = 0; k < 9; ++k) {
-        const u32x4 ak = a[k % kAhead];
-        if (k + kAhead < 9) a[k % kAhead] = a_chunk(k + kAhead);
-#pragma unroll
-        for (int j = 0; j < NHB; ++j) {
-          if (k & 1)
-            s2[j] = Ops::mma32(ak, qv[j][k], s2[j]);
-          else
-            s[j] = Ops::mma32(ak, qv[j][k], s[j]);
+      for (int c = 0; c < 18; ++c) {
+        const u32x4 a0 = a[c % kAhead][0], a1 = a[c % kAhead][1];
+        if (c + kAhead < 18) {
+          a[c % kAhead][0] = a_chunk(c + kAhead, 0);
+          a[c % kAhead][1] = a_chunk(c + kAhead, 1);
         }
+        s[0] = Ops::mma32(a0, qv[c], s[0]);
+        s[1] = Ops::mma32(a1, qv[c], s[1]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // The next row's query, once this row's last scores are issued.  The
-      // explicit wait keeps the load from being pending at the loop's back
-      // edge: the compiler would otherwise wait for every load in flight
-      // (the whole DMA ring) before the QK of every tile.
-      if (last && t + 1 < n) {
-        load_q(ctl[t + 1][3]);
-        __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0), expcnt and lgkmcnt free
-      }
-#pragma unroll
-      for (int j = 0; j < NHB; ++j) {
-        s[j] += s2[j];
-        xch[(wv * NHB + j) * 64 + lane] = s[j];
-      }
-      lds_barrier();  // the partner's partial scores
-#pragma unroll
-      for (int j = 0; j < NHB; ++j) s[j] += xch[((wv ^ 1) * NHB + j) * 64 + lane];
+    }
 
-      // PV operands (tokens 4 q4 + i, columns 256 HV + 128 b2 + 8 r16 ..).
-      const char* pv0 = slot + 4 * q4 * kPairLatStride + 256 * (2 * HV) + 16 * r16;
-      u32x4 raw[2][4];
+    // Softmax over the tile's 32 tokens: lane holds tokens 16 tb + 4 q4 + i.
+    float x[2][4];
 #pragma unroll
-      for (int b2 = 0; b2 < 2; ++b2)
+    for (int tb = 0; tb < 2; ++tb) {
+      const f32x4 st = s[tb];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          raw[b2][i] = *reinterpret_cast<const u32x4*>(pv0 + i * kPairLatStride + 256 * b2);
-
-      // Softmax per head block (lazy reference max, as the wave kernel).
-      u32x4 pbl[NHB];
-      u32x2 pb[NHB];
+      for (int i = 0; i < 4; ++i) x[tb][i] = 16 * tb + 4 * q4 + i < nv ? st[i] * p.sl2 : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                     fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+    mx = max_over_lane_groups(mx);
+    if (__ballot(mx > m_run + kWaveLazyLog2)) {
+      const float mn = fmaxf(m_run, mx);
+      const float alpha = mn == m_run ? 1.f : fast_exp2(m_run - mn);  // m_run = -inf: 0
+      m_run = mn;
+      l_run *= alpha;
 #pragma unroll
-      for (int j = 0; j < NHB; ++j) {
-        float x[4];
+      for (int bb = 0; bb < 4; ++bb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = 4 * q4 + i < nv ? s[j][i] * p.sl2 : -INFINITY;
-        float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-        mx = max_over_lane_groups(mx);
-        const bool move = mx > m_run[j] + kWaveLazyLog2;
-        if (__ballot(move)) {
-          const float mn = fmaxf(m_run[j], mx);
-          const float alpha = mn == m_run[j] ? 1.f : fast_exp2(m_run[j] - mn);  // m_run = -inf: 0
-          m_run[j] = mn;
-          l_run[j] *= alpha;
+        for (int ee = 0; ee < 8; ++ee) acc[bb][ee] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    u32x4 pbl[2];
+    u32x2 pb[2];
 #pragma unroll
-          for (int b2 = 0; b2 < 2; ++b2)
+    for (int tb = 0; tb < 2; ++tb) {
+      float pr[4];
 #pragma unroll
-            for (int ee = 0; ee < 8; ++ee) acc[j][b2][ee] *= alpha;
-        }
-        const float m_use = m_run[j] == -INFINITY ? 0.f : m_run[j];
-        float pr[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[i] - m_use);
-        pb[j] = u32x2{Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
-        pbl[j] = u32x4{pb[j][0], pb[j][1], 0u, 0u};
-        if constexpr (Ops::kSplitWeights) {
-          pbl[j][2] = Ops::rest2(pr[0], pr[1], pb[j][0]);
-          pbl[j][3] = Ops::rest2(pr[2], pr[3], pb[j][1]);
-          l_run[j] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-        } else {
-          l_run[j] += Ops::sum2(pb[j][0]) + Ops::sum2(pb[j][1]);
-        }
-      }
-
-      // PV: C tile (b2, ee) row m <-> latent column 256 HV + 128 b2 + 8 m + ee.
-#pragma unroll
-      for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-        for (int ee = 0; ee < 8; ++ee) {
-          const int wd = ee >> 1;
-          const uint32_t sel = (ee & 1) ? 0x07060302u : 0x05040100u;
-          const u32x2 av = {__builtin_amdgcn_perm(raw[b2][1][wd], raw[b2][0][wd], sel),
-                            __builtin_amdgcn_perm(raw[b2][3][wd], raw[b2][2][wd], sel)};
-#pragma unroll
-          for (int j = 0; j < NHB; ++j) {
-            if constexpr (Ops::kSplitWeights)
-              acc[j][b2][ee] = Ops::mma32(u32x4{av[0], av[1], av[0], av[1]}, pbl[j], acc[j][b2][ee]);
-            else
-              acc[j][b2][ee] = Ops::pv(av, pb[j], acc[j][b2][ee]);
-          }
-        }
-
-      if (last) {
-        // This wave's columns 256 HV .. +255 of the row segment.
-#pragma unroll
-        for (int j = 0; j < NHB; ++j) {
-          const int h = hp + 16 * j + r16;
-          const float Lt = sum_over_lane_groups(l_run[j]);
-          if (h >= p.H) continue;
-          if (whole) {
-            const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
-            S* orow = static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * kDc;
-#pragma unroll
-            for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                uint32_t wd[4];
-#pragma unroll
-                for (int ee = 0; ee < 8; ee += 2)
-                  wd[ee / 2] = Ops::pack2(acc[j][b2][ee][i] * inv, acc[j][b2][ee + 1][i] * inv);
-                *reinterpret_cast<u32x4*>(orow + 128 * (2 * HV + b2) + 32 * q4 + 8 * i) =
-                    u32x4{wd[0], wd[1], wd[2], wd[3]};
-              }
-          } else {
-            float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kDc + 2);
-            if (HV == 0 && q4 == 0) {
-              pr[0] = m_run[j] == -INFINITY ? -INFINITY : m_run[j] * kLn2;
-              pr[1] = Lt;
-            }
-            // Rows are Dc+2 floats: the accumulator starts 8 bytes in.
-#pragma unroll
-            for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int ee = 0; ee < 8; ee += 2)
-                  *reinterpret_cast<f32x2*>(pr + 2 + 128 * (2 * HV + b2) + 32 * q4 + 8 * i + ee) =
-                      f32x2{acc[j][b2][ee][i], acc[j][b2][ee + 1][i]};
-          }
-        }
+      for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[tb][i] - m_use);
+      pb[tb] = u32x2{Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
+      pbl[tb] = u32x4{pb[tb][0], pb[tb][1], 0u, 0u};
+      if constexpr (Ops::kSplitWeights) {
+        pbl[tb][2] = Ops::rest2(pr[0], pr[1], pb[tb][0]);
+        pbl[tb][3] = Ops::rest2(pr[2], pr[3], pb[tb][1]);
+        l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      } else {
+        l_run += Ops::sum2(pb[tb][0]) + Ops::sum2(pb[tb][1]);
       }
     }
-    // Drain the placeholder loads before the workgroup's LDS is released.
-    __builtin_amdgcn_s_waitcnt(0);
-  };
-  if (hv == 0)
-    body(std::integral_constant<int, 0>{});
-  else
-    body(std::integral_constant<int, 1>{});
+
+    // PV: one 16x16x32 per (bb, ee) over the tile's 32 tokens: k = 8 q4 + e
+    // is token 4 q4 + e of row block 0 for e < 4 and of row block 1 for
+    // e >= 4, in A (4 rows of each block from LDS, 8x8 byte-permute
+    // transposes) and in B (the lane's own weights); bf16 adds the lo
+    // weights with a second MFMA on the same A.  C tile (bb, ee) row m <->
+    // latent column 128 bb + 8 m + ee.  The next column block's rows are
+    // read while this block multiplies.
+    const u32x4 bhi = {pb[0][0], pb[0][1], pb[1][0], pb[1][1]};
+    const u32x4 blo = {pbl[0][2], pbl[0][3], pbl[1][2], pbl[1][3]};
+    const char* pv0 = slot + 4 * q4 * kShLatStride + 16 * r16;
+    u32x4 rw[2][2][4];  // [column block parity][row block][row]
+    auto load_rows = [&](u32x4 (&dst)[2][4], int bb) {
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dst[tb][i] = *reinterpret_cast<const u32x4*>(pv0 + (16 * tb + i) * kShLatStride + 256 * bb);
+    };
+    load_rows(rw[0], 0);
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      if (bb + 1 < 4) load_rows(rw[(bb + 1) & 1], bb + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 (&cur)[2][4] = rw[bb & 1];
+#pragma unroll
+      for (int ee = 0; ee < 8; ++ee) {
+        const int wd = ee >> 1;
+        const uint32_t sel = (ee & 1) ? 0x07060302u : 0x05040100u;
+        const u32x4 av = {__builtin_amdgcn_perm(cur[0][1][wd], cur[0][0][wd], sel),
+                          __builtin_amdgcn_perm(cur[0][3][wd], cur[0][2][wd], sel),
+                          __builtin_amdgcn_perm(cur[1][1][wd], cur[1][0][wd], sel),
+                          __builtin_amdgcn_perm(cur[1][3][wd], cur[1][2][wd], sel)};
+        acc[bb][ee] = Ops::mma32(av, bhi, acc[bb][ee]);
+        if constexpr (Ops::kSplitWeights) acc[bb][ee] = Ops::mma32(av, blo, acc[bb][ee]);
+      }
+    }
+
+    if (last) {
+      // This wave's heads for the row segment, then the next row's query;
+      // one wait covers the stores, the query and the tiles in flight.
+      const float Lt = sum_over_lane_groups(l_run);
+      if (h < p.H) {
+        if (whole) {
+          const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+          S* orow = static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * kDc;
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              uint32_t wd[4];
+#pragma unroll
+              for (int ee = 0; ee < 8; ee += 2)
+                wd[ee / 2] = Ops::pack2(acc[bb][ee][i] * inv, acc[bb][ee + 1][i] * inv);
+              *reinterpret_cast<u32x4*>(orow + 128 * bb + 32 * q4 + 8 * i) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+            }
+        } else {
+          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kPst);
+          if (q4 == 0) *reinterpret_cast<f32x2*>(pr) = f32x2{m_run == -INFINITY ? -INFINITY : m_run * kLn2, Lt};
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float* d = pr + kShPartialPad + 128 * bb + 32 * q4 + 8 * i;
+              *reinterpret_cast<f32x4*>(d) = f32x4{acc[bb][0][i], acc[bb][1][i], acc[bb][2][i], acc[bb][3][i]};
+              *reinterpret_cast<f32x4*>(d + 4) = f32x4{acc[bb][4][i], acc[bb][5][i], acc[bb][6][i], acc[bb][7][i]};
+            }
+        }
+      }
+      if (t + 1 < n) load_q(r1);
+      wait_vm_all();
+    }
+  }
+  // Drain the placeholder loads before the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
+// ----------------------------------------------------------------------------
 // Merge of the stream-K partials: one wave per (row, head) of a row split
 // across workgroups (meta[row] = {first, count >= 2}); the partial of
 // workgroup k is in slot k + row, for the k in [first, first + count) whose
@@ -1951,8 +1937,9 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
   const int first = p.meta[2 * r], nwg = p.meta[2 * r + 1];
   if (nwg < 2 || first < 0 || first + nwg > p.wgs) return;  // spans are always inside [0, wgs)
   const int64_t G = *p.gtotal;
-  const int64_t stride = static_cast<int64_t>(p.H) * (p.Dc + 2);
-  const float* base = p.part + (r * p.H + h) * static_cast<int64_t>(p.Dc + 2);  // slot k: + (k) * stride
+  const int64_t stride = static_cast<int64_t>(p.H) * p.pst;
+  const float* base = p.part + (r * p.H + h) * static_cast<int64_t>(p.pst);  // slot k: + (k) * stride
+  const int aoff = p.pst - p.Dc;                                             // accumulator offset
   auto present = [&](int k) {
     return static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
   };
@@ -1976,7 +1963,7 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
 #pragma unroll
         for (int j = 0; j < kAcc; ++j) {
           const int d = lane + 64 * j;
-          if (d < p.Dc) v[t][j] = pr[2 + d];
+          if (d < p.Dc) v[t][j] = pr[aoff + d];
         }
       }
     }
@@ -2202,7 +2189,7 @@ struct AttendPlan {
   size_t lds;
   int splits;  // VALU kernel
   bool wave;   // MFMA path through mla_attend_wave_kernel
-  bool pair;   // MFMA path through mla_attend_pair_kernel
+  bool shared;  // MFMA path through mla_attend_shared_kernel
 };
 
 // Smallest instantiated DMA-chunk count covering ceil(W/64), 0 if none.
@@ -2246,25 +2233,26 @@ AttendPlan plan_attend(const AttendShape& a, int forced, int flags) {
     const int64_t gmax =
         rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens + kWaveRowCost);
     const size_t wlds = mla_wave_lds_bytes(4, 2);
-    // The pair kernel: the same dense shapes with 64 heads or more, 64 heads
-    // per workgroup of four waves, one workgroup per CU.
-    const size_t plds = mla_pair_lds_bytes<2>();
+    // The shared-tile kernel: the same dense shapes with 64 heads or more
+    // and pages of whole 32-token tiles, 64 heads per workgroup of four
+    // waves, one workgroup per CU.
+    const size_t slds = mla_shared_lds_bytes();
     const bool dense512 = a.Dc == 512 && a.Dr == 64 && a.nk < 0 && a.P % kSubTokens == 0;
-    if ((flags & (QD_FLAG_MLA_STAGED | QD_FLAG_MLA_WAVE)) == 0 && dense512 && a.H >= 64 && rows <= kPairRows &&
-        plds <= static_cast<size_t>(device_max_lds())) {
+    if ((flags & (QD_FLAG_MLA_STAGED | QD_FLAG_MLA_WAVE)) == 0 && dense512 && a.P % kShTokens == 0 && a.H >= 64 &&
+        rows <= kShRows && slds <= static_cast<size_t>(device_max_lds())) {
       const int groups = (a.H + 63) / 64;
       const int wgs = forced > 0 ? forced : std::max(1, device_cus() / groups);
-      const int64_t pmax =
-          rows * ((static_cast<int64_t>(a.maxP) * a.P + kSubTokens - 1) / kSubTokens + kPairRowCost);
-      if ((pmax + wgs - 1) / wgs + 1 <= kPairListTiles) {
-        pl.pair = true;
+      const int64_t smax =
+          rows * ((static_cast<int64_t>(a.maxP) * a.P + kShTokens - 1) / kShTokens + kShRowCost);
+      if ((smax + wgs - 1) / wgs + 1 <= kShListTiles) {
+        pl.shared = true;
         pl.nht = 1;
         pl.head_groups = groups;
         pl.wgs = wgs;
-        pl.lds = plds;
+        pl.lds = slds;
       }
     }
-    if (!pl.pair && (flags & QD_FLAG_MLA_STAGED) == 0 && dense512 && rows <= kWaveRows &&
+    if (!pl.shared && (flags & QD_FLAG_MLA_STAGED) == 0 && dense512 && rows <= kWaveRows &&
         wlds <= static_cast<size_t>(device_max_lds())) {
       const int groups = ht;
       const int wgs = forced > 0 ? forced : std::max(1, device_cus() / groups);
@@ -2296,10 +2284,14 @@ size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
 // Workspace of the attention: VALU kernel [R, H, splits, Dc+2] fp32 when
 // splits > 1; MFMA kernel [wgs + R, H, Dc+2] fp32 partials, then the tile
 // count G (int64) and [R][2] int32 row spans.
+// Floats per stream-K partial row: {m, l, acc[Dc]}, or {m, l, pad, pad,
+// acc[Dc]} for the shared-tile kernel (16-byte accumulator stores).
+int partial_stride(const AttendShape& a, const AttendPlan& pl) { return a.Dc + (pl.shared ? kShPartialPad : 2); }
+
 size_t attend_partial_bytes(const AttendShape& a, const AttendPlan& pl) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
   if (pl.mfma)
-    return round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * (a.Dc + 2) * sizeof(float)) +
+    return round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * partial_stride(a, pl) * sizeof(float)) +
            round_up256(sizeof(int64_t) + static_cast<size_t>(rows) * 2 * sizeof(int));
   if (pl.splits <= 1) return 0;
   return static_cast<size_t>(rows) * a.H * pl.splits * (a.Dc + 2) * sizeof(float);
@@ -2334,16 +2326,16 @@ hipError_t launch_attend_wave(const MlaParams& prm, const AttendPlan& pl, int64_
 }
 
 template <int DT, bool NT>
-hipError_t launch_attend_pair(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
-  auto fn = mla_attend_pair_kernel<DT, 2, NT>;
+hipError_t launch_attend_shared(const MlaParams& prm, const AttendPlan& pl, int64_t grid, hipStream_t st) {
+  auto fn = mla_attend_shared_kernel<DT, NT>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&] {
     attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               static_cast<int>(mla_pair_lds_bytes<2>()));
+                               static_cast<int>(mla_shared_lds_bytes()));
   });
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kPairThreads), pl.lds, st, prm);
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kShThreads), pl.lds, st, prm);
   return hipSuccess;
 }
 
@@ -2392,6 +2384,7 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   prm.nht = pl.nht;
   prm.ds = pl.ds;
   prm.wgs = pl.wgs;
+  prm.pst = partial_stride(a, pl);
   prm.num_blocks = num_blocks;
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
   prm.sl2 = scale * kLog2e;
@@ -2399,7 +2392,8 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   if (need > 0 && (part_bytes < need || !part_ws || !aligned16(part_ws)))
     return mla_fail(nullptr, 0, "workspace too small for the attention partials");
   if (pl.mfma) {
-    char* meta = static_cast<char*>(part_ws) + round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * (a.Dc + 2) * 4);
+    char* meta =
+        static_cast<char*>(part_ws) + round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * partial_stride(a, pl) * 4);
     prm.gtotal = reinterpret_cast<int64_t*>(meta);
     prm.meta = reinterpret_cast<int*>(meta + sizeof(int64_t));
   }
@@ -2408,12 +2402,12 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   if (pl.mfma) {
     const int64_t grid = (static_cast<int64_t>(pl.wgs) + 7) / 8 * 8 * pl.head_groups;
     if (grid > 2147483647LL) return mla_fail(nullptr, 0, "mla_attend grid exceeds launch limits");
-    if (pl.pair && pl.head_groups == 1)
-      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_pair<QD_DTYPE_BF16, true>(prm, pl, grid, st)
-                                     : launch_attend_pair<QD_DTYPE_F16, true>(prm, pl, grid, st);
-    else if (pl.pair)
-      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_pair<QD_DTYPE_BF16, false>(prm, pl, grid, st)
-                                     : launch_attend_pair<QD_DTYPE_F16, false>(prm, pl, grid, st);
+    if (pl.shared && pl.head_groups == 1)
+      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_shared<QD_DTYPE_BF16, true>(prm, pl, grid, st)
+                                     : launch_attend_shared<QD_DTYPE_F16, true>(prm, pl, grid, st);
+    else if (pl.shared)
+      err = a.dtype == QD_DTYPE_BF16 ? launch_attend_shared<QD_DTYPE_BF16, false>(prm, pl, grid, st)
+                                     : launch_attend_shared<QD_DTYPE_F16, false>(prm, pl, grid, st);
     else if (pl.wave && pl.head_groups == 1)
       err = a.dtype == QD_DTYPE_BF16 ? launch_attend_wave<QD_DTYPE_BF16, true>(prm, pl, grid, st)
                                      : launch_attend_wave<QD_DTYPE_F16, true>(prm, pl, grid, st);
@@ -2676,7 +2670,7 @@ int qd_mla_attend_info(int batch, int q_len, int heads, int latent_dim, int rope
   const AttendPlan pl = plan_attend(a, splits, flags);
   if (out_splits) *out_splits = pl.mfma ? pl.wgs : pl.splits;
   if (head_groups) *head_groups = pl.mfma ? pl.head_groups : 0;
-  return pl.mfma ? (pl.pair ? 3 : pl.wave ? 2 : 1) : 0;
+  return pl.mfma ? (pl.shared ? 3 : pl.wave ? 2 : 1) : 0;
 }
 
 int qd_mla_attend(const void* q, const void* q_rope, const void* cache, const int32_t* block_table,

@@ -316,7 +316,7 @@ def mla_mode(args) -> None:
     a_gbs = a_bytes / (a_ms * 1e-3) / 1e9
     a_flops = 2 * rows * H * (Dc + Dr + Dc)
     a_tflops = a_flops / (a_ms * 1e-3) / 1e12
-    kname = {3: "mla_attend_pair_kernel", 2: "mla_attend_wave_kernel",
+    kname = {3: "mla_attend_shared_kernel", 2: "mla_attend_wave_kernel",
              1: "mla_attend_mfma_kernel"}.get(kind, "mla_attend_generic_kernel")
     if kind >= 1:
         kernels = kname + "+mla_merge_sk_kernel"

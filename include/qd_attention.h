@@ -64,10 +64,11 @@ enum {
   /* Use the portable VALU kernel even where the MFMA kernel applies. */
   QD_FLAG_FORCE_GENERIC = 1,
   /* MLA attention: use the workgroup-staged MFMA kernel even where the
-   * wave-streamed or the pair kernel applies (testing and comparison). */
+   * wave-streamed or the shared-tile kernel applies (testing and
+   * comparison). */
   QD_FLAG_MLA_STAGED = 2,
-  /* MLA attention: use the wave-streamed MFMA kernel even where the pair
-   * kernel applies (testing and comparison). */
+  /* MLA attention: use the wave-streamed MFMA kernel even where the
+   * shared-tile kernel applies (testing and comparison). */
   QD_FLAG_MLA_WAVE = 4
 };
 
@@ -285,9 +286,9 @@ int qd_validate_paged_metadata(const int32_t* block_table, const int32_t* contex
  * VALU kernel the number of context splits per row.
  * qd_mla_attend_info() reports the kernel and the partition.  flags:
  * QD_FLAG_FORCE_GENERIC selects the VALU kernels, QD_FLAG_MLA_STAGED the
- * workgroup-staged MFMA kernel where the wave-streamed or pair kernel would
- * run, QD_FLAG_MLA_WAVE the wave-streamed kernel where the pair kernel
- * would run.
+ * workgroup-staged MFMA kernel where the wave-streamed or shared-tile kernel
+ * would run, QD_FLAG_MLA_WAVE the wave-streamed kernel where the shared-tile
+ * kernel would run.
  * Nothing here allocates or synchronizes. */
 
 /* Reference checks in order, messages included (mla.cu:152-155). */
@@ -325,9 +326,10 @@ size_t qd_mla_attend_workspace_bytes(int batch, int q_len, int heads, int latent
                                      int block_size, int max_pages, int num_indices, int dtype, int splits,
                                      int flags);
 
-/* The plan qd_mla_attend would use: returns 3 for the pair MFMA kernel
- * (dense rows, latent 512, rope 64, 16-token pages, 64 heads or more), 2 for
- * the wave-streamed MFMA kernel (the same shapes with fewer heads), 1 for the
+/* The plan qd_mla_attend would use: returns 3 for the shared-tile MFMA
+ * kernel (dense rows, latent 512, rope 64, 32-token pages, 64 heads or more),
+ * 2 for the wave-streamed MFMA kernel (dense rows, latent 512, rope 64,
+ * 16-token pages, other head counts), 1 for the
  * workgroup-staged MFMA kernel (*out_splits = stream-K workgroups per head
  * group, *head_groups = head groups for both), 0 for the VALU kernel
  * (*out_splits = context splits per row, *head_groups = 0), -1 for invalid

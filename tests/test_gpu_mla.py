@@ -73,6 +73,9 @@ ATTEND_SHAPES = [
     ("deepseek-h64-fp16-t2", dict(lengths=[0, 40, 1500, 3000], q_len=2, heads=64, block_size=16,
                                   dtype=torch.float16)),
     ("h20-fp16-p16", dict(lengths=[5, 200, 33], q_len=2, heads=20, block_size=16, dtype=torch.float16)),
+    ("deepseek-h64-fp16-p32", dict(lengths=[0, 40, 1500, 3000, 31, 32, 33], q_len=2, heads=64, block_size=32,
+                                   dtype=torch.float16)),
+    ("deepseek-h96-p64", dict(lengths=[2100, 1, 700], q_len=1, heads=96, block_size=64, dtype=torch.bfloat16)),
     ("dc192-dr32", dict(lengths=[90, 257], q_len=1, heads=24, latent_dim=192, rope_dim=32, block_size=32,
                         dtype=torch.bfloat16)),
 ]
@@ -101,10 +104,11 @@ def test_mla_attend_kernel_choice(gpu):
     say("mla_attend plan on the device")
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64)
-    assert kind == 3 and groups == 2 and wgs * groups == cus      # pair kernel: 2 groups of 64 heads, 1 per CU
-    kind, wgs, groups = cabi.mla_attend_info(32, 1, 64, 512, 64, 16, 64)
+    assert kind == 3 and groups == 2 and wgs * groups == cus      # shared-tile kernel: 2 groups of 64 heads
+    kind, wgs, groups = cabi.mla_attend_info(32, 1, 64, 512, 64, 32, 64)
     assert kind == 3 and groups == 1
-    assert cabi.mla_attend_info(32, 1, 32, 512, 64, 16, 64)[0] == 2   # 32 heads: wave-streamed kernel
+    assert cabi.mla_attend_info(32, 1, 64, 512, 64, 16, 64)[0] == 2   # 16-token pages: wave-streamed kernel
+    assert cabi.mla_attend_info(32, 1, 32, 512, 64, 64, 64)[0] == 2   # 32 heads: wave-streamed kernel
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 128, 512, 64, 64, 64, flags=QD_FLAG_MLA_WAVE)
     assert kind == 2 and groups == 8 and wgs * groups <= 256      # wave-streamed kernel, 8 head groups
     kind, wgs, groups = cabi.mla_attend_info(32, 1, 20, 512, 64, 64, 64)
@@ -141,7 +145,7 @@ def test_mla_attend_sparse_and_causal(gpu, causal, kernel):
 
 
 @pytest.mark.parametrize("seed", range(1, 9))
-@pytest.mark.parametrize("heads,flags", [(16, 0), (16, QD_FLAG_MLA_STAGED), (64, 0)], ids=["wave", "staged", "pair"])
+@pytest.mark.parametrize("heads,flags", [(16, 0), (16, QD_FLAG_MLA_STAGED), (64, 0)], ids=["wave", "staged", "shared"])
 def test_mla_attend_bf16_accuracy_over_seeds(gpu, heads, flags, seed):
     """Random DeepSeek-shaped inputs with short rows in bf16: with one bf16
     rounding of the softmax weights in the PV product, 3 of these 8 seeds
@@ -161,7 +165,7 @@ def test_mla_attend_bf16_accuracy_over_seeds(gpu, heads, flags, seed):
 
 
 @pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_WAVE), (64, QD_FLAG_MLA_STAGED), (16, 0)],
-                         ids=["pair-h64", "wave-h64", "staged-h64", "wave-h16"])
+                         ids=["shared-h64", "wave-h64", "staged-h64", "wave-h16"])
 def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads, flags):
     """Physical page order and unreferenced cache contents do not change a bit
     of the output (index handling is exact)."""
