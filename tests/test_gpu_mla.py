@@ -277,8 +277,23 @@ DECODE_SHAPES = [
 # that into the output (observed up to ~2 bf16 ulps at |out| ~ 0.5).  So
 # every stage is checked at the 16-bit tolerance with the GPU's previous
 # stage as its input, the fused op must equal the composed GPU stages bit
-# for bit, and the chain end to end is held to CHAIN_TOL.
+# for bit, and the chain end to end is held to CHAIN_TOL.  That loosened bar
+# covers a few elements moved by the intermediate roundings; a systematic
+# mistake (a dropped term, a wrong index) moves most of them, so at most
+# CHAIN_OUTSIDE of the outputs may lie past the 16-bit bar (measured on
+# MI355X: none, in every case below).
 CHAIN_TOL = (1.5e-2, 2e-2)
+CHAIN_OUTSIDE = 0.002
+
+
+def _chain_close(got, ref, dtype, name):
+    err = np.abs(got.float().cpu().numpy() - ref)
+    atol, rtol = CHAIN_TOL if dtype != torch.float32 else TOL[dtype]
+    assert (err <= atol + rtol * np.abs(ref)).all(), f"{name}: chain max abs err {err.max():.3e}"
+    a16, r16 = TOL[dtype]
+    outside = float((err > a16 + r16 * np.abs(ref)).mean())
+    say(f"{name}: {outside:.4%} of the outputs past the {ODT[dtype]} bar")
+    assert outside <= CHAIN_OUTSIDE, f"{name}: {outside:.3%} of the outputs past the 16-bit bar"
 
 
 @pytest.mark.parametrize("name,kw", DECODE_SHAPES, ids=[s[0] for s in DECODE_SHAPES])
@@ -307,9 +322,7 @@ def test_mla_decode_matches_oracle(gpu, name, kw):
     assert torch.equal(got, composed)
     ref = oracle_mla_decode(_np(c["q_nope"]), _np(c["q_rope"]), *(_np(x) for x in meta), _np(c["w_uk"]),
                             _np(c["w_uv"]), indices=_np(idx), out_dtype=ODT[dtype])
-    atol, rtol = CHAIN_TOL if dtype != torch.float32 else TOL[dtype]
-    err = np.abs(got.float().cpu().numpy() - ref)
-    assert (err <= atol + rtol * np.abs(ref)).all(), f"chain max abs err {err.max():.3e}"
+    _chain_close(got, ref, dtype, "mla_decode " + name)
 
 
 def test_sparse_mla_is_mla_decode_with_indices(gpu):
@@ -335,10 +348,8 @@ def test_mla_decode_cabi_generic_matches_mfma(gpu):
         outs.append(out)
     torch.cuda.synchronize()
     ref = oracle_mla_decode(*(_np(x) for x in args), out_dtype="bf16")
-    atol, rtol = CHAIN_TOL
-    for out in outs:
-        err = np.abs(out.float().cpu().numpy() - ref)
-        assert (err <= atol + rtol * np.abs(ref)).all(), f"chain max abs err {err.max():.3e}"
+    for i, out in enumerate(outs):
+        _chain_close(out, ref, torch.bfloat16, f"mla_decode flags-variant {i}")
 
 
 def test_mla_validation_messages_on_device(gpu):

@@ -27,6 +27,7 @@ import torch
 from attention_amd.cases import make_mla_case
 from oracle import gqa_oracle as G
 from oracle import mla_oracle as M
+from oracle.cpu_path import reference_mla_cpu_path
 
 
 def case(lengths, q_len=1, heads=4, dn=8, dc=16, dr=8, dv=8, p=4, seed=0, num_indices=None):
@@ -205,6 +206,33 @@ def test_latent_write_matches_indexed_assignment():
     ref = cache.copy().reshape(-1, 7)
     ref[bad[keep]] = np.concatenate([lat, rope], axis=1)[keep]
     np.testing.assert_array_equal(got.reshape(-1, 7), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_torch_mla_cpu_path_matches_oracle(dtype):
+    """The timed MLA CPU baseline (oracle/cpu_path.reference_mla_cpu_path, the
+    torch CPU expressions of reference attention/reference/mla.py:6-34 read
+    through the page table) computes the attention of the pinned oracle:
+    fp32 within fp32 accumulation error; bf16 within one rounding of the
+    output, since the CPU path rounds once at the end where the oracle, fed
+    fp32 here, rounds nowhere before it.  Empty rows, causal queries (3 per
+    row, the first ones seeing fewer tokens) and a permuted page pool."""
+    c = make_mla_case(lengths=[0, 1, 7, 33, 20], q_len=3, heads=4, nope_dim=8, latent_dim=16, rope_dim=8,
+                      value_dim=8, block_size=4, dtype=dtype, seed=5)
+    scale = M.default_mla_scale(8, 8)
+    got = reference_mla_cpu_path(c["q_nope"], c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"],
+                                 c["w_uk"], c["w_uv"], scale=scale)
+    assert got.dtype == dtype and got.shape == (5, 3, 4, 8)
+    got = got.float().numpy()
+    f = lambda x: x.float().numpy()
+    ref = M.oracle_mla_decode(f(c["q_nope"]), f(c["q_rope"]), f(c["cache"]), c["table"].numpy(), c["lens"].numpy(),
+                              c["positions"].numpy(), f(c["w_uk"]), f(c["w_uv"]), scale, out_dtype="f32")
+    assert np.all(got[0] == 0.0)                                  # length 0: zeros
+    if dtype == torch.float32:
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+    else:
+        ref16 = torch.from_numpy(ref).to(torch.bfloat16).float().numpy()
+        assert np.all(np.abs(got - ref16) <= 2.0 ** -7 * np.abs(ref16) + 1e-6)
 
 
 def test_default_scale():
