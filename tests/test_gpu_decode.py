@@ -268,6 +268,77 @@ def test_poisoned_unused_slots_bitwise_product_path(gpu, dtype, wide):
     assert_close(outs[0], ref, DT_NAME[dtype], rows, "clean")
 
 
+@pytest.mark.parametrize("variant", ["aligned", "offset-table", "wide-table"])
+def test_auto_table_layouts(gpu, variant):
+    """The product path on a ragged batch (sequences split over workgroups,
+    several sequences per workgroup, -1 padding) with the block
+    table at a 4-byte offset inside a larger buffer and with a -1-padded
+    table wider than the lengths need: the same bits as the aligned table,
+    and the oracle's values."""
+    hq, hkv, d, p = 32, 8, 128, 16
+    lengths = _ragged_lengths(24, 2000, seed=31)
+    q, k, v, table, lens = make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
+                                            block_size=p, dtype=torch.bfloat16, seed=32)
+    maxp = 400 if variant == "wide-table" else 128
+    tpad = torch.full((len(lengths), maxp), -1, dtype=torch.int32)
+    tpad[:, :table.shape[1]] = table
+    base = to_dev((q, k, v, tpad, lens), gpu)
+    t_dev = base[3]
+    if variant == "offset-table":
+        buf = torch.full((tpad.numel() + 1,), -7, dtype=torch.int32, device=gpu)
+        t_dev = buf[1:].view(tpad.shape)
+        t_dev.copy_(base[3])
+        assert t_dev.data_ptr() % 16 != 0
+    say(f"table layout {variant}: max_pages={maxp}")
+    out = attention_amd.gqa_decode(base[0], base[1], base[2], t_dev, base[4])
+    ref_out = attention_amd.gqa_decode(*to_dev((q, k, v, tpad[:, :128], lens), gpu))
+    torch.cuda.synchronize()
+    if variant != "wide-table":   # a wider table may change the grid, so the split points
+        assert torch.equal(out, ref_out)
+    ref, rows = oracle_rows(to_dev((q, k, v, tpad, lens), gpu))
+    assert_close(out, ref, "bf16", rows, variant)
+
+
+def test_auto_long_and_short_poisoned(gpu):
+    """One long sequence split over most workgroups, next to short ones
+    that share workgroups with its ends; every cache slot no sequence uses
+    is NaN/Inf: the outputs match the oracle, stay finite and equal the
+    clean case bit for bit."""
+    hq, hkv, d, p = 32, 8, 128, 16
+    lengths = [12345, 17, 1, 1000, 33, 2049]
+    clean, poison = _poisoned_case("cpu", dtype=torch.bfloat16, lengths=lengths, hq=hq, hkv=hkv, d=d, p=p,
+                                   seed=44)
+    say(f"long and short sequences, poisoned: {lengths}")
+    out0 = attention_amd.gqa_decode(*to_dev(clean, gpu))
+    out1 = attention_amd.gqa_decode(*to_dev(poison, gpu))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out1).all()
+    assert torch.equal(out0, out1)
+    ref, rows = oracle_rows(to_dev(clean, gpu))
+    assert_close(out0, ref, "bf16", rows, "long and short")
+
+
+def test_auto_batch_beyond_register_lengths(gpu):
+    """Batches above 256 sequences: the prologue holds the lengths of
+    sequences 0..255 in registers and re-reads the rest from memory, for the
+    partition scan and when a workgroup enters them; empty sequences on both
+    sides of 256."""
+    hq, hkv, d, p = 8, 2, 128, 16
+    rng = np.random.default_rng(41)
+    lengths = [int(x) for x in rng.integers(1, 160, size=300)]
+    for i in (0, 5, 255, 256, 257, 299):
+        lengths[i] = 0
+    say(f"batch {len(lengths)} beyond staged lengths")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
+                                   dtype=torch.float16, seed=42), gpu)
+    kind, _, _, _ = cabi.auto_info(len(lengths), hq, hkv, d, p, case[3].shape[1], cabi.DTYPE[torch.float16])
+    assert kind == 1
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    ref, rows = oracle_rows(case)
+    assert_close(out, ref, "f16", rows, "B300")
+
+
 def test_poisoned_cfg3_bitwise_product_path(gpu):
     """cfg3's own lengths (B64, Hq28/Hkv4, up to 8192 tokens, many not a
     multiple of 16) on a pool with unused blocks, poisoned versus clean
