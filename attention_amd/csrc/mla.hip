@@ -1494,6 +1494,11 @@ constexpr int kShRows = 1024;                           // query rows (prologue 
 constexpr int kShListTiles = 512;                       // tiles of one workgroup's range
 constexpr int kShDma = 9;                               // DMA instructions per wave per tile
 constexpr int kShPartialPad = 4;                        // partial row: {m, l, pad, pad, acc[Dc]}
+constexpr int kShColBlocks = 512 / 16;                  // PV output blocks of 16 latent columns
+#ifndef QD_MLA_SHARED_PV_AHEAD
+#define QD_MLA_SHARED_PV_AHEAD 4
+#endif
+constexpr int kShPvAhead = QD_MLA_SHARED_PV_AHEAD;      // PV operand blocks read ahead of their MFMAs
 #ifndef QD_MLA_SHARED_ROW_COST
 #define QD_MLA_SHARED_ROW_COST 4
 #endif
@@ -1730,14 +1735,12 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   };
 
   float m_run = -INFINITY, l_run = 0.f;
-  f32x4 acc[4][8];
+  f32x4 acc[kShColBlocks];  // acc[cb][i]: this lane's head, latent column 16 cb + 4 q4 + i
   auto reset = [&]() {
     m_run = -INFINITY;
     l_run = 0.f;
 #pragma unroll
-    for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[bb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < kShColBlocks; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
   // The first tiles in flight and the first query, waited for here so that
@@ -1815,9 +1818,7 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
       m_run = mn;
       l_run *= alpha;
 #pragma unroll
-      for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-        for (int ee = 0; ee < 8; ++ee) acc[bb][ee] *= alpha;
+      for (int cb = 0; cb < kShColBlocks; ++cb) acc[cb] *= alpha;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     u32x4 pbl[2];
@@ -1838,41 +1839,39 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
       }
     }
 
-    // PV: one 16x16x32 per (bb, ee) over the tile's 32 tokens: k = 8 q4 + e
-    // is token 4 q4 + e of row block 0 for e < 4 and of row block 1 for
-    // e >= 4, in A (4 rows of each block from LDS, 8x8 byte-permute
-    // transposes) and in B (the lane's own weights); bf16 adds the lo
-    // weights with a second MFMA on the same A.  C tile (bb, ee) row m <->
-    // latent column 128 bb + 8 m + ee.  The next column block's rows are
-    // read while this block multiplies.
+    // PV: one 16x16x32 per 16-column block cb over the tile's 32 tokens: k =
+    // 8 q4 + e is token 4 q4 + e of row block 0 for e < 4 and of row block 1
+    // for e >= 4, in A and in B (the lane's own weights); bf16 adds the lo
+    // weights with a second MFMA on the same A.  A = V^T for columns 16 cb ..
+    // 16 cb + 15 comes from two transposing LDS reads (ds_read_b64_tr_b16):
+    // within each 16-lane group, result lane j element t is element j % 4 of
+    // what source lane 4 t + j / 4 addressed, so source lane (t, u) = (l16 /
+    // 4, l16 % 4) of group q4 addresses row 16 h + 4 q4 + t, columns 16 cb + 4
+    // u .. + 3, and lane j receives column 16 cb + j at tokens 16 h + 4 q4 +
+    // 0..3.  C tile cb: lane (head r16, q4) holds columns 16 cb + 4 q4 + i.
+    // Reads run kShPvAhead blocks ahead of their MFMAs.
     const u32x4 bhi = {pb[0][0], pb[0][1], pb[1][0], pb[1][1]};
     const u32x4 blo = {pbl[0][2], pbl[0][3], pbl[1][2], pbl[1][3]};
-    const char* pv0 = slot + 4 * q4 * kShLatStride + 16 * r16;
-    u32x4 rw[2][2][4];  // [column block parity][row block][row]
-    auto load_rows = [&](u32x4 (&dst)[2][4], int bb) {
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dst[tb][i] = *reinterpret_cast<const u32x4*>(pv0 + (16 * tb + i) * kShLatStride + 256 * bb);
+    const char* trb = slot + (4 * q4 + (r16 >> 2)) * kShLatStride + 8 * (r16 & 3);
+    auto tr_block = [&](int cb) {
+      using lds_v4s = __attribute__((address_space(3))) s16x4;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(trb + 32 * cb));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(trb + 16 * kShLatStride + 32 * cb));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+      const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+      return u32x4{l2[0], l2[1], h2[0], h2[1]};
     };
-    load_rows(rw[0], 0);
+    u32x4 av[kShPvAhead];
 #pragma unroll
-    for (int bb = 0; bb < 4; ++bb) {
-      if (bb + 1 < 4) load_rows(rw[(bb + 1) & 1], bb + 1);
+    for (int cb = 0; cb < kShPvAhead; ++cb) av[cb] = tr_block(cb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int cb = 0; cb < kShColBlocks; ++cb) {
+      const u32x4 a = av[cb % kShPvAhead];
+      if (cb + kShPvAhead < kShColBlocks) av[cb % kShPvAhead] = tr_block(cb + kShPvAhead);
+      acc[cb] = Ops::mma32(a, bhi, acc[cb]);
+      if constexpr (Ops::kSplitWeights) acc[cb] = Ops::mma32(a, blo, acc[cb]);
       __builtin_amdgcn_sched_barrier(0);
-      const u32x4 (&cur)[2][4] = rw[bb & 1];
-#pragma unroll
-      for (int ee = 0; ee < 8; ++ee) {
-        const int wd = ee >> 1;
-        const uint32_t sel = (ee & 1) ? 0x07060302u : 0x05040100u;
-        const u32x4 av = {__builtin_amdgcn_perm(cur[0][1][wd], cur[0][0][wd], sel),
-                          __builtin_amdgcn_perm(cur[0][3][wd], cur[0][2][wd], sel),
-                          __builtin_amdgcn_perm(cur[1][1][wd], cur[1][0][wd], sel),
-                          __builtin_amdgcn_perm(cur[1][3][wd], cur[1][2][wd], sel)};
-        acc[bb][ee] = Ops::mma32(av, bhi, acc[bb][ee]);
-        if constexpr (Ops::kSplitWeights) acc[bb][ee] = Ops::mma32(av, blo, acc[bb][ee]);
-      }
     }
 
     if (last) {
@@ -1884,26 +1883,15 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
           const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
           S* orow = static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * kDc;
 #pragma unroll
-          for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              uint32_t wd[4];
-#pragma unroll
-              for (int ee = 0; ee < 8; ee += 2)
-                wd[ee / 2] = Ops::pack2(acc[bb][ee][i] * inv, acc[bb][ee + 1][i] * inv);
-              *reinterpret_cast<u32x4*>(orow + 128 * bb + 32 * q4 + 8 * i) = u32x4{wd[0], wd[1], wd[2], wd[3]};
-            }
+          for (int cb = 0; cb < kShColBlocks; ++cb)
+            *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * q4) =
+                u32x2{Ops::pack2(acc[cb][0] * inv, acc[cb][1] * inv), Ops::pack2(acc[cb][2] * inv, acc[cb][3] * inv)};
         } else {
           float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kPst);
           if (q4 == 0) *reinterpret_cast<f32x2*>(pr) = f32x2{m_run == -INFINITY ? -INFINITY : m_run * kLn2, Lt};
 #pragma unroll
-          for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float* d = pr + kShPartialPad + 128 * bb + 32 * q4 + 8 * i;
-              *reinterpret_cast<f32x4*>(d) = f32x4{acc[bb][0][i], acc[bb][1][i], acc[bb][2][i], acc[bb][3][i]};
-              *reinterpret_cast<f32x4*>(d + 4) = f32x4{acc[bb][4][i], acc[bb][5][i], acc[bb][6][i], acc[bb][7][i]};
-            }
+          for (int cb = 0; cb < kShColBlocks; ++cb)
+            *reinterpret_cast<f32x4*>(pr + kShPartialPad + 16 * cb + 4 * q4) = acc[cb];
         }
       }
       if (t + 1 < n) load_q(r1);
