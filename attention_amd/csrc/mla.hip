@@ -176,6 +176,10 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
         for (int rt = 0; rt < RT; ++rt) a[u][rt] = u32x4{0u, 0u, 0u, 0u};
       }
     }
+    // Every load of the group is issued before the first MFMA: left free,
+    // the scheduler sank each load next to its MFMA with a full wait between
+    // them, one memory round trip per MFMA.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kPair; ++u)
 #pragma unroll
@@ -1487,7 +1491,10 @@ constexpr int kShThreads = 256;                         // four waves, 16 heads 
 constexpr int kShTokens = 32;                           // tokens per tile
 constexpr int kShBufs = 4;                              // LDS tile ring
 constexpr int kShRowBytes = 2 * 576;                    // cache row: 512 latent + 64 rope, 16-bit
-constexpr int kShLatStride = 1024 + 16;                 // LDS bytes per latent row (padded)
+#ifndef QD_MLA_SHARED_ROW_PAD
+#define QD_MLA_SHARED_ROW_PAD 32
+#endif
+constexpr int kShLatStride = 1024 + QD_MLA_SHARED_ROW_PAD;  // LDS bytes per latent row (padded)
 constexpr int kShLatBytes = kShTokens * kShLatStride;   // latent part of a tile
 constexpr int kShTileBytes = kShLatBytes + kShTokens * 128;  // + rope rows
 constexpr int kShRows = 1024;                           // query rows (prologue arrays in the ring)
