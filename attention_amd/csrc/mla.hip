@@ -254,7 +254,8 @@ struct MlaParams {
   int nht, ds;      // MFMA kernel: head tiles per workgroup, latent slices per head tile
   int wgs;          // MFMA kernel: workgroups per head group (stream-K ranges)
   int* meta;        // MFMA kernel: [rows][2] {first workgroup, workgroups} per row
-  int pst;          // MFMA kernel: floats per partial row {m, l, pad.., acc[Dc]} (acc at pst - Dc)
+  int pst;          // MFMA kernel: floats per partial row: {m, l, acc[Dc]} fp32, or (shared-tile
+                    // kernel) {m, l, s, 0} + Dc fp16 acc / s
   int64_t* gtotal;  // MFMA kernel: tiles G of the batch (merge: skips empty ranges)
   int64_t num_blocks;
   float sl2;        // scale * log2(e)
@@ -1500,7 +1501,7 @@ constexpr int kShTileBytes = kShLatBytes + kShTokens * 128;  // + rope rows
 constexpr int kShRows = 1024;                           // query rows (prologue arrays in the ring)
 constexpr int kShListTiles = 512;                       // tiles of one workgroup's range
 constexpr int kShDma = 9;                               // DMA instructions per wave per tile
-constexpr int kShPartialPad = 4;                        // partial row: {m, l, pad, pad, acc[Dc]}
+constexpr int kShPartialPad = 4;                        // partial row: {m, l, s, pad} + Dc fp16 acc / s
 constexpr int kShColBlocks = 512 / 16;                  // PV output blocks of 16 latent columns
 #ifndef QD_MLA_SHARED_PV_AHEAD
 #define QD_MLA_SHARED_PV_AHEAD 4
@@ -1541,6 +1542,12 @@ __device__ __forceinline__ void dma_ring_barrier() {
 // vmcnt(0) alone (expcnt and lgkmcnt left free).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
 
+// Two floats as fp16, round to nearest even, lo in the low half.
+__device__ __forceinline__ uint32_t pack_f16_rne(float lo, float hi) {
+  const f16x2 v = __builtin_convertvector(f32x2{lo, hi}, f16x2);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // Stream-K over (query row, 32-token tile) like mla_attend_wave_kernel (same
 // grid mapping, meta and merge kernel; partial rows padded to Dc + 4 floats
 // so their stores are 16-byte), one workgroup per CU with 64 heads, every
@@ -1577,7 +1584,7 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   using S = typename E::S;
   constexpr int kDc = 512;
   constexpr int kW = 576;
-  constexpr int kPst = kDc + kShPartialPad;
+  constexpr int kPst = kShPartialPad + kDc / 2;  // floats per partial row
   extern __shared__ __align__(16) char smem[];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
@@ -1894,11 +1901,26 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
             *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * q4) =
                 u32x2{Ops::pack2(acc[cb][0] * inv, acc[cb][1] * inv), Ops::pack2(acc[cb][2] * inv, acc[cb][3] * inv)};
         } else {
-          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kPst);
-          if (q4 == 0) *reinterpret_cast<f32x2*>(pr) = f32x2{m_run == -INFINITY ? -INFINITY : m_run * kLn2, Lt};
+          // Partial as {m, l, s, 0} and acc / s in fp16, s = the largest |acc|
+          // of the head (the 4 lanes q4 of r16): every value lies in [-1, 1]
+          // and keeps 11 bits relative to s, half the bytes of fp32.
+          float amax = 0.f;
 #pragma unroll
           for (int cb = 0; cb < kShColBlocks; ++cb)
-            *reinterpret_cast<f32x4*>(pr + kShPartialPad + 16 * cb + 4 * q4) = acc[cb];
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(acc[cb][0]), fabsf(acc[cb][1])),
+                                     fmaxf(fabsf(acc[cb][2]), fabsf(acc[cb][3]))));
+          amax = fmaxf(amax, __shfl_xor(amax, 16));
+          amax = fmaxf(amax, __shfl_xor(amax, 32));
+          const float sc = amax > 0.f ? amax : 1.f;
+          const float isc = 1.f / sc;
+          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kPst);
+          if (q4 == 0)
+            *reinterpret_cast<f32x4*>(pr) = f32x4{m_run == -INFINITY ? -INFINITY : m_run * kLn2, Lt, sc, 0.f};
+          char* pa = reinterpret_cast<char*>(pr + kShPartialPad) + 8 * q4;
+#pragma unroll
+          for (int cb = 0; cb < kShColBlocks; ++cb)
+            *reinterpret_cast<u32x2*>(pa + 32 * cb) =
+                u32x2{pack_f16_rne(acc[cb][0] * isc, acc[cb][1] * isc), pack_f16_rne(acc[cb][2] * isc, acc[cb][3] * isc)};
         }
       }
       if (t + 1 < n) load_q(r1);
@@ -1918,7 +1940,11 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
 // online_softmax.cuh:17-24 (empty partials skipped, an all-empty row gives
 // zeros), kBatch of them loaded per memory round trip: one trip after the
 // meta entry covers a typical row.
-template <int DT>
+//
+// HALF: the shared-tile kernel's rows, {m, l, s, 0} then Dc = 512 fp16
+// values acc / s; lane j folds columns 8 j .. 8 j + 7 (one 16-byte load per
+// row and one store).
+template <int DT, bool HALF>
 __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
   using E = Elem<DT>;
   using S = typename E::S;
@@ -1953,12 +1979,21 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
       const int k = first + c + t;
       if (c + t < nwg && present(k)) {  // wave-uniform
         const float* pr = base + k * stride;
-        ms[t] = pr[0];
-        ls[t] = pr[1];
+        if constexpr (HALF) {
+          const f32x4 hd = *reinterpret_cast<const f32x4*>(pr);
+          const f16x8 hv = *reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(pr + 4) + 16 * lane);
+          ms[t] = hd[0];
+          ls[t] = hd[1];
 #pragma unroll
-        for (int j = 0; j < kAcc; ++j) {
-          const int d = lane + 64 * j;
-          if (d < p.Dc) v[t][j] = pr[aoff + d];
+          for (int j = 0; j < kAcc; ++j) v[t][j] = static_cast<float>(hv[j]) * hd[2];
+        } else {
+          ms[t] = pr[0];
+          ls[t] = pr[1];
+#pragma unroll
+          for (int j = 0; j < kAcc; ++j) {
+            const int d = lane + 64 * j;
+            if (d < p.Dc) v[t][j] = pr[aoff + d];
+          }
         }
       }
     }
@@ -1976,10 +2011,17 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
   }
   S* orow = static_cast<S*>(p.out) + wid * p.Dc;
   const float inv = L > 0.f ? 1.f / L : 0.f;
+  if constexpr (HALF) {
+    S o[kAcc];
 #pragma unroll
-  for (int j = 0; j < kAcc; ++j) {
-    const int d = lane + 64 * j;
-    if (d < p.Dc) orow[d] = E::from_f(acc[j] * inv);
+    for (int j = 0; j < kAcc; ++j) o[j] = E::from_f(acc[j] * inv);
+    *reinterpret_cast<u32x4*>(orow + 8 * lane) = __builtin_bit_cast(u32x4, o);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kAcc; ++j) {
+      const int d = lane + 64 * j;
+      if (d < p.Dc) orow[d] = E::from_f(acc[j] * inv);
+    }
   }
 }
 
@@ -2281,7 +2323,11 @@ size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
 // count G (int64) and [R][2] int32 row spans.
 // Floats per stream-K partial row: {m, l, acc[Dc]}, or {m, l, pad, pad,
 // acc[Dc]} for the shared-tile kernel (16-byte accumulator stores).
-int partial_stride(const AttendShape& a, const AttendPlan& pl) { return a.Dc + (pl.shared ? kShPartialPad : 2); }
+// Floats per partial row: the shared-tile kernel's {m, l, s, 0} + Dc fp16,
+// the other MFMA kernels' {m, l} + Dc fp32.
+int partial_stride(const AttendShape& a, const AttendPlan& pl) {
+  return pl.shared ? kShPartialPad + a.Dc / 2 : a.Dc + 2;
+}
 
 size_t attend_partial_bytes(const AttendShape& a, const AttendPlan& pl) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
@@ -2436,10 +2482,13 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   if (rc != QD_OK || (!pl.mfma && pl.splits == 1)) return rc;
   const int64_t mgrid = (rows * a.H + 3) / 4;
   if (pl.mfma) {
+    using MergeFn = void (*)(MlaParams);
+    MergeFn fn = nullptr;
     if (a.dtype == QD_DTYPE_BF16)
-      hipLaunchKernelGGL(mla_merge_sk_kernel<QD_DTYPE_BF16>, dim3(mgrid), dim3(256), 0, st, prm);
+      fn = pl.shared ? mla_merge_sk_kernel<QD_DTYPE_BF16, true> : mla_merge_sk_kernel<QD_DTYPE_BF16, false>;
     else
-      hipLaunchKernelGGL(mla_merge_sk_kernel<QD_DTYPE_F16>, dim3(mgrid), dim3(256), 0, st, prm);
+      fn = pl.shared ? mla_merge_sk_kernel<QD_DTYPE_F16, true> : mla_merge_sk_kernel<QD_DTYPE_F16, false>;
+    hipLaunchKernelGGL(fn, dim3(mgrid), dim3(256), 0, st, prm);
     return launch_status("mla_attend merge");
   }
   switch (a.dtype) {
