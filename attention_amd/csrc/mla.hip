@@ -131,6 +131,7 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   using S = typename E::S;
   constexpr int kPair = PAIR;
   __shared__ f32x4 red[4][8][64];
+  __shared__ __align__(16) S stage[16][128];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r16 = lane & 15, q4 = lane >> 4;
   const int h = blockIdx.y;
@@ -187,6 +188,9 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[rt][e] = Ops::mma32(a[u][rt], bop[u][e], acc[rt][e]);
   }
+  // The 4 waves' partial tiles are summed through LDS and the 16 x 128 output
+  // tile is staged there as well, so that each lane writes 16 contiguous
+  // bytes (8 columns of one row) instead of 8 scattered 2-byte stores.
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
@@ -196,14 +200,17 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
     for (int ee = 0; ee < 2; ++ee) {
       const int e = 2 * wv + ee;
       const f32x4 s = red[0][e][lane] + red[1][e][lane] + red[2][e][lane] + red[3][e][lane];
-      const int ocol = cbase + 8 * r16 + e;
-      if (ocol < p.dout) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t row = r0 + 16 * rt + 4 * q4 + i;
-          if (row < p.rows) out[(row * p.H + h) * p.dout + ocol] = E::from_f(s[i]);
-        }
-      }
+      for (int i = 0; i < 4; ++i) stage[4 * q4 + i][8 * r16 + e] = E::from_f(s[i]);
+    }
+    __syncthreads();
+    {
+      const int orow = static_cast<int>(threadIdx.x) >> 4;  // 0..15
+      const int oc = 8 * (static_cast<int>(threadIdx.x) & 15);
+      const int64_t row = r0 + 16 * rt + orow;
+      if (row < p.rows && cbase + oc < p.dout)  // dout % 8 == 0: whole 8-column groups
+        *reinterpret_cast<u32x4*>(out + (row * p.H + h) * p.dout + cbase + oc) =
+            *reinterpret_cast<const u32x4*>(&stage[orow][oc]);
     }
     __syncthreads();
   }
