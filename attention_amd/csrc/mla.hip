@@ -262,11 +262,23 @@ struct MlaParams {
   int wgs;          // MFMA kernel: workgroups per head group (stream-K ranges)
   int* meta;        // MFMA kernel: [rows][2] {first workgroup, workgroups} per row
   int pst;          // MFMA kernel: floats per partial row: {m, l, acc[Dc]} fp32, or (shared-tile
-                    // kernel) {m, l, s, 0} + Dc fp16 acc / s
+                    // and wave kernels) kHalfHeader floats + Dc fp16 (kHalfPst)
   int64_t* gtotal;  // MFMA kernel: tiles G of the batch (merge: skips empty ranges)
   int64_t num_blocks;
   float sl2;        // scale * log2(e)
 };
+
+// Half-precision partial rows (shared-tile and wave kernels): {m, l, s0, s1,
+// s2, s3, 0, 0} in fp32, then Dc = 512 fp16 values acc / s_k for latent
+// columns [128 k, 128 k + 128), s_k the block's largest |acc| for the head.
+constexpr int kHalfHeader = 8;                         // floats before the fp16 values
+constexpr int kHalfPst = kHalfHeader + 512 / 2;        // floats per partial row
+
+// Two floats as fp16, round to nearest even, lo in the low half.
+__device__ __forceinline__ uint32_t pack_f16_rne(float lo, float hi) {
+  const f16x2 v = __builtin_convertvector(f32x2{lo, hi}, f16x2);
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // Visible prefix of query row r (mla.cu:37), clamped to the table capacity
 // so that a length beyond the table never reads past the table row.
@@ -1329,17 +1341,36 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
             *reinterpret_cast<u32x4*>(orow + 128 * bb + 32 * q4 + 8 * i) = u32x4{wd[0], wd[1], wd[2], wd[3]};
           }
         } else {
-          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(Lay::kDc + 2);
-          if (bb == 0 && q4 == 0) {
-            pr[0] = M == -INFINITY ? -INFINITY : M * kLn2;
-            pr[1] = Lt;
+          // Half-precision partial row (kHalfHeader): block bb as fp16
+          // values o / s_bb, s_bb the block's largest |o| for the head (the
+          // 4 lanes q4 of r16 hold the block).
+          float amax = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o[e][0]), fabsf(o[e][1])), fmaxf(fabsf(o[e][2]), fabsf(o[e][3]))));
+          amax = fmaxf(amax, __shfl_xor(amax, 16));
+          amax = fmaxf(amax, __shfl_xor(amax, 32));
+          const float sbb = amax > 0.f ? amax : 1.f;
+          const float isc = 1.f / sbb;
+          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kHalfPst);
+          if (q4 == 0) {
+            if (bb == 0) {
+              pr[0] = M == -INFINITY ? -INFINITY : M * kLn2;
+              pr[1] = Lt;
+              pr[6] = 0.f;
+              pr[7] = 0.f;
+            }
+            pr[2 + bb] = sbb;
           }
-          // Rows are Dc+2 floats: the accumulator starts 8 bytes in.
+          // Lane (r16, q4), row i: columns 128 bb + 32 q4 + 8 i + e, e = 0..7.
+          char* pa = reinterpret_cast<char*>(pr + kHalfHeader) + 2 * (128 * bb + 32 * q4);
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < 4; ++i) {
+            uint32_t wd[4];
 #pragma unroll
-            for (int e = 0; e < 8; e += 2)
-              *reinterpret_cast<f32x2*>(pr + 2 + 128 * bb + 32 * q4 + 8 * i + e) = f32x2{o[e][i], o[e + 1][i]};
+            for (int e = 0; e < 8; e += 2) wd[e / 2] = pack_f16_rne(o[e][i] * isc, o[e + 1][i] * isc);
+            *reinterpret_cast<u32x4*>(pa + 16 * i) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+          }
         }
       }
       lds_barrier();
@@ -1508,7 +1539,6 @@ constexpr int kShTileBytes = kShLatBytes + kShTokens * 128;  // + rope rows
 constexpr int kShRows = 1024;                           // query rows (prologue arrays in the ring)
 constexpr int kShListTiles = 512;                       // tiles of one workgroup's range
 constexpr int kShDma = 9;                               // DMA instructions per wave per tile
-constexpr int kShPartialPad = 4;                        // partial row: {m, l, s, pad} + Dc fp16 acc / s
 constexpr int kShColBlocks = 512 / 16;                  // PV output blocks of 16 latent columns
 #ifndef QD_MLA_SHARED_PV_AHEAD
 #define QD_MLA_SHARED_PV_AHEAD 4
@@ -1549,11 +1579,6 @@ __device__ __forceinline__ void dma_ring_barrier() {
 // vmcnt(0) alone (expcnt and lgkmcnt left free).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
 
-// Two floats as fp16, round to nearest even, lo in the low half.
-__device__ __forceinline__ uint32_t pack_f16_rne(float lo, float hi) {
-  const f16x2 v = __builtin_convertvector(f32x2{lo, hi}, f16x2);
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 // Stream-K over (query row, 32-token tile) like mla_attend_wave_kernel (same
 // grid mapping, meta and merge kernel; partial rows padded to Dc + 4 floats
@@ -1591,7 +1616,6 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   using S = typename E::S;
   constexpr int kDc = 512;
   constexpr int kW = 576;
-  constexpr int kPst = kShPartialPad + kDc / 2;  // floats per partial row
   extern __shared__ __align__(16) char smem[];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
@@ -1908,26 +1932,34 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
             *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * q4) =
                 u32x2{Ops::pack2(acc[cb][0] * inv, acc[cb][1] * inv), Ops::pack2(acc[cb][2] * inv, acc[cb][3] * inv)};
         } else {
-          // Partial as {m, l, s, 0} and acc / s in fp16, s = the largest |acc|
-          // of the head (the 4 lanes q4 of r16): every value lies in [-1, 1]
-          // and keeps 11 bits relative to s, half the bytes of fp32.
-          float amax = 0.f;
+          // Half-precision partial (kHalfHeader): acc / s_k in fp16, s_k the
+          // largest |acc| of the head's 128-column block k (the 4 lanes q4 of
+          // r16 hold it): every value lies in [-1, 1] and keeps 11 bits
+          // relative to s_k, half the bytes of fp32.
+          float sk[4];
 #pragma unroll
-          for (int cb = 0; cb < kShColBlocks; ++cb)
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(acc[cb][0]), fabsf(acc[cb][1])),
-                                     fmaxf(fabsf(acc[cb][2]), fabsf(acc[cb][3]))));
-          amax = fmaxf(amax, __shfl_xor(amax, 16));
-          amax = fmaxf(amax, __shfl_xor(amax, 32));
-          const float sc = amax > 0.f ? amax : 1.f;
-          const float isc = 1.f / sc;
-          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kPst);
-          if (q4 == 0)
-            *reinterpret_cast<f32x4*>(pr) = f32x4{m_run == -INFINITY ? -INFINITY : m_run * kLn2, Lt, sc, 0.f};
-          char* pa = reinterpret_cast<char*>(pr + kShPartialPad) + 8 * q4;
+          for (int k = 0; k < 4; ++k) {
+            float amax = 0.f;
 #pragma unroll
-          for (int cb = 0; cb < kShColBlocks; ++cb)
+            for (int cb = 8 * k; cb < 8 * k + 8; ++cb)
+              amax = fmaxf(amax, fmaxf(fmaxf(fabsf(acc[cb][0]), fabsf(acc[cb][1])),
+                                       fmaxf(fabsf(acc[cb][2]), fabsf(acc[cb][3]))));
+            amax = fmaxf(amax, __shfl_xor(amax, 16));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            sk[k] = amax > 0.f ? amax : 1.f;
+          }
+          float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kHalfPst);
+          if (q4 == 0) {
+            *reinterpret_cast<f32x4*>(pr) = f32x4{m_run == -INFINITY ? -INFINITY : m_run * kLn2, Lt, sk[0], sk[1]};
+            *reinterpret_cast<f32x4*>(pr + 4) = f32x4{sk[2], sk[3], 0.f, 0.f};
+          }
+          char* pa = reinterpret_cast<char*>(pr + kHalfHeader) + 8 * q4;
+#pragma unroll
+          for (int cb = 0; cb < kShColBlocks; ++cb) {
+            const float isc = 1.f / sk[cb / 8];
             *reinterpret_cast<u32x2*>(pa + 32 * cb) =
                 u32x2{pack_f16_rne(acc[cb][0] * isc, acc[cb][1] * isc), pack_f16_rne(acc[cb][2] * isc, acc[cb][3] * isc)};
+          }
         }
       }
       if (t + 1 < n) load_q(r1);
@@ -1948,9 +1980,9 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
 // zeros), kBatch of them loaded per memory round trip: one trip after the
 // meta entry covers a typical row.
 //
-// HALF: the shared-tile kernel's rows, {m, l, s, 0} then Dc = 512 fp16
-// values acc / s; lane j folds columns 8 j .. 8 j + 7 (one 16-byte load per
-// row and one store).
+// HALF: half-precision rows of the shared-tile and wave kernels
+// (kHalfHeader, Dc = 512); lane j folds columns 8 j .. 8 j + 7 (one 16-byte
+// load per row and one store).
 template <int DT, bool HALF>
 __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
   using E = Elem<DT>;
@@ -1988,11 +2020,15 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
         const float* pr = base + k * stride;
         if constexpr (HALF) {
           const f32x4 hd = *reinterpret_cast<const f32x4*>(pr);
-          const f16x8 hv = *reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(pr + 4) + 16 * lane);
+          const f32x4 hs = *reinterpret_cast<const f32x4*>(pr + 4);
+          const f16x8 hv = *reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(pr + kHalfHeader) + 16 * lane);
           ms[t] = hd[0];
           ls[t] = hd[1];
+          // Lane j holds columns 8 j .. 8 j + 7, of block j / 16.
+          const int kb = lane >> 4;
+          const float sc = kb == 0 ? hd[2] : kb == 1 ? hd[3] : kb == 2 ? hs[0] : hs[1];
 #pragma unroll
-          for (int j = 0; j < kAcc; ++j) v[t][j] = static_cast<float>(hv[j]) * hd[2];
+          for (int j = 0; j < kAcc; ++j) v[t][j] = static_cast<float>(hv[j]) * sc;
         } else {
           ms[t] = pr[0];
           ls[t] = pr[1];
@@ -2330,10 +2366,11 @@ size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
 // count G (int64) and [R][2] int32 row spans.
 // Floats per stream-K partial row: {m, l, acc[Dc]}, or {m, l, pad, pad,
 // acc[Dc]} for the shared-tile kernel (16-byte accumulator stores).
-// Floats per partial row: the shared-tile kernel's {m, l, s, 0} + Dc fp16,
-// the other MFMA kernels' {m, l} + Dc fp32.
+// Floats per partial row: the half-precision rows of the shared-tile and
+// wave kernels (kHalfPst), the staged kernel's {m, l} + Dc fp32.
+bool half_partials(const AttendPlan& pl) { return pl.shared || pl.wave; }
 int partial_stride(const AttendShape& a, const AttendPlan& pl) {
-  return pl.shared ? kShPartialPad + a.Dc / 2 : a.Dc + 2;
+  return half_partials(pl) ? kHalfPst : a.Dc + 2;
 }
 
 size_t attend_partial_bytes(const AttendShape& a, const AttendPlan& pl) {
@@ -2492,9 +2529,9 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
     using MergeFn = void (*)(MlaParams);
     MergeFn fn = nullptr;
     if (a.dtype == QD_DTYPE_BF16)
-      fn = pl.shared ? mla_merge_sk_kernel<QD_DTYPE_BF16, true> : mla_merge_sk_kernel<QD_DTYPE_BF16, false>;
+      fn = half_partials(pl) ? mla_merge_sk_kernel<QD_DTYPE_BF16, true> : mla_merge_sk_kernel<QD_DTYPE_BF16, false>;
     else
-      fn = pl.shared ? mla_merge_sk_kernel<QD_DTYPE_F16, true> : mla_merge_sk_kernel<QD_DTYPE_F16, false>;
+      fn = half_partials(pl) ? mla_merge_sk_kernel<QD_DTYPE_F16, true> : mla_merge_sk_kernel<QD_DTYPE_F16, false>;
     hipLaunchKernelGGL(fn, dim3(mgrid), dim3(256), 0, st, prm);
     return launch_status("mla_attend merge");
   }
