@@ -164,6 +164,33 @@ def test_mla_attend_bf16_accuracy_over_seeds(gpu, heads, flags, seed):
     _close(out, _oracle_attend(c, qa, scale, dtype=dtype), dtype, f"seed {seed}")
 
 
+@pytest.mark.parametrize("dtype,mag", [(torch.bfloat16, 1e4), (torch.bfloat16, 1e-4), (torch.float16, 8e3),
+                                       (torch.float16, 1e-3)], ids=["bf16-1e4", "bf16-1e-4", "f16-8e3", "f16-1e-3"])
+@pytest.mark.parametrize("heads,flags,splits", [(64, 0, 0), (64, 0, 3), (16, 0, 3), (64, QD_FLAG_MLA_WAVE, 3),
+                                                (64, QD_FLAG_MLA_STAGED, 3), (64, QD_FLAG_FORCE_GENERIC, 3)],
+                         ids=["shared-auto", "shared-split3", "wave-h16", "wave-h64", "staged", "generic"])
+def test_mla_attend_latent_magnitude(gpu, dtype, mag, heads, flags, splits):
+    """Latent rows scaled by ``mag`` and the absorbed query by ``1/mag``: the
+    scores stay put and the output scales by ``mag``.  The split rows' partial
+    results pass through 16-bit storage in some kernels, so values far above
+    the fp16 range (1e4 latent rows summed over thousands of tokens) and far
+    below it must come back with the 16-bit tolerance relative to ``mag``."""
+    say(f"mla_attend latent magnitude {mag} {ODT[dtype]} heads={heads} flags={flags} splits={splits}")
+    c = _case(gpu, lengths=[3000, 700, 1, 1500], q_len=1, heads=heads, block_size=64, dtype=dtype, seed=11)
+    Dc = c["w_uk"].shape[-1]
+    c["cache"][..., :Dc] = (c["cache"][..., :Dc].float() * mag).to(dtype)
+    qa = (_absorbed(c, dtype).float() / mag).to(dtype).to(gpu)
+    scale = default_mla_scale(c["q_nope"].shape[-1], c["q_rope"].shape[-1])
+    out = torch.empty_like(qa)
+    rc = cabi.mla_attend(qa, c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"], out, scale=scale,
+                         splits=splits, flags=flags)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = _oracle_attend(c, qa, scale, dtype=dtype)
+    _close(out.float() / mag, ref / mag, dtype, f"magnitude {mag}")
+
+
 @pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_WAVE), (64, QD_FLAG_MLA_STAGED), (16, 0)],
                          ids=["shared-h64", "wave-h64", "staged-h64", "wave-h16"])
 def test_mla_attend_page_permutation_and_poison_bitwise(gpu, heads, flags):
