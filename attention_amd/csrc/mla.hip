@@ -1538,12 +1538,14 @@ constexpr int kShLatBytes = kShTokens * kShLatStride;   // latent part of a tile
 constexpr int kShTileBytes = kShLatBytes + kShTokens * 128;  // + rope rows
 constexpr int kShRows = 1024;                           // query rows (prologue arrays in the ring)
 constexpr int kShListTiles = 512;                       // tiles of one workgroup's range
+constexpr int kShCtlPad = 8;                            // placeholder entries after the tile list
 constexpr int kShDma = 9;                               // DMA instructions per wave per tile
 constexpr int kShColBlocks = 512 / 16;                  // PV output blocks of 16 latent columns
 #ifndef QD_MLA_SHARED_PV_AHEAD
 #define QD_MLA_SHARED_PV_AHEAD 4
 #endif
 constexpr int kShPvAhead = QD_MLA_SHARED_PV_AHEAD;      // PV operand blocks read ahead of their MFMAs
+static_assert(kShDma <= 18, "one DMA instruction per QK chunk");
 #ifndef QD_MLA_SHARED_ROW_COST
 #define QD_MLA_SHARED_ROW_COST 4
 #endif
@@ -1556,7 +1558,7 @@ constexpr int kShRowCost = QD_MLA_SHARED_ROW_COST;
 
 __host__ __device__ constexpr size_t mla_shared_lds_bytes() {
   return static_cast<size_t>(kShBufs) * kShTileBytes    // tile ring (prologue arrays before the first tile)
-         + static_cast<size_t>(kShListTiles) * 16;      // tile list
+         + static_cast<size_t>(kShListTiles + kShCtlPad) * 16;  // tile list
 }
 
 static_assert(kShRows * (4 + 4 + 8) + kShListTiles * 16 <= kShBufs * kShTileBytes,
@@ -1579,34 +1581,74 @@ __device__ __forceinline__ void dma_ring_barrier() {
 // vmcnt(0) alone (expcnt and lgkmcnt left free).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
 
+// f(std::integral_constant<int, I>) for I = B .. E-1, in order.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// LDS byte address of a pointer into this workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// ds_read_b64_tr_b16 at LDS address base + OFF, as inline asm.  The
+// compiler's wait insertion treats the builtin form as a read of any LDS
+// buffer a DMA (global_load_lds) may be filling and waits for every DMA in
+// flight before it; the asm form is not tracked, so its result may be used
+// only after lds_wait_tied.
+template <int OFF>
+struct TrRead {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  __device__ __forceinline__ static void issue(uint32_t base, u32x2& out) {
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(out) : "v"(base), "i"(OFF));
+  }
+};
+
+// Waits until at most N LDS (and scalar-memory) operations are outstanding.
+// LDS operations complete in order, so with N = the number of LDS reads
+// issued after the ones that produced a and b, those are complete (other
+// operations outstanding only make the wait longer).  a and b are tied to
+// the wait so that no use of them is scheduled before it.
+template <int N>
+__device__ __forceinline__ void lds_wait_tied(u32x2& a, u32x2& b) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
 
 // Stream-K over (query row, 32-token tile) like mla_attend_wave_kernel (same
-// grid mapping, meta and merge kernel; partial rows padded to Dc + 4 floats
-// so their stores are 16-byte), one workgroup per CU with 64 heads, every
-// wave on every tile of the workgroup's range.  Wave v serves heads
-// 16 v .. 16 v + 15 of the workgroup's:
+// grid mapping, meta and merge kernel; fp16 partial rows), one workgroup per
+// CU with 64 heads, every wave on every tile of the workgroup's range.  Wave
+// v serves heads 16 v .. 16 v + 15 of the workgroup's:
 //   load     each wave DMAs a quarter of the tile's 32 cache rows (latent
 //            rows 8v .. 8v + 7, 1 KB per instruction, and their rope bytes)
 //            into one of kShBufs LDS buffers (global_load_lds), kShBufs - 1
-//            tiles ahead; no registers hold tiles in flight.  Latent rows are
-//            1 KB apart plus 16 bytes (each instruction has its own LDS
-//            base), so the operand reads meet no LDS bank conflict and take
-//            immediate offsets from one lane address; rope chunk c of row R
-//            sits at c ^ (R/2 % 8).  Rows past the tile's visible count
-//            re-read its last visible row and get weight 0.
+//            tiles ahead, one instruction per QK chunk of the current tile
+//            (issued back to back after the barrier, the four waves' loads
+//            queued on the CU's load path for as long as the QK products
+//            take); no registers hold tiles in flight.  Latent rows are 1 KB
+//            apart plus kShLatStride - 1024 bytes (each instruction has its
+//            own LDS base), so the operand reads take immediate offsets from
+//            one lane address; rope chunk c of row R sits at c ^ (R/2 % 8).
+//            Rows past the tile's visible count re-read its last visible row
+//            and get weight 0.
 //   QK       per 16-row block of the tile: S^T = K chunk x [q | q_rope]
 //            chunk over the 18 32-element chunks (query in registers, loaded
 //            when a row segment starts).
 //   softmax  fp32 over the tile's 32 tokens, with the lazy reference max of
 //            the wave kernel.
-//   PV       16x16x16 per row block with A = C^T from 4 LDS rows (8x8
-//            byte-permute transposes, as in the wave kernel); bf16 weights
-//            as hi + lo in one 16x16x32.
+//   PV       one 16x16x32 per 16 output columns over all 32 tokens, A = V^T
+//            from transposing LDS reads; bf16 weights as hi + lo (two MFMAs
+//            on the same A).
 // No per-tile exchange between waves: one barrier per tile, for the ring.
 // At the end of a row segment each wave stores its heads: the output (whole
-// row) or the partial {m, l, acc} in slot (w + row); the next row's query is
-// loaded there too, and one wait for every load in flight covers both (the
-// stores would otherwise hold the tile waits behind them).
+// row) or the partial {m, l, scales, acc} in slot (w + row); the next row's
+// query is loaded there too, and one wait for every load in flight covers
+// both (the stores would otherwise hold the tile waits behind them).
 // NT: nontemporal cache loads (one head group); with several head groups
 // the tiles stay in L2 for the other groups' workgroups on the XCD.
 template <int DT, bool NT>
@@ -1727,6 +1769,8 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
       count += __popcll(bal);
     }
     if (lane == 0) *nreal = count;
+    // Placeholders past the last tile: the cache's first row, no query row.
+    if (lane < kShCtlPad) ctl[count + lane] = i32x4{0, 0, 1, -1};
   }
   __syncthreads();
   const int n = *nreal;
@@ -1734,28 +1778,24 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   if (n == 0) return;  // whole workgroup: uniform
 
   // --- Main loop ------------------------------------------------------------
-  // DMA of tile t (past the end: a re-read of the cache's first row into the
-  // unused slot, so every step issues the same loads).
-  auto dma = [&](int t) {
+  // DMA of tile t from its list entry e (past the end a placeholder: a
+  // re-read of the cache's first row into the unused slot, so every step
+  // issues the same loads).
+  // Instruction k < 8 loads latent row 8 wv + k, instruction 8 the rope
+  // bytes of rows 8 wv .. 8 wv + 7.
+  auto dma_one = [&](int t, const i32x4 e, int k) {
     char* slot = ring + (t % kShBufs) * kShTileBytes;
-    int64_t base = 0;
-    int nv = 1;
-    if (t < n) {
-      const i32x4 e = ctl[t];
-      base = static_cast<int64_t>(static_cast<uint32_t>(e[0])) | (static_cast<int64_t>(e[1]) << 32);
-      nv = e[2] & 0xFFFF;
-    }
+    const int64_t base = static_cast<int64_t>(static_cast<uint32_t>(e[0])) | (static_cast<int64_t>(e[1]) << 32);
+    const int nv = e[2] & 0xFFFF;
     const char* tb = cache + 2 * base;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    if (k < 8) {
       const int R = 8 * wv + k;
       const int Rc = R < nv ? R : nv - 1;
       const char* src = tb + Rc * kShRowBytes + 16 * lane;
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
                                        (__attribute__((address_space(3))) void*)(slot + R * kShLatStride), 16, 0,
                                        NT ? 2 : 0);
-    }
-    {
+    } else {
       const int R = 8 * wv + (lane >> 3);
       const int Rc = R < nv ? R : nv - 1;
       const int c = (lane & 7) ^ ((R >> 1) & 7);
@@ -1764,6 +1804,10 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
                                        (__attribute__((address_space(3))) void*)(slot + kShLatBytes + wv * 1024), 16,
                                        0, NT ? 2 : 0);
     }
+  };
+  auto dma = [&](int t, const i32x4 e) {
+#pragma unroll
+    for (int k = 0; k < kShDma; ++k) dma_one(t, e, k);
   };
   // This lane's head's query, 18 chunks of 32 elements ([q | q_rope]).
   // Heads past H read head 0's query (never stored; no select on the loaded
@@ -1792,18 +1836,26 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   // no register load is pending when the loop starts (the compiler would
   // otherwise wait for every load in flight, the whole ring, in every step).
 #pragma unroll
-  for (int t = 0; t < kShBufs - 1; ++t) dma(t);
+  for (int t = 0; t < kShBufs - 1; ++t) dma(t, ctl[t]);
   load_q(ctl[0][3]);
+  // List entries are read one step ahead of their use (an LDS round trip
+  // at the top of each step would sit on the critical path): e_cur = tile
+  // t, r_nxt = row of tile t + 1, e_dma = tile t + kShBufs - 1.
+  i32x4 e_cur = ctl[0], e_dma = ctl[kShBufs - 1];
+  int r_nxt = ctl[1][3];
   wait_vm_all();
   int row = -1;
   for (int t = 0; t < n; ++t) {
     dma_ring_barrier<(kShBufs - 2) * kShDma>();  // tile t in LDS; tile t-1 done by every wave
-    dma(t + kShBufs - 1);                         // into tile t-1's slot
-    const i32x4 e = ctl[t];
+    const i32x4 ed = e_dma;                       // tile t + kShBufs - 1, into tile t-1's slot
+    const i32x4 e = e_cur;
+    const int r1 = r_nxt;
+    e_cur = ctl[t + 1];
+    r_nxt = ctl[t + 2][3];
+    e_dma = ctl[t + kShBufs];
     const int nv = e[2] & 0xFFFF;
     const bool whole = (e[2] >> 16) != 0;
     const int r = e[3];
-    const int r1 = t + 1 < n ? ctl[t + 1][3] : -1;
     const bool last = r1 != r;
     if (r != row) {
       row = r;
@@ -1842,17 +1894,35 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
         }
         s[0] = Ops::mma32(a0, qv[c], s[0]);
         s[1] = Ops::mma32(a1, qv[c], s[1]);
+        // The next tile's DMA, one instruction per chunk: issued together
+        // after the barrier, the four waves' loads queue on the CU's load
+        // path for about as long as the QK products take.
+        if (c < kShDma) dma_one(t + kShBufs - 1, ed, c);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 
+    // The first PV operand reads, in flight during the softmax (inline asm,
+    // TrRead: the builtin form would wait for the next tiles' DMA, issued
+    // during QK).
+    const uint32_t trb = lds_addr(slot) + (4 * q4 + (r16 >> 2)) * kShLatStride + 8 * (r16 & 3);
+    u32x2 av[kShPvAhead][2];
+    static_for<0, kShPvAhead>([&](auto c) {
+      constexpr int cb = decltype(c)::value;
+      TrRead<32 * cb>::issue(trb, av[cb][0]);
+      TrRead<16 * kShLatStride + 32 * cb>::issue(trb, av[cb][1]);
+    });
+
     // Softmax over the tile's 32 tokens: lane holds tokens 16 tb + 4 q4 + i.
+    // Rows past the visible count hold a copy of the last visible row (the
+    // DMA clamps them), so their scores cannot raise the max: only their
+    // weights are zeroed, and only in a tile with such rows.
     float x[2][4];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
       const f32x4 st = s[tb];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[tb][i] = 16 * tb + 4 * q4 + i < nv ? st[i] * p.sl2 : -INFINITY;
+      for (int i = 0; i < 4; ++i) x[tb][i] = st[i] * p.sl2;
     }
     float mx = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
                      fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
@@ -1873,6 +1943,10 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
       float pr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(x[tb][i] - m_use);
+      if (nv < kShTokens) {  // uniform
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = 16 * tb + 4 * q4 + i < nv ? pr[i] : 0.f;
+      }
       pb[tb] = u32x2{Ops::pack2(pr[0], pr[1]), Ops::pack2(pr[2], pr[3])};
       pbl[tb] = u32x4{pb[tb][0], pb[tb][1], 0u, 0u};
       if constexpr (Ops::kSplitWeights) {
@@ -1897,27 +1971,22 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
     // Reads run kShPvAhead blocks ahead of their MFMAs.
     const u32x4 bhi = {pb[0][0], pb[0][1], pb[1][0], pb[1][1]};
     const u32x4 blo = {pbl[0][2], pbl[0][3], pbl[1][2], pbl[1][3]};
-    const char* trb = slot + (4 * q4 + (r16 >> 2)) * kShLatStride + 8 * (r16 & 3);
-    auto tr_block = [&](int cb) {
-      using lds_v4s = __attribute__((address_space(3))) s16x4;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(trb + 32 * cb));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(trb + 16 * kShLatStride + 32 * cb));
-      const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
-      const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
-      return u32x4{l2[0], l2[1], h2[0], h2[1]};
-    };
-    u32x4 av[kShPvAhead];
-#pragma unroll
-    for (int cb = 0; cb < kShPvAhead; ++cb) av[cb] = tr_block(cb);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int cb = 0; cb < kShColBlocks; ++cb) {
-      const u32x4 a = av[cb % kShPvAhead];
-      if (cb + kShPvAhead < kShColBlocks) av[cb % kShPvAhead] = tr_block(cb + kShPvAhead);
+    static_for<0, kShColBlocks>([&](auto c) {
+      constexpr int cb = decltype(c)::value;
+      constexpr int j = cb % kShPvAhead;
+      // LDS reads issued after this block's two: the later blocks in flight.
+      constexpr int later = 2 * (kShColBlocks - 1 - cb < kShPvAhead - 1 ? kShColBlocks - 1 - cb : kShPvAhead - 1);
+      lds_wait_tied<later>(av[j][0], av[j][1]);
+      const u32x4 a = {av[j][0][0], av[j][0][1], av[j][1][0], av[j][1][1]};
+      if constexpr (cb + kShPvAhead < kShColBlocks) {
+        TrRead<32 * (cb + kShPvAhead)>::issue(trb, av[j][0]);
+        TrRead<16 * kShLatStride + 32 * (cb + kShPvAhead)>::issue(trb, av[j][1]);
+      }
       acc[cb] = Ops::mma32(a, bhi, acc[cb]);
       if constexpr (Ops::kSplitWeights) acc[cb] = Ops::mma32(a, blo, acc[cb]);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
 
     if (last) {
       // This wave's heads for the row segment, then the next row's query;
