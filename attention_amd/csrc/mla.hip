@@ -104,12 +104,40 @@ __global__ __launch_bounds__(64) void latent_write_elem_kernel(LatentWriteParams
 //   value:  W_h(k, o) = w[h, o, k]   (w [H, Dv, Dc], k = Dc, o = Dv)
 // fp32 accumulation, one rounding to the dtype (mla.cu:21-26).
 
+// Half-precision partial rows (shared-tile and wave kernels): {m, l, s0, s1,
+// s2, s3, 0, 0} in fp32, then Dc = 512 fp16 values acc / s_k for latent
+// columns [128 k, 128 k + 128), s_k the block's largest |acc| for the head.
+constexpr int kHalfHeader = 8;                         // floats before the fp16 values
+constexpr int kHalfPst = kHalfHeader + 512 / 2;        // floats per partial row
+
+// One step of the log-sum-exp fold of partial rows (online_softmax.cuh:17-24)
+// as every merge here runs it: state (M, L, acc[N]) absorbs the partial
+// (ms, ls, v[N]).  Shared so that a merge inside another kernel rounds
+// exactly as the merge kernel does.
+template <int N>
+__device__ __forceinline__ void lse_fold(float& M, float& L, float (&acc)[N], float ms, float ls, const float (&v)[N]) {
+  const float mn = fmaxf(M, ms);
+  const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
+  const float bw = fast_exp2((ms - mn) * kLog2e);
+  // Explicit fused multiply-adds: the same rounding whichever kernel inlines it.
+  L = __builtin_fmaf(a, L, bw * ls);
+#pragma unroll
+  for (int j = 0; j < N; ++j) acc[j] = __builtin_fmaf(a, acc[j], bw * v[j]);
+  M = mn;
+}
+
 struct ProjParams {
   const void* x;
   const void* w;
   void* out;
   int64_t rows;
   int H, di, dout;
+  // Value projection with the merge of split attention rows folded in
+  // (MERGE): the half-precision partials, their row spans and tile count.
+  const float* part = nullptr;
+  const int* meta = nullptr;
+  const int64_t* gtotal = nullptr;
+  int wgs = 0;
 };
 
 // grid (ceil(dout/128), H, ceil(rows/(16 RT))), block 256.  The workgroup
@@ -124,14 +152,24 @@ struct ProjParams {
 // contiguous) is loaded as is.  Small batches take RT = 1 (four times the
 // workgroups; the per-head weights are then re-read from L2) and, for a long
 // k range, PAIR = 4 (one round trip for a wave's loads).
-template <int DT, bool ABSORB, int RT, int PAIR>
+//
+// MERGE (value projection of mla_decode, RT = 1, di = 512): the x rows of
+// attention rows split across workgroups are merged here from their
+// half-precision partials (lse_fold in the merge kernel's order, rounded to
+// the input dtype as the merge kernel rounds them) into an LDS tile, the
+// other rows copied there from x; the weight loads of the first chunk group
+// are issued before, so their round trip overlaps the merge's.
+template <int DT, bool ABSORB, int RT, int PAIR, bool MERGE = false>
 __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   using E = Elem<DT>;
   using Ops = MfmaOps<DT>;
   using S = typename E::S;
   constexpr int kPair = PAIR;
+  static_assert(!MERGE || (!ABSORB && RT == 1), "the merged input serves the value projection's 16-row tiles");
+  constexpr int kXtStride = 512 + 8;  // merged tile row (elements): 16 bytes of padding, no bank conflicts
   __shared__ f32x4 red[4][8][64];
   __shared__ __align__(16) S stage[16][128];
+  __shared__ __align__(16) S xt[MERGE ? 16 : 1][MERGE ? kXtStride : 8];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r16 = lane & 15, q4 = lane >> 4;
   const int h = blockIdx.y;
@@ -147,30 +185,114 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[rt][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto load_w = [&](int c, u32x4 (&bop)[8]) {
+    const int k0 = 32 * c + 8 * q4;
+    if constexpr (ABSORB) {
+      u32x4 raw[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        raw[t] = *reinterpret_cast<const u32x4*>(wb + ((static_cast<int64_t>(h) * p.di + k0 + t) * p.dout + col) * 2);
+      transpose8x8_b16(raw, bop);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        bop[e] = *reinterpret_cast<const u32x4*>(wb + ((static_cast<int64_t>(h) * p.dout + col + e) * p.di + k0) * 2);
+    }
+  };
+  u32x4 bop0[kPair][8];  // MERGE: the weights of the first chunk group, loaded before the merge
+  if constexpr (MERGE) {
+#pragma unroll
+    for (int u = 0; u < kPair; ++u) load_w(min(kPair * wv + u, nch - 1), bop0[u]);
+    // Thread (row, seg) builds columns 32 seg .. 32 seg + 31 of tile row `row`.
+    const int row = static_cast<int>(threadIdx.x) >> 4, seg = static_cast<int>(threadIdx.x) & 15;
+    int64_t rr = r0 + row;
+    if (rr >= p.rows) rr = p.rows - 1;
+    const int first = p.meta[2 * rr], nwg = p.meta[2 * rr + 1];
+    u32x4 v16[4];
+    if (nwg < 2 || first < 0 || first + nwg > p.wgs) {
+      // Written whole by the attention kernel (or zero-filled): as stored.
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v16[i] = *reinterpret_cast<const u32x4*>(xb + ((rr * p.H + h) * p.di + 32 * seg + 8 * i) * 2);
+    } else {
+      const int64_t G = *p.gtotal;
+      auto present = [&](int k) {
+        return static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
+      };
+      const int64_t stride = static_cast<int64_t>(p.H) * kHalfPst;
+      const float* base = p.part + (rr * p.H + h) * static_cast<int64_t>(kHalfPst);
+      constexpr int kBatch = 8;
+      float M = -INFINITY, L = 0.f, am[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) am[j] = 0.f;
+      for (int c = 0; c < nwg; c += kBatch) {
+        float ms[kBatch], ls[kBatch], sc[kBatch];
+        f16x8 hv[kBatch][4];
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+          ms[t] = -INFINITY;
+          ls[t] = 0.f;
+          sc[t] = 0.f;
+          const int k = first + c + t;
+          if (c + t < nwg && present(k)) {
+            const float* pr = base + k * stride;
+            const f32x4 hd = *reinterpret_cast<const f32x4*>(pr);
+            const f32x4 hs = *reinterpret_cast<const f32x4*>(pr + 4);
+            ms[t] = hd[0];
+            ls[t] = hd[1];
+            const int kb = seg >> 2;  // 128-column block
+            sc[t] = kb == 0 ? hd[2] : kb == 1 ? hd[3] : kb == 2 ? hs[0] : hs[1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              hv[t][i] = *reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(pr + kHalfHeader) + 64 * seg + 16 * i);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hv[t][i] = f16x8{};
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+          if (ls[t] == 0.f) continue;  // absent or empty partial
+          float v[32];
+#pragma unroll
+          for (int j = 0; j < 32; ++j) v[j] = static_cast<float>(hv[t][j / 8][j % 8]) * sc[t];
+          lse_fold(M, L, am, ms[t], ls[t], v);
+        }
+      }
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        S o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = E::from_f(am[8 * i + j] * inv);
+        v16[i] = __builtin_bit_cast(u32x4, o);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&xt[row][32 * seg + 8 * i]) = v16[i];
+    __syncthreads();
+  }
   for (int c0 = kPair * wv; c0 < nch; c0 += 4 * kPair) {
     u32x4 bop[kPair][8], a[kPair][RT];
 #pragma unroll
     for (int u = 0; u < kPair; ++u) {
       const int c = min(c0 + u, nch - 1);  // a missing second chunk repeats the first, weight 0 below
       const int k0 = 32 * c + 8 * q4;
-      if constexpr (ABSORB) {
-        u32x4 raw[8];
+      if (MERGE && c0 == kPair * wv) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          raw[t] = *reinterpret_cast<const u32x4*>(
-              wb + ((static_cast<int64_t>(h) * p.di + k0 + t) * p.dout + col) * 2);
-        transpose8x8_b16(raw, bop[u]);
+        for (int e = 0; e < 8; ++e) bop[u][e] = bop0[u][e];
       } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          bop[u][e] = *reinterpret_cast<const u32x4*>(
-              wb + ((static_cast<int64_t>(h) * p.dout + col + e) * p.di + k0) * 2);
+        load_w(c, bop[u]);
       }
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        int64_t row = r0 + 16 * rt + r16;
-        if (row >= p.rows) row = p.rows - 1;
-        a[u][rt] = *reinterpret_cast<const u32x4*>(xb + ((row * p.H + h) * p.di + k0) * 2);
+        if constexpr (MERGE) {
+          a[u][rt] = *reinterpret_cast<const u32x4*>(&xt[r16][k0]);
+        } else {
+          int64_t row = r0 + 16 * rt + r16;
+          if (row >= p.rows) row = p.rows - 1;
+          a[u][rt] = *reinterpret_cast<const u32x4*>(xb + ((row * p.H + h) * p.di + k0) * 2);
+        }
       }
       if (c0 + u >= nch) {
 #pragma unroll
@@ -267,12 +389,6 @@ struct MlaParams {
   int64_t num_blocks;
   float sl2;        // scale * log2(e)
 };
-
-// Half-precision partial rows (shared-tile and wave kernels): {m, l, s0, s1,
-// s2, s3, 0, 0} in fp32, then Dc = 512 fp16 values acc / s_k for latent
-// columns [128 k, 128 k + 128), s_k the block's largest |acc| for the head.
-constexpr int kHalfHeader = 8;                         // floats before the fp16 values
-constexpr int kHalfPst = kHalfHeader + 512 / 2;        // floats per partial row
 
 // Two floats as fp16, round to nearest even, lo in the low half.
 __device__ __forceinline__ uint32_t pack_f16_rne(float lo, float hi) {
@@ -2112,13 +2228,7 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
 #pragma unroll
     for (int t = 0; t < kBatch; ++t) {
       if (ls[t] == 0.f) continue;  // absent or empty partial
-      const float mn = fmaxf(M, ms[t]);
-      const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
-      const float bw = fast_exp2((ms[t] - mn) * kLog2e);
-      L = a * L + bw * ls[t];
-#pragma unroll
-      for (int j = 0; j < kAcc; ++j) acc[j] = a * acc[j] + bw * v[t][j];
-      M = mn;
+      lse_fold(M, L, acc, ms[t], ls[t], v[t]);
     }
   }
   S* orow = static_cast<S*>(p.out) + wid * p.Dc;
@@ -2509,9 +2619,26 @@ hipError_t dispatch_attend_mfma(const MlaParams& prm, const AttendPlan& pl, int6
 }
 
 // Enqueues attention (+ merge) writing [R, H, Dc] of the dtype to `out`.
+// Where the stream-K MFMA kernels keep their partial rows, the tile count G
+// and the row spans `meta`, inside the partial workspace.
+struct PartialRefs {
+  float* part;
+  int64_t* gtotal;
+  int* meta;
+};
+PartialRefs partial_refs(const AttendShape& a, const AttendPlan& pl, void* part_ws) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T;
+  char* meta =
+      static_cast<char*>(part_ws) + round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * partial_stride(a, pl) * 4);
+  return {static_cast<float*>(part_ws), reinterpret_cast<int64_t*>(meta), reinterpret_cast<int*>(meta + sizeof(int64_t))};
+}
+
+// skip_merge: the caller merges the split rows itself (mla_decode's value
+// projection, MFMA kernels with half-precision partials only).
 int run_attend(const AttendShape& a, const void* q, const void* qr, const void* cache, const int32_t* table,
                const int32_t* lens, const int32_t* pos, const int32_t* idx, int causal, int64_t num_blocks,
-               float scale, void* out, void* part_ws, size_t part_bytes, const AttendPlan& pl, hipStream_t st) {
+               float scale, void* out, void* part_ws, size_t part_bytes, const AttendPlan& pl, hipStream_t st,
+               bool skip_merge = false) {
   MlaParams prm{};
   prm.q = q;
   prm.qr = qr;
@@ -2546,10 +2673,9 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
   if (need > 0 && (part_bytes < need || !part_ws || !aligned16(part_ws)))
     return mla_fail(nullptr, 0, "workspace too small for the attention partials");
   if (pl.mfma) {
-    char* meta =
-        static_cast<char*>(part_ws) + round_up256(static_cast<size_t>(pl.wgs + rows) * a.H * partial_stride(a, pl) * 4);
-    prm.gtotal = reinterpret_cast<int64_t*>(meta);
-    prm.meta = reinterpret_cast<int*>(meta + sizeof(int64_t));
+    const PartialRefs pr = partial_refs(a, pl, part_ws);
+    prm.gtotal = pr.gtotal;
+    prm.meta = pr.meta;
   }
   (void)hipGetLastError();
   hipError_t err = hipSuccess;
@@ -2592,7 +2718,7 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
     return static_cast<int>(err);
   }
   int rc = launch_status("mla_attend");
-  if (rc != QD_OK || (!pl.mfma && pl.splits == 1)) return rc;
+  if (rc != QD_OK || (!pl.mfma && pl.splits == 1) || (skip_merge && pl.mfma && half_partials(pl))) return rc;
   const int64_t mgrid = (rows * a.H + 3) / 4;
   if (pl.mfma) {
     using MergeFn = void (*)(MlaParams);
@@ -2610,6 +2736,15 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
     default: hipLaunchKernelGGL(mla_merge_kernel<QD_DTYPE_BF16>, dim3(mgrid), dim3(256), 0, st, prm); break;
   }
   return launch_status("mla_attend merge");
+}
+
+// The value projection of mla_decode with the merge of split rows folded in
+// (mla_project_mfma_kernel MERGE): the 16-row, 4-chunk-group tiling that
+// launch_project picks for small batches with di = 512.
+template <int DT>
+void launch_project_merge(const ProjParams& prm, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((prm.dout + 127) / 128), prm.H, static_cast<unsigned>((prm.rows + 15) / 16));
+  hipLaunchKernelGGL((mla_project_mfma_kernel<DT, false, 1, 4, true>), grid, dim3(256), 0, st, prm);
 }
 
 bool project_mfma_applies(int64_t rows, int di, int dout, int dtype, const void* x, const void* w,
@@ -2924,10 +3059,29 @@ int qd_mla_decode(const void* q_nope, const void* q_rope, const void* cache, con
   int rc = run_project(q_nope, w_uk, qa, rows, heads, nope_dim, latent_dim, true, dtype, flags, st);
   if (rc != QD_OK) return rc;
   if (pl.mfma && !aligned16(cache)) pl.mfma = false;
+  // The merge of split rows folded into the value projection when it runs
+  // the 16-row MFMA tiling (launch_project's choice for small batches).
+  const int64_t fill = 2 * static_cast<int64_t>(device_cus());
+  const bool fuse = pl.mfma && half_partials(pl) && latent_dim == 512 && (flags & QD_FLAG_FORCE_GENERIC) == 0 &&
+                    project_mfma_applies(rows, latent_dim, value_dim, dtype, latent, w_uv, out) &&
+                    (rows < 64 || (value_dim + 127) / 128 * heads * ((rows + 63) / 64) < fill) &&
+                    (rows + 15) / 16 <= 65535;
   rc = run_attend(a, qa, q_rope, cache, block_table, lengths, positions, indices, causal, num_blocks, scale, latent,
-                  ws + lay.part, workspace_bytes - lay.part, pl, st);
+                  ws + lay.part, workspace_bytes - lay.part, pl, st, fuse);
   if (rc != QD_OK) return rc;
-  return run_project(latent, w_uv, out, rows, heads, latent_dim, value_dim, false, dtype, flags, st);
+  if (!fuse) return run_project(latent, w_uv, out, rows, heads, latent_dim, value_dim, false, dtype, flags, st);
+  ProjParams prm{latent, w_uv, out, rows, heads, latent_dim, value_dim};
+  const PartialRefs refs = partial_refs(a, pl, ws + lay.part);
+  prm.part = refs.part;
+  prm.meta = refs.meta;
+  prm.gtotal = refs.gtotal;
+  prm.wgs = pl.wgs;
+  (void)hipGetLastError();
+  if (dtype == QD_DTYPE_BF16)
+    launch_project_merge<QD_DTYPE_BF16>(prm, st);
+  else
+    launch_project_merge<QD_DTYPE_F16>(prm, st);
+  return launch_status("mla_decode value projection");
 }
 
 }  // extern "C"
