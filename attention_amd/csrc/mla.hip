@@ -216,8 +216,12 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
         v16[i] = *reinterpret_cast<const u32x4*>(xb + ((rr * p.H + h) * p.di + 32 * seg + 8 * i) * 2);
     } else {
       const int64_t G = *p.gtotal;
+      // Workgroup k's range [k G / wgs, (k + 1) G / wgs) holds a partial row
+      // when it is not empty, which it never is for G >= wgs (skips two
+      // 64-bit divisions per slot and lane).
+      const bool dense = G >= p.wgs;
       auto present = [&](int k) {
-        return static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
+        return dense || static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
       };
       const int64_t stride = static_cast<int64_t>(p.H) * kHalfPst;
       const float* base = p.part + (rr * p.H + h) * static_cast<int64_t>(kHalfPst);
@@ -2185,8 +2189,11 @@ __global__ __launch_bounds__(256) void mla_merge_sk_kernel(MlaParams p) {
   const int64_t stride = static_cast<int64_t>(p.H) * p.pst;
   const float* base = p.part + (r * p.H + h) * static_cast<int64_t>(p.pst);  // slot k: + (k) * stride
   const int aoff = p.pst - p.Dc;                                             // accumulator offset
+  // Workgroup k's range [k G / wgs, (k + 1) G / wgs) holds a partial row
+  // when it is not empty, which it never is for G >= wgs.
+  const bool dense = G >= p.wgs;
   auto present = [&](int k) {
-    return static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
+    return dense || static_cast<int64_t>(k) * G / p.wgs != static_cast<int64_t>(k + 1) * G / p.wgs;
   };
   float M = -INFINITY, L = 0.f;
   float acc[kAcc];
