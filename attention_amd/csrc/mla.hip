@@ -157,8 +157,8 @@ struct ProjParams {
 // attention rows split across workgroups are merged here from their
 // half-precision partials (lse_fold in the merge kernel's order, rounded to
 // the input dtype as the merge kernel rounds them) into an LDS tile, the
-// other rows copied there from x; the weight loads of the first chunk group
-// are issued before, so their round trip overlaps the merge's.
+// other rows copied there from x.  (Issuing the first weight loads before
+// the merge measured no faster and held 128 more registers.)
 template <int DT, bool ABSORB, int RT, int PAIR, bool MERGE = false>
 __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   using E = Elem<DT>;
@@ -199,10 +199,7 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
         bop[e] = *reinterpret_cast<const u32x4*>(wb + ((static_cast<int64_t>(h) * p.dout + col + e) * p.di + k0) * 2);
     }
   };
-  u32x4 bop0[kPair][8];  // MERGE: the weights of the first chunk group, loaded before the merge
   if constexpr (MERGE) {
-#pragma unroll
-    for (int u = 0; u < kPair; ++u) load_w(min(kPair * wv + u, nch - 1), bop0[u]);
     // Thread (row, seg) builds columns 32 seg .. 32 seg + 31 of tile row `row`.
     const int row = static_cast<int>(threadIdx.x) >> 4, seg = static_cast<int>(threadIdx.x) & 15;
     int64_t rr = r0 + row;
@@ -282,12 +279,7 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
     for (int u = 0; u < kPair; ++u) {
       const int c = min(c0 + u, nch - 1);  // a missing second chunk repeats the first, weight 0 below
       const int k0 = 32 * c + 8 * q4;
-      if (MERGE && c0 == kPair * wv) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bop[u][e] = bop0[u][e];
-      } else {
-        load_w(c, bop[u]);
-      }
+      load_w(c, bop[u]);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         if constexpr (MERGE) {
