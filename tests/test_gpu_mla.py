@@ -288,6 +288,13 @@ def test_latent_kv_write_bitwise(gpu, dtype, dc, dr):
 
 DECODE_SHAPES = [
     ("deepseek-h128-t1", dict(lengths=[33, 700, 2049], q_len=1, heads=128, block_size=64, dtype=torch.bfloat16)),
+    # One query per row, so the C ABI's fused op runs: the value projection
+    # merges the split rows itself (wave kernel; shared-tile kernel in fp16
+    # with every workgroup range non-empty).
+    ("deepseek-h16-t1-b40", dict(lengths=[(37 * i * i + 11 * i) % 3001 + 1 for i in range(40)], q_len=1, heads=16,
+                                 block_size=64, dtype=torch.bfloat16)),
+    ("deepseek-h128-t1-fp16-long", dict(lengths=[3000, 2500, 1, 4000, 2047, 64, 3333, 1800], q_len=1, heads=128,
+                                        block_size=64, dtype=torch.float16)),
     ("deepseek-h16-t2", dict(lengths=[5, 1000], q_len=2, heads=16, block_size=64, dtype=torch.bfloat16)),
     ("ref-bench-bf16", dict(lengths=[4096], q_len=1, heads=4, nope_dim=32, latent_dim=64, rope_dim=16,
                             value_dim=32, block_size=16, dtype=torch.bfloat16)),
