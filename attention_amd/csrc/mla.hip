@@ -1135,8 +1135,7 @@ struct WaveLayout {
 };
 
 __host__ __device__ constexpr size_t mla_wave_lds_bytes(int nb, int rc) {
-  return 5 * static_cast<size_t>(kSubTokens) * (2 * (128 * nb + 32 * rc) + 32)  // wave tiles, query
-         + 4 * 64 * 32 * 4                                                      // merge exchange
+  return 5 * static_cast<size_t>(kSubTokens) * (2 * (128 * nb + 32 * rc) + 32)  // wave tiles, query; merge exchange
          + 4 * 16 * 2 * 4                                                       // merge m, l
          + static_cast<size_t>(kWaveRows) * (4 + 4 + 8)                         // row tiles, ends, prefix
          + static_cast<size_t>(kWaveListTiles) * 16                             // tiles {base, rows, row}
@@ -1206,8 +1205,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
   char* qbuf = smem + 4 * Lay::kBuf;                                      // the current row's query
   // [wave][e][lane] f32x4: consecutive lanes at consecutive 16 bytes, so
   // the exchange's LDS accesses are free of bank conflicts.
-  float* red = reinterpret_cast<float*>(smem + 5 * Lay::kBuf);          // [4][8][64] x 4
-  float* ml = red + 4 * 64 * 32;                                          // [4][16][2]
+  float* ml = reinterpret_cast<float*>(smem + 5 * Lay::kBuf);           // [4][16][2]
   int* rt = reinterpret_cast<int*>(ml + 4 * 16 * 2);                      // [rows] tiles
   int* re = rt + kWaveRows;                                               // [rows] visible end
   int64_t* incl = reinterpret_cast<int64_t*>(re + kWaveRows);            // [rows] prefix of tiles
@@ -1427,45 +1425,59 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
     const float sc = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
     const int64_t first_tile = incl[r] - rt[r];
     const bool whole = first_tile >= g0 && incl[r] <= g1;
+    // Two rounds of two 128-column blocks.  Every wave deposits its scaled
+    // blocks 2k and 2k + 1 (16 KB) in the tile buffers, idle during the
+    // merge (xr: [wave][8 jb + e][lane] f32x4, lane-contiguous); then wave v
+    // sums half e = 4 (v % 2) .. + 3 of block 2k + v / 2, so all four sum at
+    // once.  The block's fp16 scale is the larger of the two halves' |max|,
+    // exchanged through ml (free once every wave has read M and L).
+    static_assert(NB == 4, "two rounds of two blocks");
+    static_assert(4 * 16 * 64 * 16 <= 4 * Lay::kBuf, "the exchange fits in the four tile buffers");
+    float* xr = reinterpret_cast<float*>(smem);
+    const int eh = 4 * (wv & 1);
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) {
-      // Every wave deposits its scaled block bb; wave bb % 4 sums them.
+    for (int k = 0; k < 2; ++k) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<f32x4*>(red + 4 * ((wv * 8 + e) * 64 + lane)) = acc[bb][e] * sc;
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<f32x4*>(xr + 4 * ((wv * 16 + 8 * jb + e) * 64 + lane)) = acc[2 * k + jb][e] * sc;
       lds_barrier();
-      if (wv == bb % 4 && head_ok) {
-        f32x4 o[8];
+      const int bb = 2 * k + (wv >> 1);
+      f32x4 o[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          o[e] = *reinterpret_cast<const f32x4*>(red + 4 * ((0 * 8 + e) * 64 + lane));
+      for (int e = 0; e < 4; ++e) {
+        const int j = 8 * (wv >> 1) + eh + e;
+        o[e] = *reinterpret_cast<const f32x4*>(xr + 4 * ((0 * 16 + j) * 64 + lane));
 #pragma unroll
-          for (int v = 1; v < 4; ++v) o[e] += *reinterpret_cast<const f32x4*>(red + 4 * ((v * 8 + e) * 64 + lane));
-        }
+        for (int v = 1; v < 4; ++v) o[e] += *reinterpret_cast<const f32x4*>(xr + 4 * ((v * 16 + j) * 64 + lane));
+      }
+      float amax = 0.f;
+      if (!whole) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o[e][0]), fabsf(o[e][1])), fmaxf(fabsf(o[e][2]), fabsf(o[e][3]))));
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        if (q4 == 0) ml[wv * 16 + r16] = amax;
+      }
+      lds_barrier();  // every wave has read xr (the next round rewrites it) and written its half's max
+      if (head_ok) {
         if (whole) {
           const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
           S* orow = static_cast<S*>(p.out) + (static_cast<int64_t>(r) * p.H + h) * Lay::kDc;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            uint32_t wd[4];
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) wd[e / 2] = Ops::pack2(o[e][i] * inv, o[e + 1][i] * inv);
-            *reinterpret_cast<u32x4*>(orow + 128 * bb + 32 * q4 + 8 * i) = u32x4{wd[0], wd[1], wd[2], wd[3]};
-          }
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x2*>(orow + 128 * bb + 32 * q4 + 8 * i + eh) =
+                u32x2{Ops::pack2(o[0][i] * inv, o[1][i] * inv), Ops::pack2(o[2][i] * inv, o[3][i] * inv)};
         } else {
           // Half-precision partial row (kHalfHeader): block bb as fp16
-          // values o / s_bb, s_bb the block's largest |o| for the head (the
-          // 4 lanes q4 of r16 hold the block).
-          float amax = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o[e][0]), fabsf(o[e][1])), fmaxf(fabsf(o[e][2]), fabsf(o[e][3]))));
-          amax = fmaxf(amax, __shfl_xor(amax, 16));
-          amax = fmaxf(amax, __shfl_xor(amax, 32));
-          const float sbb = amax > 0.f ? amax : 1.f;
+          // values o / s_bb, s_bb the block's largest |o| for the head.
+          const float sbb0 = fmaxf(amax, ml[(wv ^ 1) * 16 + r16]);
+          const float sbb = sbb0 > 0.f ? sbb0 : 1.f;
           const float isc = 1.f / sbb;
           float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kHalfPst);
-          if (q4 == 0) {
+          if (q4 == 0 && eh == 0) {
             if (bb == 0) {
               pr[0] = M == -INFINITY ? -INFINITY : M * kLn2;
               pr[1] = Lt;
@@ -1474,19 +1486,16 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
             }
             pr[2 + bb] = sbb;
           }
-          // Lane (r16, q4), row i: columns 128 bb + 32 q4 + 8 i + e, e = 0..7.
-          char* pa = reinterpret_cast<char*>(pr + kHalfHeader) + 2 * (128 * bb + 32 * q4);
+          // Lane (r16, q4), row i: columns 128 bb + 32 q4 + 8 i + eh + e, e = 0..3.
+          char* pa = reinterpret_cast<char*>(pr + kHalfHeader) + 2 * (128 * bb + 32 * q4 + eh);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            uint32_t wd[4];
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) wd[e / 2] = pack_f16_rne(o[e][i] * isc, o[e + 1][i] * isc);
-            *reinterpret_cast<u32x4*>(pa + 16 * i) = u32x4{wd[0], wd[1], wd[2], wd[3]};
-          }
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x2*>(pa + 16 * i) =
+                u32x2{pack_f16_rne(o[0][i] * isc, o[1][i] * isc), pack_f16_rne(o[2][i] * isc, o[3][i] * isc)};
         }
       }
-      lds_barrier();
     }
+    lds_barrier();  // the tile buffers and ml are read; the next row may stage and merge
     // Stores pending next to the loads in flight would make every later
     // wait a full drain; drain here (row ends only) instead.
     __builtin_amdgcn_s_waitcnt(0);
