@@ -159,13 +159,19 @@ struct ProjParams {
 // the input dtype as the merge kernel rounds them) into an LDS tile, the
 // other rows copied there from x.  (Issuing the first weight loads before
 // the merge measured no faster and held 128 more registers.)
-template <int DT, bool ABSORB, int RT, int PAIR, bool MERGE = false>
+//
+// HC (value layout): half-width column tiles, so that small grids cover
+// every CU: workgroup x serves column blocks e = 4 (x % 2) .. + 3 of tile
+// x / 2 (columns 128 (x / 2) + 8 n + e).
+template <int DT, bool ABSORB, int RT, int PAIR, bool MERGE = false, bool HC = false>
 __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   using E = Elem<DT>;
   using Ops = MfmaOps<DT>;
   using S = typename E::S;
   constexpr int kPair = PAIR;
+  constexpr int NE = HC ? 4 : 8;  // MFMA column blocks per workgroup
   static_assert(!MERGE || (!ABSORB && RT == 1), "the merged input serves the value projection's 16-row tiles");
+  static_assert(!HC || !ABSORB, "half-width tiles serve the value layout");
   constexpr int kXtStride = 512 + 8;  // merged tile row (elements): 16 bytes of padding, no bank conflicts
   __shared__ f32x4 red[4][8][64];
   __shared__ __align__(16) S stage[16][128];
@@ -173,19 +179,20 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r16 = lane & 15, q4 = lane >> 4;
   const int h = blockIdx.y;
-  const int cbase = 128 * blockIdx.x;
+  const int cbase = 128 * static_cast<int>(HC ? blockIdx.x >> 1 : blockIdx.x);
+  const int e0 = HC ? 4 * static_cast<int>(blockIdx.x & 1) : 0;
   const int64_t r0 = 16 * RT * static_cast<int64_t>(blockIdx.z);
   const int col = min(cbase + 8 * r16, p.dout - 8);  // clamped load column
   const int nch = p.di / 32;
   const char* xb = static_cast<const char*>(p.x);
   const char* wb = static_cast<const char*>(p.w);
   S* out = static_cast<S*>(p.out);
-  f32x4 acc[RT][8];
+  f32x4 acc[RT][NE];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[rt][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto load_w = [&](int c, u32x4 (&bop)[8]) {
+    for (int e = 0; e < NE; ++e) acc[rt][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto load_w = [&](int c, u32x4 (&bop)[NE]) {
     const int k0 = 32 * c + 8 * q4;
     if constexpr (ABSORB) {
       u32x4 raw[8];
@@ -195,8 +202,8 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
       transpose8x8_b16(raw, bop);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        bop[e] = *reinterpret_cast<const u32x4*>(wb + ((static_cast<int64_t>(h) * p.dout + col + e) * p.di + k0) * 2);
+      for (int e = 0; e < NE; ++e)
+        bop[e] = *reinterpret_cast<const u32x4*>(wb + ((static_cast<int64_t>(h) * p.dout + col + e0 + e) * p.di + k0) * 2);
     }
   };
   if constexpr (MERGE) {
@@ -274,7 +281,7 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
     __syncthreads();
   }
   for (int c0 = kPair * wv; c0 < nch; c0 += 4 * kPair) {
-    u32x4 bop[kPair][8], a[kPair][RT];
+    u32x4 bop[kPair][NE], a[kPair][RT];
 #pragma unroll
     for (int u = 0; u < kPair; ++u) {
       const int c = min(c0 + u, nch - 1);  // a missing second chunk repeats the first, weight 0 below
@@ -304,7 +311,7 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[rt][e] = Ops::mma32(a[u][rt], bop[u][e], acc[rt][e]);
+        for (int e = 0; e < NE; ++e) acc[rt][e] = Ops::mma32(a[u][rt], bop[u][e], acc[rt][e]);
   }
   // The 4 waves' partial tiles are summed through LDS and the 16 x 128 output
   // tile is staged there as well, so that each lane writes 16 contiguous
@@ -312,23 +319,28 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(ProjParams p) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[wv][e][lane] = acc[rt][e];
+    for (int e = 0; e < NE; ++e) red[wv][e][lane] = acc[rt][e];
     __syncthreads();
 #pragma unroll
-    for (int ee = 0; ee < 2; ++ee) {
-      const int e = 2 * wv + ee;
+    for (int ee = 0; ee < NE / 4; ++ee) {
+      const int e = (NE / 4) * wv + ee;
       const f32x4 s = red[0][e][lane] + red[1][e][lane] + red[2][e][lane] + red[3][e][lane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) stage[4 * q4 + i][8 * r16 + e] = E::from_f(s[i]);
+      for (int i = 0; i < 4; ++i) stage[4 * q4 + i][8 * r16 + e0 + e] = E::from_f(s[i]);
     }
     __syncthreads();
     {
       const int orow = static_cast<int>(threadIdx.x) >> 4;  // 0..15
       const int oc = 8 * (static_cast<int>(threadIdx.x) & 15);
       const int64_t row = r0 + 16 * rt + orow;
-      if (row < p.rows && cbase + oc < p.dout)  // dout % 8 == 0: whole 8-column groups
-        *reinterpret_cast<u32x4*>(out + (row * p.H + h) * p.dout + cbase + oc) =
-            *reinterpret_cast<const u32x4*>(&stage[orow][oc]);
+      if (row < p.rows && cbase + oc < p.dout) {  // dout % 8 == 0: whole 8-column groups
+        if constexpr (HC)
+          *reinterpret_cast<u32x2*>(out + (row * p.H + h) * p.dout + cbase + oc + e0) =
+              *reinterpret_cast<const u32x2*>(&stage[orow][oc + e0]);
+        else
+          *reinterpret_cast<u32x4*>(out + (row * p.H + h) * p.dout + cbase + oc) =
+              *reinterpret_cast<const u32x4*>(&stage[orow][oc]);
+      }
     }
     __syncthreads();
   }
@@ -2749,10 +2761,18 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
 // The value projection of mla_decode with the merge of split rows folded in
 // (mla_project_mfma_kernel MERGE): the 16-row, 4-chunk-group tiling that
 // launch_project picks for small batches with di = 512.
+// Half-width column tiles when full ones would leave CUs idle (mla-h16:
+// 128 workgroups; each tile's rows are then merged twice, once per half).
 template <int DT>
 void launch_project_merge(const ProjParams& prm, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((prm.dout + 127) / 128), prm.H, static_cast<unsigned>((prm.rows + 15) / 16));
-  hipLaunchKernelGGL((mla_project_mfma_kernel<DT, false, 1, 4, true>), grid, dim3(256), 0, st, prm);
+  const int64_t col_tiles = (prm.dout + 127) / 128;
+  const int64_t row_tiles = (prm.rows + 15) / 16;
+  const bool half = col_tiles * prm.H * row_tiles < device_cus();
+  const dim3 grid(static_cast<unsigned>(col_tiles * (half ? 2 : 1)), prm.H, static_cast<unsigned>(row_tiles));
+  if (half)
+    hipLaunchKernelGGL((mla_project_mfma_kernel<DT, false, 1, 4, true, true>), grid, dim3(256), 0, st, prm);
+  else
+    hipLaunchKernelGGL((mla_project_mfma_kernel<DT, false, 1, 4, true>), grid, dim3(256), 0, st, prm);
 }
 
 bool project_mfma_applies(int64_t rows, int di, int dout, int dtype, const void* x, const void* w,
