@@ -2801,9 +2801,17 @@ void launch_project(const ProjParams& prm, bool absorb, bool mfma, hipStream_t s
         else if (long_k) go(mla_project_mfma_kernel<DT, true, 1, 4>);
         else go(mla_project_mfma_kernel<DT, true, 1, 1>);
       } else {
-        if (!small) go(mla_project_mfma_kernel<DT, false, 4, 2>);
-        else if (long_k) go(mla_project_mfma_kernel<DT, false, 1, 4>);
-        else go(mla_project_mfma_kernel<DT, false, 1, 1>);
+        if (!small) {
+          go(mla_project_mfma_kernel<DT, false, 4, 2>);
+        } else if (long_k && col_tiles * prm.H * ((prm.rows + 15) / 16) < device_cus()) {
+          // Half-width column tiles: twice the workgroups (same arithmetic).
+          const dim3 hgrid(static_cast<unsigned>(2 * col_tiles), prm.H, static_cast<unsigned>((prm.rows + 15) / 16));
+          hipLaunchKernelGGL((mla_project_mfma_kernel<DT, false, 1, 4, false, true>), hgrid, dim3(256), 0, st, prm);
+        } else if (long_k) {
+          go(mla_project_mfma_kernel<DT, false, 1, 4>);
+        } else {
+          go(mla_project_mfma_kernel<DT, false, 1, 1>);
+        }
       }
       return;
     }
