@@ -295,6 +295,10 @@ DECODE_SHAPES = [
                                  block_size=64, dtype=torch.bfloat16)),
     ("deepseek-h128-t1-fp16-long", dict(lengths=[3000, 2500, 1, 4000, 2047, 64, 3333, 1800], q_len=1, heads=128,
                                         block_size=64, dtype=torch.float16)),
+    # 256 rows x 128 heads: the value projection takes 64-row tiles, so the
+    # fused op runs the merge kernel and the plain projection.
+    ("deepseek-h128-t1-b256", dict(lengths=[(13 * i) % 97 + 1 for i in range(256)], q_len=1, heads=128,
+                                   block_size=64, dtype=torch.bfloat16)),
     ("deepseek-h16-t2", dict(lengths=[5, 1000], q_len=2, heads=16, block_size=64, dtype=torch.bfloat16)),
     ("ref-bench-bf16", dict(lengths=[4096], q_len=1, heads=4, nope_dim=32, latent_dim=64, rope_dim=16,
                             value_dim=32, block_size=16, dtype=torch.bfloat16)),
