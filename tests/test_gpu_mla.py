@@ -293,6 +293,8 @@ DECODE_SHAPES = [
     # with every workgroup range non-empty).
     ("deepseek-h16-t1-b40", dict(lengths=[(37 * i * i + 11 * i) % 3001 + 1 for i in range(40)], q_len=1, heads=16,
                                  block_size=64, dtype=torch.bfloat16)),
+    ("deepseek-h16-t1-fp16-b20", dict(lengths=[(53 * i + 7) % 2500 + 1 for i in range(20)], q_len=1, heads=16,
+                                      block_size=64, dtype=torch.float16)),
     ("deepseek-h128-t1-fp16-long", dict(lengths=[3000, 2500, 1, 4000, 2047, 64, 3333, 1800], q_len=1, heads=128,
                                         block_size=64, dtype=torch.float16)),
     # 256 rows x 128 heads: the value projection takes 64-row tiles, so the
