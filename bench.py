@@ -98,7 +98,7 @@ def copy_mode(args) -> None:
 def cpu_threads() -> tuple[int, dict]:
     """Threads for the CPU baseline and what they were derived from.
 
-    BASELINE.md's plan is one thread per host core (``os.cpu_count()``).  A
+    The baseline's plan is one thread per host core (``os.cpu_count()``).  A
     job on the GPU box is confined to its CPU share (its affinity mask) and
     gets ``OMP_NUM_THREADS`` set to that share, so the thread count is the
     smallest of the three: more threads than the cores the process may run
@@ -133,8 +133,8 @@ def _time_cpu(fn, repeats: int, min_s: float, max_s: float) -> list[float]:
 def cpu_baseline(case_cpu, cfg, repeats: int) -> dict:
     """Times the reference CPU path (oracle/cpu_path.py, the torch CPU ops of
     reference attention/reference/gqa.py:21-44) on the host cores: the whole
-    batch of the benchmark config, and cfg1 (BASELINE.md's mandatory
-    CPU-path config)."""
+    batch of the benchmark config, and cfg1 (the reference's own
+    CPU-runnable config, which the baseline plan requires)."""
     from oracle.cpu_path import reference_cpu_path
     from attention_amd.cases import CONFIGS, algorithmic_bytes
 
