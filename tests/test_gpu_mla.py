@@ -365,6 +365,40 @@ def test_mla_decode_matches_oracle(gpu, name, kw):
     _chain_close(got, ref, dtype, "mla_decode " + name)
 
 
+@pytest.mark.parametrize("heads,lengths", [(16, [(37 * i * i + 11 * i) % 3001 + 1 for i in range(40)]),
+                                           (128, [33, 700, 2049, 1, 1500])], ids=["wave-h16", "shared-h128"])
+def test_mla_decode_graph_capture_replays_match_eager(gpu, heads, lengths):
+    """mla_decode (fused op: absorption, latent attention with rows split
+    across workgroups, value projection merging them) captured in a HIP
+    graph: the workspace comes from the graph's pool and nothing in the op
+    clears memory, so every replay, with eager calls and synchronizations
+    between replays, equals the eager output bit for bit."""
+    say(f"mla_decode graph capture {heads} heads: replays vs eager")
+    c = _case(gpu, lengths=lengths, q_len=1, heads=heads, block_size=64, dtype=torch.bfloat16)
+    args = (c["q_nope"], c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"], c["w_uk"], c["w_uv"])
+    ref = attention_amd.mla_decode(*args)
+    o = _case(gpu, lengths=[90, 2500], q_len=1, heads=heads, block_size=64, dtype=torch.bfloat16, seed=5)
+    other = (o["q_nope"], o["q_rope"], o["cache"], o["table"], o["lens"], o["positions"], o["w_uk"], o["w_uv"])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            attention_amd.mla_decode(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = attention_amd.mla_decode(*args)
+    torch.cuda.synchronize()
+    for i in range(3):
+        say(f"graph replay {i}")
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}"
+        attention_amd.mla_decode(*other)   # eager work on the same stream between replays
+        torch.cuda.synchronize()
+
+
 def test_sparse_mla_is_mla_decode_with_indices(gpu):
     say("sparse_mla entry point")
     c = _case(gpu, lengths=[300, 64], q_len=1, heads=32, block_size=64, dtype=torch.bfloat16, num_indices=16)
