@@ -160,3 +160,37 @@ def test_kv_append_cabi_matches_op(gpu):
     assert rc == 0, cabi.error_string(rc)
     torch.cuda.synchronize()
     assert torch.equal(a_k, b_k) and torch.equal(a_v, b_v)
+
+
+def test_kv_append_graph_capture_replays(gpu):
+    """kv_append captured in a HIP graph: each replay writes the rows and
+    positions then held in the captured input buffers, so after every replay
+    (with new inputs copied in, and an eager append to other caches between
+    replays) both caches equal the oracle applied replay by replay, bit for
+    bit."""
+    say("kv_append graph capture: replays vs oracle")
+    key, value, kc, vc, table, pos = _case(7, 8, 128, 16, torch.bfloat16, seed=21)
+    dkey, dval, dkc, dvc, dtable, dpos = (x.to(gpu) for x in (key, value, kc, vc, table, pos))
+    okey, oval, okc, ovc, otable, opos = (x.to(gpu) for x in _case(3, 8, 128, 16, torch.bfloat16, seed=22))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        attention_amd.kv_append(dkey, dval, dkc, dvc, dtable, dpos)
+    torch.cuda.synchronize()
+    state_k, state_v = kc, vc
+    gen = torch.Generator().manual_seed(23)
+    for i in range(3):
+        say(f"graph replay {i}")
+        k_i = torch.randn(key.shape, generator=gen).to(key.dtype)
+        v_i = torch.randn(value.shape, generator=gen).to(value.dtype)
+        p_i = torch.randint(0, table.shape[1] * kc.shape[1], pos.shape, generator=gen, dtype=torch.int32)
+        dkey.copy_(k_i)
+        dval.copy_(v_i)
+        dpos.copy_(p_i)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref_k, ref_v = oracle_kv_append(_np(k_i), _np(v_i), _np(state_k), _np(state_v), table.numpy(), p_i.numpy())
+        assert np.array_equal(_np(dkc.cpu()), ref_k), f"replay {i}: k_cache differs from the oracle"
+        assert np.array_equal(_np(dvc.cpu()), ref_v), f"replay {i}: v_cache differs from the oracle"
+        state_k, state_v = dkc.cpu(), dvc.cpu()
+        attention_amd.kv_append(okey, oval, okc, ovc, otable, opos)   # eager work between replays
+        torch.cuda.synchronize()
