@@ -28,6 +28,11 @@ ARCH = "gfx950"
 
 HIP_LIB = os.path.join(LIB_DIR, "libqd_attention.so")
 TORCH_LIB = os.path.join(LIB_DIR, "libqd_attention_torch.so")
+# Diagnostic library, loaded only by bench.py --mode stamps / --mode read:
+# a copy of the decode kernels with per-wave timestamps (gqa_decode.hip
+# built with -DQD_STAMPS) and the streaming-read probes (stream_probe.hip).
+DIAG_LIB = os.path.join(LIB_DIR, "libqd_attention_diag.so")
+DIAG_SOURCES = ["gqa_decode", "stream_probe"]
 
 # Packed-fp32 VALU forms are disabled for every HIP compile.
 HIP_FLAGS = [
@@ -128,11 +133,29 @@ def build(verbose: bool = False, incremental: bool = False) -> None:
     os.replace(TORCH_LIB + ".tmp", TORCH_LIB)
 
 
+def build_diag(verbose: bool = False) -> None:
+    """The diagnostic library: gqa_decode.hip with -DQD_STAMPS and the
+    streaming-read probes."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    objs = [os.path.join(OBJ_DIR, f"{n}_diag.o") for n in DIAG_SOURCES]
+    with ThreadPoolExecutor(max_workers=len(objs)) as ex:
+        futs = [ex.submit(_run, [_hipcc(), *HIP_FLAGS, "-DQD_STAMPS", f"-I{INCLUDE}", "-c",
+                                 os.path.join(CSRC, f"{n}.hip"), "-o", o], verbose)
+                for n, o in zip(DIAG_SOURCES, objs)]
+        for f in futs:
+            f.result()
+    _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", DIAG_LIB + ".tmp",
+          f"-Wl,-rpath,{ROCM}/lib"], verbose)
+    os.replace(DIAG_LIB + ".tmp", DIAG_LIB)
+
+
 def build_parallel(extra: list[list[str]] | None = None, verbose: bool = False) -> None:
-    """Build the libraries and any extra independent commands concurrently."""
+    """Build the libraries (and the diagnostic one) and any extra independent
+    commands concurrently."""
     os.makedirs(LIB_DIR, exist_ok=True)
     with ThreadPoolExecutor(max_workers=4) as ex:
-        futs = [ex.submit(build, verbose)]
+        futs = [ex.submit(build, verbose), ex.submit(build_diag, verbose)]
         for cmd in extra or []:
             futs.append(ex.submit(_run, cmd, verbose))
         for f in futs:

@@ -23,6 +23,7 @@ QD_FLAG_MLA_STAGED = 2
 QD_FLAG_MLA_WAVE = 4
 QD_STAGE_DECODE, QD_STAGE_MERGE, QD_STAGE_ALL = 1, 2, 3
 QD_STAGE_VALU = 4   # measurement option: VALU math in the balanced decode kernel
+QD_STAGE_UNFUSED, QD_STAGE_FUSED = 8, 16   # measurement options: where split sequences are merged
 
 
 class TensorDesc(ctypes.Structure):
@@ -99,6 +100,8 @@ def lib():
         L.qd_validate_paged_metadata.argtypes = ([ctypes.c_void_p] * 3 + [ctypes.c_int] * 3
                                                  + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p])
         L.qd_gqa_decode_auto_info.restype = ctypes.c_int
+        L.qd_gqa_decode_auto_counter_bytes.restype = ctypes.c_size_t
+        L.qd_gqa_decode_auto_counter_bytes.argtypes = []
         L.qd_gqa_decode_auto_info.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int)] * 3
         V, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
         MSG = [ctypes.c_char_p, ctypes.c_size_t]
@@ -177,8 +180,24 @@ def auto_workspace_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pag
                                                     max_pages, dtype)
 
 
+def auto_counter_bytes() -> int:
+    """Bytes of arrival counters at the start of every automatic-path workspace."""
+    return lib().qd_gqa_decode_auto_counter_bytes()
+
+
+def auto_workspace(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, device, fill=0):
+    """A workspace for auto_launch: auto_workspace_bytes() bytes whose arrival
+    counters (the first auto_counter_bytes()) are zero, as they must be before
+    first use, and whose other bytes all hold `fill`."""
+    n = max(16, auto_workspace_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype))
+    ws = torch.full((n,), fill, dtype=torch.uint8, device=device)
+    ws[:min(n, auto_counter_bytes())].zero_()
+    return ws
+
+
 def auto_info(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype=2):
-    """(kind, waves, splits, chunk_pages); kind 1 = balanced MFMA path, 0 = split path."""
+    """(kind, waves, splits, chunk_pages); kind 2 = balanced MFMA path with the
+    fused merge, 1 = balanced MFMA path with the merge kernel, 0 = split path."""
     w, s, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     kind = lib().qd_gqa_decode_auto_info(batch, q_heads, kv_heads, head_dim, block_size, max_pages,
                                          dtype, ctypes.byref(w), ctypes.byref(s), ctypes.byref(c))
@@ -189,7 +208,8 @@ def auto_launch(q, k, v, table, lens, out, *, scale, workspace=None, stream=None
     """Calls qd_gqa_decode_auto on torch device tensors (no validation).
 
     ``workspace`` (any dtype, contiguous) must hold auto_workspace_bytes();
-    its contents need no initialization."""
+    its first auto_counter_bytes() must be zero before first use (every call
+    leaves them zero: see auto_workspace), the rest needs no initialization."""
     B, Hq, D = q.shape
     _, P, Hkv, _ = k.shape
     if stream is None:

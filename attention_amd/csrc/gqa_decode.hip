@@ -73,7 +73,32 @@ struct DecodeParams {
   float sl2;  // scale * log2(e)
   int* meta;      // stream-K path: per sequence {first workgroup, workgroups}
   int wg_waves;   // stream-K path: waves per workgroup
+  uint32_t* ctr;  // fused stream-K path: arrival counter per (sequence, kv-head), zero between calls
+#ifdef QD_STAMPS
+  uint64_t* stamps;  // diagnostic build: per-wave timestamps (stamp_wave)
+#endif
 };
+
+#ifdef QD_STAMPS
+// Diagnostic build only (-DQD_STAMPS): 8 words per wave of the stream-K
+// kernel, at stamps[(workgroup * waves + wave) * 8]: s_memrealtime (100 MHz)
+// at entry [0], after the partition search [1], at the end of streaming [2],
+// after the partial stores retired [3], after the arrival atomics returned
+// [4], after the last merge [5]; the XCD id [6]; merges done [7].
+__device__ __forceinline__ void stamp_wave(const DecodeParams& p, int slot, uint64_t value) {
+  if (p.stamps && (threadIdx.x & 63) == 0)
+    p.stamps[(static_cast<int64_t>(blockIdx.x) * p.wg_waves + (threadIdx.x >> 6)) * 8 + slot] = value;
+}
+__device__ __forceinline__ uint64_t stamp_now() { return __builtin_amdgcn_s_memrealtime(); }
+__device__ __forceinline__ uint64_t stamp_xcc() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x;
+}
+#define QD_STAMP(p, slot, value) stamp_wave((p), (slot), (value))
+#else
+#define QD_STAMP(p, slot, value) ((void)0)
+#endif
 
 // Valid tokens of a sequence: lengths are clamped to the table capacity
 // max_pages*block_size so that a length beyond the table never reads past
@@ -578,21 +603,66 @@ struct MfmaWave {
     }
   }
 
-  // Partial {m (natural-log units), l, acc[D]} of kv-head kvh0+jk, this
-  // lane's head, at w + head*head_stride (head_stride even).
-  __device__ void store_partial(const DecodeParams& p, int jk, float* w, int64_t head_stride, float l_tot) {
+  // Fused merge: a partial that would be stored in the middle of the
+  // workgroup's range waits in LDS until the range ends instead.  An sc1
+  // store completes only at the device coherence point, and the wave's
+  // next loads (the following item's K/V) count behind it in vmcnt, so a
+  // mid-range store stalled the next item's pipeline (and, through the
+  // lockstep barrier, the workgroup's).  Area per kv-head: kStashFields rows
+  // of 64 floats, field-major (lane l at column l: conflict-free).
+  static constexpr int kStashFields = 2 + 4 * DV;
+
+  __device__ void stash_partial(int jk, float* stash, float l_tot) const {
+    float* s = stash + jk * kStashFields * 64 + lane;
+    s[0] = m_run[jk] * kLn2;
+    s[64] = l_tot;
+#pragma unroll
+    for (int d = 0; d < DV; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[(2 + 4 * d + i) * 64] = acc[jk][d][i];
+  }
+
+  // Stores a stashed partial as store_partial<true> stores a live one.
+  __device__ void store_stashed(const DecodeParams& p, int jk, const float* stash, float* w,
+                                int64_t head_stride) const {
     if (r16 >= p.g) return;
+    const float* s = stash + jk * kStashFields * 64 + lane;
     w += r16 * head_stride;
-    if (q4 == 0) {
-      w[0] = m_run[jk] * kLn2;
-      w[1] = l_tot;
-    }
+    if (q4 == 0) coherent_store2(w, s[0], s[64]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float* dst = w + 2 + DV * (4 * q4 + i);
 #pragma unroll
       for (int j = 0; j < DV; j += 2)
-        *reinterpret_cast<f32x2*>(dst + j) = f32x2{acc[jk][j][i], acc[jk][j + 1][i]};
+        coherent_store2(dst + j, s[(2 + 4 * j + i) * 64], s[(2 + 4 * (j + 1) + i) * 64]);
+    }
+  }
+
+  // Partial {m (natural-log units), l, acc[D]} of kv-head kvh0+jk, this
+  // lane's head, at w + head*head_stride (head_stride even).  COH: sc1
+  // stores, for a merge by another workgroup of the same launch.
+  template <bool COH = false>
+  __device__ void store_partial(const DecodeParams& p, int jk, float* w, int64_t head_stride, float l_tot) {
+    if (r16 >= p.g) return;
+    w += r16 * head_stride;
+    if (q4 == 0) {
+      if constexpr (COH) {
+        coherent_store2(w, m_run[jk] * kLn2, l_tot);
+      } else {
+        w[0] = m_run[jk] * kLn2;
+        w[1] = l_tot;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float* dst = w + 2 + DV * (4 * q4 + i);
+#pragma unroll
+      for (int j = 0; j < DV; j += 2) {
+        if constexpr (COH)
+          coherent_store2(dst + j, acc[jk][j][i], acc[jk][j + 1][i]);
+        else
+          *reinterpret_cast<f32x2*>(dst + j) = f32x2{acc[jk][j][i], acc[jk][j + 1][i]};
+      }
     }
   }
 };
@@ -856,9 +926,10 @@ __device__ __forceinline__ int seq_groups(const DecodeParams& p, int len_raw) {
 // l == 0 (gqa_decode.cu:84-86).  Each 16-lane group (j4 = lane / 16) holds
 // one head's state, D/16 consecutive elements per lane (one vector store):
 // four heads per wave, or one head whose rows the four groups share
-// (combine_groups).  Partials come from an earlier kernel on the same
-// stream: plain loads.
-template <int D, int KB>
+// (combine_groups).  Partials from an earlier kernel on the same stream are
+// read with plain loads; COH: sc1 loads, for partials that other workgroups
+// of the same launch wrote with sc1 stores.
+template <int D, int KB, bool COH = false>
 struct MergeRows {
   static constexpr int EPL = D / 16;
   static constexpr int kBatch = KB;  // rows loaded per memory round trip
@@ -880,12 +951,14 @@ struct MergeRows {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) av[t][e] = 0.f;
     if (present) {
-      ms[t] = row[0];
-      ls[t] = row[1];
-      // Rows are D+2 floats (D even): acc is 8-byte aligned.
+      // Rows are D+2 floats (D even): every pair is 8-byte aligned.
+      const f32x2 ml = COH ? coherent_load2(row) : *reinterpret_cast<const f32x2*>(row);
+      ms[t] = ml[0];
+      ls[t] = ml[1];
 #pragma unroll
       for (int e = 0; e < EPL; e += 2) {
-        const f32x2 x = *reinterpret_cast<const f32x2*>(row + 2 + c16 * EPL + e);
+        const float* src = row + 2 + c16 * EPL + e;
+        const f32x2 x = COH ? coherent_load2(src) : *reinterpret_cast<const f32x2*>(src);
         av[t][e] = x[0];
         av[t][e + 1] = x[1];
       }
@@ -999,6 +1072,97 @@ __device__ __forceinline__ int64_t seq_cost(int groups) {
   return groups > 0 ? kSkGroupCost * groups + kSkSeqCost : 0;
 }
 
+// Fused merge of one (sequence, kv-head item) by the wave that arrived last
+// (see decode_mfma_sk_kernel): heads [h_begin, h_begin + nheads) of sequence
+// b, from the partial slots first+b .. first+b+nwg-1 written with sc1 stores
+// by the workgroups that hold the sequence.  Same fold as merge_sk_kernel
+// (SoftmaxState::merge, online_softmax.cuh:17-24; output as
+// gqa_decode.cu:84-86): four heads per pass (16 lanes each, D/16 columns
+// per lane), sc1 buffer loads addressed by one VGPR offset per lane and a
+// scalar row offset, fused_merge_rows() rows per memory round trip.
+template <int D>
+constexpr int fused_merge_rows() {
+  return D <= 128 ? 16 : 8;
+}
+
+template <int D, int DT>
+__device__ void merge_item_fused(const DecodeParams& p, int b, int h_begin, int nheads, int first, int nwg) {
+  using S = typename Elem<DT>::S;
+  constexpr int EPL = D / 16;
+  constexpr int KB = fused_merge_rows<D>();
+  const int lane = threadIdx.x & 63;
+  const int j4 = lane >> 4;
+  const int c16 = lane & 15;
+  const uint32_t slot_bytes = static_cast<uint32_t>(p.Hq) * (D + 2) * 4;
+  const float* slots = p.ws + static_cast<int64_t>(first + b) * p.Hq * (D + 2);
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(slots, static_cast<uint32_t>(nwg) * slot_bytes);
+  for (int h4 = 0; h4 < nheads; h4 += 4) {
+    const bool active = h4 + j4 < nheads;
+    const int h = h_begin + (active ? h4 + j4 : 0);
+    const uint32_t v_ml = static_cast<uint32_t>(h) * (D + 2) * 4;  // {m, l} of the lane's head
+    const uint32_t v_acc = v_ml + 8 + c16 * EPL * 4;               // its columns of acc
+    float M = -INFINITY, L = 0.f;
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+    for (int s0 = 0; s0 < nwg; s0 += KB) {
+      // Every row slot of the batch is loaded (rows past the last repeat
+      // it, unused), so the loads form one branch-free clause.
+      float ms[KB], ls[KB], av[KB][EPL];
+#pragma unroll
+      for (int t = 0; t < KB; ++t) {
+        const uint32_t so = static_cast<uint32_t>(min(s0 + t, nwg - 1)) * slot_bytes;
+        const f32x2 ml = coherent_buffer_load2(rs, v_ml, so);
+        ms[t] = ml[0];
+        ls[t] = ml[1];
+#pragma unroll
+        for (int e = 0; e < EPL; e += 2) {
+          const f32x2 x = coherent_buffer_load2(rs, v_acc + 4 * e, so);
+          av[t][e] = x[0];
+          av[t][e + 1] = x[1];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < KB; ++t) {
+        if (s0 + t >= nwg || ls[t] == 0.f) continue;
+        const float mn = fmaxf(M, ms[t]);
+        const float a = L == 0.f ? 0.f : fast_exp2((M - mn) * kLog2e);
+        const float bb = fast_exp2((ms[t] - mn) * kLog2e);
+        L = a * L + bb * ls[t];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = a * acc[e] + bb * av[t][e];
+        M = mn;
+      }
+    }
+    if (active) {
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      uint32_t wv[EPL / 2];
+#pragma unroll
+      for (int e = 0; e < EPL; e += 2)
+        wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
+      char* dst = reinterpret_cast<char*>(static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D + c16 * EPL);
+      if constexpr (EPL == 4) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
+      } else {
+#pragma unroll
+        for (int t = 0; t < EPL / 8; ++t)
+          *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+      }
+    }
+  }
+}
+
+// Arrival of this wave's item (sequence b, kv-heads kvh0..) at its counter:
+// lane 0 increments it with wrap-around at nwg - 1 (the last of the nwg
+// arrivals reads nwg - 1 and leaves 0 behind).  Returns the value read.
+__device__ __forceinline__ uint32_t arrive(const DecodeParams& p, int b, int kvh0, int nwg) {
+  uint32_t old = 0;
+  if ((threadIdx.x & 63) == 0)
+    old = __builtin_amdgcn_atomic_inc32(p.ctr + static_cast<int64_t>(b) * p.Hkv + kvh0, static_cast<uint32_t>(nwg - 1),
+                                        __ATOMIC_RELAXED, "agent");
+  return old;
+}
+
 // Balanced ("stream-K") layout.  grid: W = p.splits workgroups of
 // p.wg_waves waves; wave j of a workgroup serves kv-heads j*NKV .. j*NKV +
 // NKV-1, then the same plus wg_waves*NKV, ... so that a workgroup reads
@@ -1018,9 +1182,19 @@ __device__ __forceinline__ int64_t seq_cost(int groups) {
 // heads into slot (w + b) of the workspace (Hq*(D+2) floats per slot; the
 // slot is unique per (sequence, workgroup) because the workgroups of
 // sequence b+1 start at or after the last one of b, so W + B slots
-// suffice).  merge_sk_kernel combines the slots of every split sequence.
-// Rows of empty sequences are zero-filled by workgroup b % W.
-template <int D, int DT, int PF, int NKV, int GV = 0>
+// suffice).  Rows of empty sequences are zero-filled by workgroup b % W.
+//
+// Only the first and the last sequence of a workgroup's range can be split
+// (every sequence in between lies wholly inside the range).  The split
+// sequences are merged either by merge_sk_kernel (FUSED = false; the
+// workgroup holding a sequence's first group records its span in p.meta)
+// or here (FUSED = true): every wave stores its partials with sc1 stores,
+// and after its whole range it waits for them to retire and arrives at the
+// counter of each of its split items (sequence, kv-heads); the arrival
+// that completes a counter (the nwg-th) merges that item's heads from all
+// nwg slots and resets the counter to zero.  No wave ever waits for
+// another, and the counters are left as they were found (zero).
+template <int D, int DT, int PF, int NKV, int GV = 0, bool FUSED = false>
 __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_mfma_sk_kernel(DecodeParams p) {
   using S = typename Elem<DT>::S;
   const int lane = threadIdx.x & 63;
@@ -1030,6 +1204,8 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
   const int W = p.splits;
   const int B = p.B;
   __shared__ __align__(16) char ktile[sk_max_waves<D, NKV, GV, PF>()][KTile<D>::kBytes];
+  QD_STAMP(p, 0, stamp_now());
+  QD_STAMP(p, 6, stamp_xcc());
 
   // Prologue, one memory round trip for B <= 64*kRegChunks: every lane loads
   // the lengths of sequences c*64 + lane, and the group counts and the
@@ -1061,14 +1237,14 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
   const int64_t C = carry;
 
   // Empty sequences (no workgroup holds them): workgroup b % W writes their
-  // zero rows and a meta entry that tells merge_sk_kernel to skip them.
+  // zero rows (and, for merge_sk_kernel, a meta entry that says to skip them).
   auto zero_fill = [&](uint64_t mask, int c0) {
     while (mask) {
       const int bb = c0 + __builtin_ctzll(mask);
       mask &= mask - 1;
       S* o = static_cast<S*>(p.out) + static_cast<int64_t>(bb) * p.Hq * p.D;
       for (int i = threadIdx.x; i < p.Hq * p.D; i += 64 * nw) o[i] = Elem<DT>::from_f(0.f);
-      if (threadIdx.x == 0) {
+      if (!FUSED && threadIdx.x == 0) {
         p.meta[2 * bb] = 0;
         p.meta[2 * bb + 1] = 0;
       }
@@ -1125,6 +1301,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
     }
   }
   if (b >= B) return;  // unreachable when C is consistent
+  QD_STAMP(p, 1, stamp_now());
 
   // Workgroup whose unit range holds unit x.
   auto wg_of = [&](int64_t x) { return static_cast<int>(div_nonneg((x + 1) * Wu - 1, C)); };
@@ -1135,12 +1312,23 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
     return static_cast<int>(i < nb ? i : nb);
   };
 
-
   // GV > 0: the VALU comparison variant (ValuWave, GV heads per group).
   using Wave = std::conditional_t<GV == 0, MfmaWave<D, DT, PF, NKV>, ValuWave<D, DT, PF, (GV > 0 ? GV : 4)>>;
   Wave wv;
   wv.init_lane();
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
+  // FUSED: the split sequences of this range, {sequence, first workgroup,
+  // workgroups}; the second is used when the range ends inside a sequence.
+  int sp_b0 = -1, sp_f0 = 0, sp_n0 = 0, sp_b1 = -1, sp_f1 = 0, sp_n1 = 0;
+  bool sp_stashed = false;  // the first split sequence's partials wait in LDS
+  // This wave's stash area (dynamic LDS, FUSED only): one item per kv-head
+  // group the wave serves.
+  float* stash = nullptr;
+  if constexpr (FUSED && GV == 0) {
+    extern __shared__ __align__(16) float qd_stash[];
+    const int items = (p.Hkv + nw * NKV - 1) / (nw * NKV);
+    stash = qd_stash + static_cast<int64_t>(wid) * items * NKV * Wave::kStashFields * 64;
+  }
   while (true) {
     const int len = len_first >= 0 ? len_first : clamp_len(p, p.lens[b]);
     len_first = -1;
@@ -1150,6 +1338,10 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
     const int i1 = groups_below(c1, x0, nb);
     if (i1 > i0) {
       const bool whole = i0 == 0 && i1 == nb;
+      // The range goes on past this sequence (only its first sequence can
+      // then be split).
+      const bool mid_range = cs + seq_cost(nb) < c1;
+      if (FUSED && !whole && mid_range) sp_stashed = true;
       float* slot = p.ws + static_cast<int64_t>(w + b) * slot_floats;
       for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
         wv.begin_item(p, b, kvh0, len, i0);
@@ -1162,9 +1354,11 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
             const float l_tot = wv.total_l(j);
             if (whole)
               wv.store_direct(p, b, kvh0, j, l_tot);
+            else if (FUSED && mid_range)
+              wv.stash_partial(j, stash + ((kvh0 - wid * NKV) / (nw * NKV)) * NKV * Wave::kStashFields * 64, l_tot);
             else
-              wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
-                                               D + 2, l_tot);
+              wv.template store_partial<FUSED>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
+                                                D + 2, l_tot);
           }
         } else {
           wv.finish_item();
@@ -1174,20 +1368,68 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
             wv.store_partial(p, slot + static_cast<int64_t>(kvh0) * p.g * (D + 2));
         }
       }
-      // The workgroup holding a sequence's first group records which
-      // workgroups span it, for merge_sk_kernel (also for a whole sequence,
-      // so that nothing from an earlier call survives).
-      if (i0 == 0 && threadIdx.x == 0) {
-        const int first = wg_of(x0);
-        p.meta[2 * b] = first;
-        p.meta[2 * b + 1] = wg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
+      if constexpr (FUSED) {
+        if (!whole) {
+          const int first = wg_of(x0);
+          const int nwg = wg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
+          if (sp_b0 < 0) {
+            sp_b0 = b;
+            sp_f0 = first;
+            sp_n0 = nwg;
+          } else {
+            sp_b1 = b;
+            sp_f1 = first;
+            sp_n1 = nwg;
+          }
+        }
+      } else {
+        // The workgroup holding a sequence's first group records which
+        // workgroups span it, for merge_sk_kernel (also for a whole sequence,
+        // so that nothing from an earlier call survives).
+        if (i0 == 0 && threadIdx.x == 0) {
+          const int first = wg_of(x0);
+          p.meta[2 * b] = first;
+          p.meta[2 * b + 1] = wg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
+        }
       }
     }
     cs += seq_cost(nb);
     if (cs >= c1) break;
     do {
-      if (++b >= B) return;  // unreachable when C is consistent
-    } while (p.lens[b] <= 0);
+      ++b;
+    } while (b < B && p.lens[b] <= 0);
+    if (b >= B) break;  // unreachable when C is consistent
+  }
+  QD_STAMP(p, 2, stamp_now());
+
+  if constexpr (FUSED && GV == 0) {
+    if (sp_b0 >= 0) {
+      if (sp_stashed) {
+        float* slot0 = p.ws + static_cast<int64_t>(w + sp_b0) * slot_floats;
+        for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
+          const float* st = stash + ((kvh0 - wid * NKV) / (nw * NKV)) * NKV * Wave::kStashFields * 64;
+#pragma unroll
+          for (int j = 0; j < NKV; ++j)
+            wv.store_stashed(p, j, st, slot0 + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2), D + 2);
+        }
+      }
+      wait_memory_retired();  // this wave's sc1 partial stores are visible device-wide
+      QD_STAMP(p, 3, stamp_now());
+      int merged = 0;
+      for (int kvh0 = wid * NKV; kvh0 < p.Hkv; kvh0 += nw * NKV) {
+        // Both arrivals are issued before either result is used.
+        const uint32_t o0 = arrive(p, sp_b0, kvh0, sp_n0);
+        const uint32_t o1 = sp_b1 >= 0 ? arrive(p, sp_b1, kvh0, sp_n1) : 0u;
+        const bool last0 = __builtin_amdgcn_readfirstlane(o0) == static_cast<uint32_t>(sp_n0 - 1);
+        const bool last1 = sp_b1 >= 0 && __builtin_amdgcn_readfirstlane(o1) == static_cast<uint32_t>(sp_n1 - 1);
+        QD_STAMP(p, 4, stamp_now());
+        if (last0) merge_item_fused<D, DT>(p, sp_b0, kvh0 * p.g, NKV * p.g, sp_f0, sp_n0);
+        if (last1) merge_item_fused<D, DT>(p, sp_b1, kvh0 * p.g, NKV * p.g, sp_f1, sp_n1);
+        merged += static_cast<int>(last0) + static_cast<int>(last1);
+      }
+      QD_STAMP(p, 5, stamp_now());
+      QD_STAMP(p, 7, static_cast<uint64_t>(merged));
+    }
   }
 }
 
@@ -1420,24 +1662,28 @@ constexpr int kPrefetchDual = QD_PREFETCH_DUAL;
 // with 3 or 4 in flight and one workgroup per CU).
 constexpr int kSkWidePrefetch = 3;
 
-template <int DT>
+template <int DT, bool FUSED>
 KernelFn pick_mfma_sk(int D, int nkv, bool wide) {
-  if (wide) return decode_mfma_sk_kernel<128, DT, kSkWidePrefetch, 1>;
+  if (wide) return decode_mfma_sk_kernel<128, DT, kSkWidePrefetch, 1, 0, FUSED>;
   if (nkv == 2) {
     switch (D) {
-      case 64: return decode_mfma_sk_kernel<64, DT, kPrefetchDual, 2>;
-      default: return decode_mfma_sk_kernel<128, DT, kPrefetchDual, 2>;
+      case 64: return decode_mfma_sk_kernel<64, DT, kPrefetchDual, 2, 0, FUSED>;
+      default: return decode_mfma_sk_kernel<128, DT, kPrefetchDual, 2, 0, FUSED>;
     }
   }
   switch (D) {
-    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch, 1>;
-    case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch, 1>;
-    default: return decode_mfma_sk_kernel<256, DT, 2, 1>;
+    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch, 1, 0, FUSED>;
+    case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch, 1, 0, FUSED>;
+    default: return decode_mfma_sk_kernel<256, DT, 2, 1, 0, FUSED>;
   }
 }
 
-KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv, bool wide = false) {
-  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16>(D, nkv, wide) : pick_mfma_sk<QD_DTYPE_BF16>(D, nkv, wide);
+KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv, bool wide = false, bool fused = false) {
+  if (fused)
+    return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16, true>(D, nkv, wide)
+                                 : pick_mfma_sk<QD_DTYPE_BF16, true>(D, nkv, wide);
+  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16, false>(D, nkv, wide)
+                               : pick_mfma_sk<QD_DTYPE_BF16, false>(D, nkv, wide);
 }
 
 // One wave per SIMD needs exactly 4 single-kv-head waves per workgroup;
@@ -1507,11 +1753,12 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 // Resident workgroups of `fn` (block of `threads`) on the current device:
 // CUs x blocks per CU from the HIP occupancy calculator; cached per
 // (device, fn, threads).
-int resident_blocks(KernelFn fn, int threads) {
+int resident_blocks(KernelFn fn, int threads, size_t dyn_lds = 0) {
   struct Entry {
     int device;
     KernelFn fn;
     int threads;
+    size_t dyn_lds;
     int blocks;
   };
   static std::mutex mu;
@@ -1521,18 +1768,52 @@ int resident_blocks(KernelFn fn, int threads) {
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < used; ++i)
-    if (cache[i].device == dev && cache[i].fn == fn && cache[i].threads == threads) return cache[i].blocks;
+    if (cache[i].device == dev && cache[i].fn == fn && cache[i].threads == threads && cache[i].dyn_lds == dyn_lds)
+      return cache[i].blocks;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), threads, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), threads, dyn_lds) !=
           hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
   (void)hipGetLastError();
   const int blocks = cus * per_cu;
-  if (used < 64) cache[used++] = Entry{dev, fn, threads, blocks};
+  if (used < 64) cache[used++] = Entry{dev, fn, threads, dyn_lds, blocks};
   return blocks;
+}
+
+// Dynamic LDS of the fused kernel at most (the partials a workgroup keeps
+// until its range ends; with the K tiles well inside gfx950's 160 KiB).
+constexpr size_t kFusedMaxStash = 96 << 10;
+
+// Raises `fn`'s dynamic LDS limit to kFusedMaxStash (above the default
+// 64 KiB), once per (device, kernel); false when HIP refuses.  Without a
+// device (plans made for sizing only, as resident_blocks' fallback) it
+// reports true.
+bool allow_fused_stash(KernelFn fn) {
+  struct Entry {
+    int device;
+    KernelFn fn;
+    bool ok;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int used = 0;
+  int dev = 0, count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    (void)hipGetLastError();
+    return true;
+  }
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].device == dev && cache[i].fn == fn) return cache[i].ok;
+  const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(kFusedMaxStash)) == hipSuccess;
+  (void)hipGetLastError();
+  if (used < 64) cache[used++] = Entry{dev, fn, ok};
+  return ok;
 }
 
 // Kv-heads per wave on the stream-K path.  One (a workgroup of up to 8
@@ -1565,23 +1846,73 @@ int sk_wg_waves(int kv_heads, int nkv, int head_dim, bool valu = false, bool wid
   return 1;
 }
 
+// Arrival counters of the fused stream-K path: one 32-bit word per
+// (sequence, kv-head), at the start of every automatic-path workspace.  The
+// place and size are fixed, so calls of any shape sharing a workspace never
+// write partials over them; they must be zero before the workspace's first
+// use, and every call leaves them zero.
+constexpr int64_t kFusedMaxCounters = 65536;
+constexpr size_t kCounterBytes = static_cast<size_t>(kFusedMaxCounters) * sizeof(uint32_t);  // 256 KiB
+
+// The automatic plan merges split sequences with merge_sk_kernel; the fused
+// merge (decode_mfma_sk_kernel<..., FUSED = true>) is kept as the
+// QD_STAGE_FUSED measurement option.  Per-wave timestamps on cfg2's shape
+// (bench.py --mode stamps) put the fused chain after a wave's last group
+// at 1.4 us (sc1 partial stores retiring) + 1.0 us (arrival atomic) +
+// 6-8 us (sc1 row reads, all merging waves at once), against about 4.7 us
+// for the separate kernel including its launch: 78 against 59 us per call.
+constexpr bool kFusedByDefault = false;
+
+// Fused merge cost bound: the merging wave folds NKV*g heads, four per pass,
+// over about ceil(W/B) rows, fused_merge_rows() per memory round trip.  The
+// fused path is taken when that is at most kFusedMaxTrips dependent round
+// trips, since the last merge of the launch is not hidden behind streaming;
+// beyond it merge_sk_kernel's one-head-per-wave layout finishes sooner.
+constexpr int64_t kFusedMaxTrips = 2;
+
 struct AutoPlan {
   bool stream_k;
   int wgs;          // stream-K grid (workgroups)
   int wg_waves;     // stream-K waves per workgroup
   int kv_per_wave;  // stream-K kv-heads per wave
   bool wide;        // stream-K: one wave per SIMD, kSkWidePrefetch groups in flight
+  bool fused;       // stream-K: split sequences merged inside the decode kernel
+  size_t stash_bytes;  // fused: dynamic LDS per workgroup for mid-range partials
   int splits;       // explicit-split path
   int chunk_pages;
-  size_t ws_bytes;  // scratch bytes
+  size_t ws_bytes;  // scratch bytes (kCounterBytes of counters first)
   size_t meta_offset;  // stream-K: byte offset of the meta table in the scratch
 };
+
+// Shapes the fused merge can address: one counter per (sequence, kv-head)
+// in the counter area, and 32-bit buffer offsets over a sequence's slots.
+bool fused_fits(int batch, int q_heads, int kv_heads, int head_dim, int64_t wgs) {
+  return static_cast<int64_t>(batch) * kv_heads <= kFusedMaxCounters &&
+         (wgs + batch) * q_heads * (head_dim + 2) * 4 < (int64_t{1} << 31);
+}
+
+// Dynamic LDS of the fused kernel: each wave keeps one partial per kv-head
+// group it serves, (2 + head_dim/4) fields x 64 lanes x 4 bytes per kv-head.
+
+size_t fused_stash_bytes(int kv_heads, int head_dim, int nkv, int wg_waves) {
+  const int items = (kv_heads + wg_waves * nkv - 1) / (wg_waves * nkv);
+  return static_cast<size_t>(wg_waves) * items * nkv * (2 + head_dim / 4) * 64 * sizeof(float);
+}
+
+bool fused_applies(int batch, int q_heads, int kv_heads, int head_dim, int nkv, int64_t wgs) {
+  if (!fused_fits(batch, q_heads, kv_heads, head_dim, wgs)) return false;
+  const int64_t heads = static_cast<int64_t>(nkv) * (q_heads / kv_heads);
+  const int64_t passes = (heads + 3) / 4;
+  const int64_t rows = (wgs + batch - 1) / batch + 1;  // a sequence may touch one more workgroup
+  const int64_t kb = head_dim <= 128 ? 16 : 8;
+  return passes * ((rows + kb - 1) / kb) <= kFusedMaxTrips;
+}
 
 // Chooses the automatic path from static shapes only.  `aligned` says
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
               int dtype, bool aligned, AutoPlan* ap, bool valu = false) {
-  *ap = AutoPlan{false, 0, 1, 1, false, 1, 0, 0, 0};
+  *ap = AutoPlan{false, 0, 1, 1, false, false, 0, 1, 0, kCounterBytes, 0};
   if (batch <= 0) return QD_OK;
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
@@ -1602,12 +1933,31 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     const int64_t by_work = (gmax + kSkMinGroups - 1) / kSkMinGroups;
     if (w > by_work) w = by_work;
     if (w < 1) w = 1;
+    if (valu) {
+      // The comparison variant runs on the product plan's grid (and fits its
+      // workspace).
+      AutoPlan prod;
+      auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, aligned, &prod, false);
+      if (prod.stream_k && w > prod.wgs) w = prod.wgs;
+    }
     ap->stream_k = true;
     ap->wgs = static_cast<int>(w);
     ap->wg_waves = nw;
     ap->kv_per_wave = nkv;
     ap->wide = wide && nkv == 1;
-    ap->meta_offset = static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
+    ap->stash_bytes = fused_stash_bytes(kv_heads, head_dim, nkv, nw);
+    const KernelFn ffn = pick_mfma_sk_dt(dtype, head_dim, nkv, ap->wide, true);
+    if (kFusedByDefault && !valu && fused_applies(batch, q_heads, kv_heads, head_dim, nkv, w) &&
+        ap->stash_bytes <= kFusedMaxStash && allow_fused_stash(ffn)) {
+      // The fused kernel's own occupancy (registers and the stash) bounds
+      // the grid; without waits between workgroups a larger grid would
+      // still be correct, only slower.
+      const int64_t rf = resident_blocks(ffn, 64 * nw, ap->stash_bytes) * kSkOversubscribe;
+      if (w > rf) w = rf;
+      ap->wgs = static_cast<int>(w);
+      ap->fused = fused_fits(batch, q_heads, kv_heads, head_dim, w);
+    }
+    ap->meta_offset = kCounterBytes + static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
     ap->ws_bytes = ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
     return QD_OK;
   }
@@ -1617,7 +1967,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
   if (st != QD_OK) return st;
   ap->splits = s;
   ap->chunk_pages = c;
-  ap->ws_bytes = qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, s);
+  ap->ws_bytes = kCounterBytes + qd_gqa_decode_workspace_bytes(batch, q_heads, head_dim, s);
   return QD_OK;
 }
 
@@ -1637,6 +1987,10 @@ int check_launch_shapes(int batch, int q_heads, int kv_heads, int head_dim, int 
     return fail(QD_ERR_INVALID_VALUE, "batch and head counts must be <= 65535 (grid limit)");
   return QD_OK;
 }
+
+#ifdef QD_STAMPS
+uint64_t* g_stamps = nullptr;  // diagnostic build: qd_diag_set_stamps
+#endif
 
 DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache,
                          const int32_t* block_table, const int32_t* context_lens, void* out,
@@ -1665,27 +2019,26 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.sl2 = scale * kLog2e;
   prm.meta = nullptr;
   prm.wg_waves = 1;
+  prm.ctr = nullptr;
+#ifdef QD_STAMPS
+  prm.stamps = g_stamps;
+#endif
   return prm;
 }
 
 // Scratch bytes the automatic path needs for these shapes: the larger of
 // the aligned and unaligned plans, so that the size does not depend on
-// pointer alignment, and with_valu: also QD_STAGE_VALU's plan (its
-// partition may have more workgroups).  0 for invalid shapes.
+// pointer alignment (QD_STAGE_VALU's plan runs on the same grid and fits).
+// 0 for invalid shapes.
 size_t auto_scratch_bytes(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
-                          int dtype, bool with_valu) {
+                          int dtype) {
   if (check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, 1, dtype, 1.f) != QD_OK)
     return 0;
-  AutoPlan a, b, c;
+  AutoPlan a, b;
   if (auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &a) != QD_OK ||
       auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, false, &b) != QD_OK)
     return 0;
-  size_t bytes = a.ws_bytes > b.ws_bytes ? a.ws_bytes : b.ws_bytes;
-  if (with_valu && valu_sk_applies(q_heads, kv_heads, head_dim, dtype) &&
-      auto_plan(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true, &c, true) == QD_OK &&
-      c.ws_bytes > bytes)
-    bytes = c.ws_bytes;
-  return bytes;
+  return a.ws_bytes > b.ws_bytes ? a.ws_bytes : b.ws_bytes;
 }
 
 int launch_error() {
@@ -1900,8 +2253,10 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
 
 size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
                                           int block_size, int max_pages, int dtype) {
-  return auto_scratch_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, true);
+  return auto_scratch_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype);
 }
+
+size_t qd_gqa_decode_auto_counter_bytes(void) { return kCounterBytes; }
 
 int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_table, const int32_t* context_lens, void* out,
@@ -1909,9 +2264,12 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
                               int kv_heads, int head_dim, int block_size, int max_pages,
                               int64_t num_blocks, int dtype, float scale, int stages, void* stream) {
   const bool valu = (stages & QD_STAGE_VALU) != 0;
-  stages &= ~QD_STAGE_VALU;
+  const bool unfused = (stages & QD_STAGE_UNFUSED) != 0;
+  const bool force_fused = (stages & QD_STAGE_FUSED) != 0;
+  stages &= ~(QD_STAGE_VALU | QD_STAGE_UNFUSED | QD_STAGE_FUSED);
   if ((stages & ~QD_STAGE_ALL) != 0 || stages == 0)
     return fail(QD_ERR_INVALID_VALUE, "stages must be a non-empty mask of QD_STAGE_*");
+  if (unfused && force_fused) return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_UNFUSED and QD_STAGE_FUSED exclude each other");
   int st = check_launch_shapes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
                                dtype, scale);
   if (st != QD_OK) return st;
@@ -1932,17 +2290,34 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
     if (stages != QD_STAGE_ALL)
       return fail(QD_ERR_INVALID_VALUE, "stages apply to the balanced MFMA path only");
     return qd_gqa_decode_launch(q, k_cache, v_cache, block_table, context_lens, out,
-                                reinterpret_cast<float*>(scratch), ap.ws_bytes,
+                                reinterpret_cast<float*>(scratch + kCounterBytes), ap.ws_bytes - kCounterBytes,
                                 batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks,
                                 dtype, scale, ap.splits, ap.chunk_pages, 0, stream);
   }
-  DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, scratch, batch,
-                                 q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
+  bool fused = ap.fused;
+  if (unfused) fused = false;
+  if (force_fused) {
+    if (valu || !fused_fits(batch, q_heads, kv_heads, head_dim, ap.wgs) || ap.stash_bytes > kFusedMaxStash ||
+        !allow_fused_stash(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, true)))
+      return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_FUSED needs MFMA math, batch * kv_heads <= 65536 and "
+                                        "partial slots below 2 GiB");
+    fused = true;
+  }
+  DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, scratch + kCounterBytes,
+                                 batch, q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
                                  ap.wgs, 0);
   prm.meta = reinterpret_cast<int*>(scratch + ap.meta_offset);
+  prm.ctr = reinterpret_cast<uint32_t*>(scratch);
   prm.wg_waves = ap.wg_waves;
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
+  if (fused) {
+    // One kernel: decode and merge.  QD_STAGE_MERGE alone has nothing to do.
+    if (stages & QD_STAGE_DECODE)
+      hipLaunchKernelGGL(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, true), dim3(ap.wgs),
+                         dim3(64 * ap.wg_waves), ap.stash_bytes, stm, prm);
+    return launch_error();
+  }
   if (stages & QD_STAGE_DECODE)
     hipLaunchKernelGGL(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads) : pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide),
                        dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
@@ -1974,8 +2349,7 @@ int qd_gqa_decode_auto_noalloc(const void* q, const void* k_cache, const void* v
                                scale);
   if (st != QD_OK) return st;
   if (batch == 0) return QD_OK;
-  const size_t need =
-      auto_scratch_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype, false);
+  const size_t need = auto_scratch_bytes(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype);
   if (need > kNoAllocScratchBytes)
     return fail(QD_ERR_INVALID_VALUE, "shapes need " + std::to_string(need) +
                                           " bytes of scratch, more than the no-allocation scratch holds (" +
@@ -1998,7 +2372,17 @@ int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, 
   if (waves) *waves = ap.stream_k ? ap.wgs * ap.wg_waves : 0;
   if (splits) *splits = ap.splits;
   if (chunk_pages) *chunk_pages = ap.chunk_pages;
-  return ap.stream_k ? 1 : 0;
+  return ap.stream_k ? (ap.fused ? 2 : 1) : 0;
 }
+
+#ifdef QD_STAMPS
+// Diagnostic build only: per-wave timestamps of the stream-K kernel go to
+// `buffer` (8 words per wave, the grid's waves in order) for the launches
+// that follow, until called again (NULL stops them).
+int qd_diag_set_stamps(void* buffer) {
+  g_stamps = static_cast<uint64_t*>(buffer);
+  return QD_OK;
+}
+#endif
 
 }  // extern "C"

@@ -219,6 +219,50 @@ __device__ __forceinline__ void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&o
 }
 
 // ----------------------------------------------------------------------------
+// Data exchanged between workgroups of one launch
+// ----------------------------------------------------------------------------
+//
+// Each XCD of gfx950 has its own L2, and plain stores may stay dirty in the
+// writer's L2 until the kernel ends.  Relaxed agent-scope atomics avoid the
+// whole-L2 writeback/invalidate of an agent-scope fence: the stores carry
+// sc1 (written through to the device coherence point) and the loads carry
+// sc1 (never answered from a stale line in the reader's L2).  Once a wave's
+// `s_waitcnt vmcnt(0)` has retired its sc1 stores, they are visible to sc1
+// loads from any XCD.  8 bytes per access (two floats).
+
+__device__ __forceinline__ void coherent_store2(float* p, float a, float b) {
+  const uint64_t v = static_cast<uint64_t>(__float_as_uint(a)) | (static_cast<uint64_t>(__float_as_uint(b)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ f32x2 coherent_load2(const float* p) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return f32x2{__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32))};
+}
+
+// Buffer resource over [base, base + bytes) for raw buffer loads (word 3:
+// the gfx9 raw-buffer format, 32-bit elements).  A load's address is base +
+// voffset (VGPR) + soffset (SGPR) + an immediate; bytes past `bytes` read 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// Cache-policy operand of the raw buffer builtins on gfx950: bit 4 = sc1.
+constexpr int kBufferSc1 = 16;
+
+// 8 bytes at base + voffset + soffset with an sc1 load (see above).
+__device__ __forceinline__ f32x2 coherent_buffer_load2(__amdgpu_buffer_rsrc_t rs, uint32_t voffset, uint32_t soffset) {
+  const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, voffset, soffset, kBufferSc1));
+  return f32x2{__uint_as_float(v[0]), __uint_as_float(v[1])};
+}
+
+// Waits until every memory access this wave issued has completed (for sc1
+// stores: reached the coherence point).
+__device__ __forceinline__ void wait_memory_retired() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ----------------------------------------------------------------------------
 // Streaming loads
 // ----------------------------------------------------------------------------
 

@@ -1,0 +1,156 @@
+// Streaming-read probes for the diagnostic library (libqd_attention_diag.so,
+// loaded only by bench.py --mode read): the HBM read rate the decode kernel
+// could reach with its access pattern and none of its work.
+//
+//   probe_paged_kernel   the balanced decode kernel's loads without the
+//                        math, partition or merge: W workgroups of `waves`
+//                        waves; workgroup w streams pages [w*N/W,
+//                        (w+1)*N/W) of a page list (a shuffled permutation of
+//                        the pool), 16-token groups in order; wave j reads
+//                        kv-heads j, j+waves, ... of each group (K: four 1 KiB
+//                        coalesced loads, V: four 16-byte row loads per lane,
+//                        head_dim 128), PF groups in flight, nontemporal
+//                        16-byte loads, a workgroup barrier every PF groups
+//                        (the decode kernel's lockstep).
+//   probe_linear_kernel  a plain contiguous read of the same bytes (K pool
+//                        then V pool), W workgroups of `waves` waves, each
+//                        a contiguous 1/W share, nontemporal 16-byte loads,
+//                        8 loads in flight per lane.
+// Each wave folds what it read into one word (XOR) and writes it, so that
+// nothing is optimized away.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qd_attention.h"
+#include "qd_device.h"
+
+namespace {
+
+constexpr int kProbeD = 128;       // head_dim of the paged probe (16-bit elements)
+constexpr int kProbePf = 2;        // groups in flight per wave, as the decode kernel
+constexpr int kProbeMaxWaves = 8;
+
+struct ProbeGroup {
+  u32x4 k[4];
+  u32x4 v[4];
+};
+
+__device__ __forceinline__ void probe_issue(ProbeGroup& g, const char* kb, const char* vb, int64_t row_bytes,
+                                            int lane) {
+  // K: rows 4c + lane/16 (c = 0..3), bytes 16*(lane%16) of the kv-head slice.
+#pragma unroll
+  for (int c = 0; c < 4; ++c) g.k[c] = stream_load16(kb + (4 * c + lane / 16) * row_bytes + 16 * (lane % 16));
+  // V: rows 4*(lane/16) + i, bytes 16*(lane%16).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) g.v[i] = stream_load16(vb + (4 * (lane / 16) + i) * row_bytes + 16 * (lane % 16));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ uint32_t probe_fold(const ProbeGroup& g) {
+  uint32_t x = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) x ^= g.k[c][0] ^ g.k[c][1] ^ g.k[c][2] ^ g.k[c][3];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x ^= g.v[i][0] ^ g.v[i][1] ^ g.v[i][2] ^ g.v[i][3];
+  return x;
+}
+
+__global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_paged_kernel(const char* k, const char* v,
+                                                                          const int32_t* pages, int64_t npages,
+                                                                          int P, int Hkv, int waves,
+                                                                          uint32_t* sink) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int64_t W = gridDim.x;
+  const int64_t p0 = blockIdx.x * npages / W;
+  const int64_t p1 = (blockIdx.x + 1) * npages / W;
+  const int gpp = P / 16;
+  const int64_t ngroups = (p1 - p0) * gpp;
+  const int64_t row_bytes = static_cast<int64_t>(Hkv) * kProbeD * 2;
+  const bool lockstep = Hkv == waves;
+  uint32_t acc = 0;
+  for (int kvh = wid; kvh < Hkv; kvh += waves) {
+    auto base = [&](int64_t gi, const char* pool) {
+      const int64_t page = pages[p0 + gi / gpp];
+      return pool + (page * P + 16 * (gi % gpp)) * row_bytes + static_cast<int64_t>(kvh) * kProbeD * 2;
+    };
+    ProbeGroup buf[kProbePf];
+    int64_t i = 0;
+#pragma unroll
+    for (int u = 0; u < kProbePf - 1; ++u)
+      if (u < ngroups) probe_issue(buf[u], base(u, k), base(u, v), row_bytes, lane);
+    for (; i + 2 * kProbePf - 2 < ngroups; i += kProbePf) {
+      if (lockstep) __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int u = 0; u < kProbePf; ++u) {
+        const int64_t nx = i + u + kProbePf - 1;
+        probe_issue(buf[(u + kProbePf - 1) % kProbePf], base(nx, k), base(nx, v), row_bytes, lane);
+        acc ^= probe_fold(buf[u]);
+      }
+    }
+    for (; i < ngroups; i += kProbePf) {
+#pragma unroll
+      for (int u = 0; u < kProbePf; ++u) {
+        const int64_t nx = i + u + kProbePf - 1;
+        if (nx < ngroups) probe_issue(buf[(u + kProbePf - 1) % kProbePf], base(nx, k), base(nx, v), row_bytes, lane);
+        if (i + u < ngroups) acc ^= probe_fold(buf[u]);
+      }
+    }
+  }
+  sink[static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_linear_kernel(const char* a, const char* b,
+                                                                           int64_t bytes_each, uint32_t* sink) {
+  // 16-byte words of the two buffers, one contiguous share per workgroup.
+  const int64_t words = 2 * (bytes_each / 16);
+  const int64_t W = gridDim.x;
+  const int64_t w0 = blockIdx.x * words / W;
+  const int64_t w1 = (blockIdx.x + 1) * words / W;
+  const int64_t per_a = bytes_each / 16;
+  constexpr int kUnroll = 8;
+  uint32_t acc = 0;
+  const int64_t stride = blockDim.x;
+  for (int64_t x = w0 + threadIdx.x; x < w1; x += stride * kUnroll) {
+    u32x4 r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t y = x + u * stride;
+      const int64_t z = y < w1 ? y : w0;
+      const char* src = z < per_a ? a + 16 * z : b + 16 * (z - per_a);
+      r[u] = stream_load16(src);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc ^= r[u][0] ^ r[u][1] ^ r[u][2] ^ r[u][3];
+  }
+  sink[static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+// mode 0: probe_paged_kernel over pages[0, npages) of k and v ([N, P, Hkv,
+// 128] 16-bit pools, P a multiple of 16); mode 1: probe_linear_kernel over
+// npages*P*Hkv*128*2 bytes of each pool.  `sink` holds wgs*waves*64 words.
+// Returns 0, or a HIP error (invalid shapes: QD_ERR_INVALID_VALUE).
+int qd_diag_stream_read(const void* k, const void* v, const int32_t* pages, int64_t npages, int P, int Hkv,
+                        int wgs, int waves, int mode, void* sink, void* stream) {
+  if (!k || !v || !sink || npages <= 0 || P <= 0 || P % 16 != 0 || Hkv <= 0 || wgs <= 0 || waves <= 0 ||
+      waves > kProbeMaxWaves || (mode == 0 && !pages) || (mode != 0 && mode != 1))
+    return QD_ERR_INVALID_VALUE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  if (mode == 0) {
+    hipLaunchKernelGGL(probe_paged_kernel, dim3(wgs), dim3(64 * waves), 0, st, static_cast<const char*>(k),
+                       static_cast<const char*>(v), pages, npages, P, Hkv, waves, static_cast<uint32_t*>(sink));
+  } else {
+    const int64_t bytes = npages * P * static_cast<int64_t>(Hkv) * kProbeD * 2;
+    hipLaunchKernelGGL(probe_linear_kernel, dim3(wgs), dim3(64 * waves), 0, st, static_cast<const char*>(k),
+                       static_cast<const char*>(v), bytes, static_cast<uint32_t*>(sink));
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // extern "C"

@@ -91,12 +91,40 @@ at::Tensor decode_impl(const at::Tensor& q, const at::Tensor& k, const at::Tenso
   return out;
 }
 
+// Workspace of the automatic path for a call on `stream`.  Its first
+// qd_gqa_decode_auto_counter_bytes() bytes are arrival counters that must
+// be zero before first use and that every call leaves zero, so one
+// workspace per (device, stream) is allocated zeroed and then reused by
+// every call on that stream (calls on one stream never overlap; calls on
+// different streams get different workspaces).  It grows (a new zeroed
+// tensor) when a call needs more.  Under stream capture the call instead
+// gets a fresh workspace from the graph's private pool, zeroed by a fill
+// kernel captured with it, so every replay starts from zero counters on
+// whatever stream it runs.  The map is never destroyed: its tensors must not
+// be freed after the HIP runtime at process exit.
+at::Tensor auto_workspace(const at::Tensor& q, size_t bytes, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(std::max<size_t>(bytes, 16));
+  const auto opts = q.options().dtype(at::kByte);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+    (void)hipGetLastError();
+    capture = hipStreamCaptureStatusNone;
+  }
+  if (capture != hipStreamCaptureStatusNone) return at::zeros({n}, opts);
+  static std::mutex mu;
+  static auto* cache = new std::map<std::pair<int, hipStream_t>, at::Tensor>();
+  std::lock_guard<std::mutex> lock(mu);
+  at::Tensor& ws = (*cache)[{static_cast<int>(q.get_device()), stream}];
+  if (!ws.defined() || ws.numel() < n) ws = at::zeros({n}, opts);
+  return ws;
+}
+
 // The reference's gqa_decode (gqa_decode.cu:186-188): same validation and
 // output, body replaced by the library's automatic path (balanced MFMA
-// partition or planned splits).  The workspace is allocated per call from
-// the caching allocator, as the reference allocates its split partials
-// (gqa_decode.cu:154): it needs no initialization, so under stream capture
-// it comes from the graph's private pool like any other tensor of the call.
+// partition or planned splits).  The workspace (auto_workspace) is kept per
+// stream rather than allocated per call as the reference allocates its
+// split partials (gqa_decode.cu:154), because the fused merge's counters
+// must start at zero.
 at::Tensor gqa_decode_hip(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                           const at::Tensor& table, const at::Tensor& lens, double scale) {
   const qd_tensor_desc dq = describe(q), dk = describe(k), dv = describe(v), dt = describe(table),
@@ -115,7 +143,7 @@ at::Tensor gqa_decode_hip(const at::Tensor& q, const at::Tensor& k, const at::Te
   const int maxP = static_cast<int>(table.size(1));
   const size_t ws_bytes = qd_gqa_decode_auto_workspace_bytes(B, Hq, Hkv, D, P, maxP, dq.dtype);
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  const at::Tensor ws = at::empty({static_cast<int64_t>(std::max<size_t>(ws_bytes, 16))}, q.options().dtype(at::kByte));
+  const at::Tensor ws = auto_workspace(q, ws_bytes, stream);
   st = qd_gqa_decode_auto(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr<int32_t>(),
                           lens.data_ptr<int32_t>(), out.data_ptr(), ws.data_ptr(), ws_bytes, B, Hq, Hkv, D,
                           P, maxP, k.size(0), dq.dtype, static_cast<float>(scale), stream);

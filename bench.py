@@ -55,7 +55,13 @@ def parse():
     ap.add_argument("--chunk-pages", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=5)
-    ap.add_argument("--mode", choices=["decode", "copy"], default="decode")
+    ap.add_argument("--mode", choices=["decode", "copy", "stamps", "read"], default="decode",
+                    help="copy: HBM copy of known size (counter calibration); stamps: per-wave timestamps "
+                         "of the balanced decode kernel; read: streaming-read ceiling of the decode access "
+                         "pattern (both from the diagnostic library)")
+    ap.add_argument("--merge", choices=["auto", "fused", "unfused"], default="auto",
+                    help="where split sequences are merged (C ABI path, QD_STAGE_FUSED/UNFUSED)")
+    ap.add_argument("--launches", type=int, default=6, help="--mode stamps: launches recorded")
     ap.add_argument("--op", choices=["decode", "kv_append", "mla"], default="decode",
                     help="kv_append: time the paged cache append on the config's shapes instead; "
                          "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config")
@@ -84,6 +90,30 @@ def time_loop(fn, steps: int, warmup: int, stream) -> float:
     return start.elapsed_time(end) / steps
 
 
+SAMPLES = 5
+
+
+def time_samples(fn, steps: int, warmup: int, stream, samples: int = SAMPLES) -> list[float]:
+    """The reference's timing method (benchmarks/measure_decode.py:47-57):
+    `warmup` untimed calls, then `samples` samples of exactly `steps` calls,
+    each bracketed by synchronizations and HIP events on `stream`.
+    Milliseconds per call of each sample; callers report the median."""
+    for i in range(warmup):
+        fn(i)
+    out = []
+    for s in range(samples):
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            fn(s * steps + i)
+        end.record(stream)
+        torch.cuda.synchronize()
+        out.append(start.elapsed_time(end) / steps)
+    return out
+
+
 def copy_mode(args) -> None:
     n = 1 << 30  # bytes per copy
     src = torch.empty(n, dtype=torch.uint8, device="cuda").random_()
@@ -93,6 +123,177 @@ def copy_mode(args) -> None:
     gbs = 2 * n / (ms * 1e-3) / 1e9
     print(json.dumps({"mode": "copy", "bytes_read_per_call": n, "bytes_written_per_call": n,
                       "ms_per_call": ms, "gbs": gbs}), flush=True)
+
+
+def _pct(xs, q):
+    xs = sorted(xs)
+    return xs[min(len(xs) - 1, max(0, int(round(q * (len(xs) - 1)))))]
+
+
+def stamps_mode(args) -> None:
+    """Per-wave s_memrealtime stamps (100 MHz) of the balanced decode kernel,
+    from attention_amd/lib/libqd_attention_diag.so (gqa_decode.hip built
+    with -DQD_STAMPS): entry, end of the partition search, end of streaming,
+    partial stores retired, arrival atomics returned, last merge done (the
+    last three for the fused merge), and the XCD.  --launches launches, each
+    alone on an idle GPU, over rotated K/V pools; one JSON line per launch
+    with the phase times in microseconds from the first wave's entry."""
+    import ctypes
+    from attention_amd import _build, cabi
+    from attention_amd.cases import CONFIGS
+
+    L = ctypes.CDLL(_build.DIAG_LIB)
+    V, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    L.qd_diag_set_stamps.argtypes = [V]
+    L.qd_gqa_decode_auto_stages.argtypes = [V] * 7 + [ctypes.c_size_t] + [I] * 6 + [I64, I, F, I, V]
+    L.qd_gqa_decode_auto_info.argtypes = [I] * 7 + [ctypes.POINTER(I)] * 3
+    L.qd_error_string.restype = ctypes.c_char_p
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    lengths = cfg.lengths()
+    case = (cfg.make(device=dev, device_gen=True, lengths=lengths) if args.device_gen
+            else tuple(x.to(dev) for x in cfg.make(device="cpu", lengths=lengths)))
+    q, k, v, table, lens = case
+    kv_bytes = 2 * k.numel() * k.element_size()
+    pools = args.pools or max(2, math.ceil(768e6 / kv_bytes))
+    ks, vs = [k], [v]
+    for i in range(1, pools):
+        ks.append(k.roll(i, dims=0).contiguous())
+        vs.append(v.roll(i, dims=0).contiguous())
+    dt = cabi.DTYPE[q.dtype]
+    w_, s_, c_ = I(), I(), I()
+    kind = L.qd_gqa_decode_auto_info(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size,
+                                     table.shape[1], dt, ctypes.byref(w_), ctypes.byref(s_), ctypes.byref(c_))
+    if kind < 1:
+        raise SystemExit(f"{cfg.name} does not take the balanced path")
+    waves = w_.value
+    flag = {"auto": 0, "fused": cabi.QD_STAGE_FUSED, "unfused": cabi.QD_STAGE_UNFUSED}[args.merge]
+    fused = args.merge == "fused" or (args.merge == "auto" and kind == 2)
+    ws = cabi.auto_workspace(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size,
+                             table.shape[1], dt, dev)
+    out = torch.empty_like(q)
+    buf = torch.zeros(waves * 8, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    scale = 1.0 / math.sqrt(cfg.head_dim)
+
+    def launch(i, stamped):
+        L.qd_diag_set_stamps(buf.data_ptr() if stamped else None)
+        rc = L.qd_gqa_decode_auto_stages(q.data_ptr(), ks[i % pools].data_ptr(), vs[i % pools].data_ptr(),
+                                         table.data_ptr(), lens.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                         ws.numel(), cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                                         cfg.block_size, table.shape[1], k.shape[0], dt, scale,
+                                         cabi.QD_STAGE_ALL | flag, stream.cuda_stream)
+        if rc:
+            raise RuntimeError(L.qd_error_string(rc).decode())
+
+    for i in range(args.warmup):
+        launch(i, False)
+    torch.cuda.synchronize()
+    log(f"stamps: {cfg.name} waves={waves} fused={fused} launches={args.launches}")
+    for n in range(args.launches):
+        buf.zero_()
+        torch.cuda.synchronize()
+        launch(n, True)
+        torch.cuda.synchronize()
+        s = buf.view(waves, 8).cpu().tolist()
+        t0 = min(r[0] for r in s)
+        us = lambda x: (x - t0) / 100.0  # noqa: E731  (100 MHz ticks)
+        ran = [r for r in s if r[1]]  # waves that held work
+        ends = []
+        for r in s:
+            last = max(r[0], r[1], r[2], r[3], r[4], r[5])
+            ends.append(us(last))
+        rec = {"launch": n, "config": cfg.name, "fused": fused, "waves": waves, "waves_with_work": len(ran),
+               "entry_max_us": round(max(us(r[0]) for r in s), 2),
+               "prologue_end_us": {"p50": round(_pct([us(r[1]) for r in ran], .5), 2),
+                                   "p90": round(_pct([us(r[1]) for r in ran], .9), 2)},
+               "stream_end_us": {q_: round(_pct([us(r[2]) for r in ran], x), 2)
+                                 for q_, x in (("p10", .1), ("p50", .5), ("p90", .9), ("max", 1.0))},
+               "last_wave_end_us": round(max(ends), 2)}
+        arr = [r for r in ran if r[3]]
+        if arr:
+            rec["store_retire_us"] = {"p50": round(_pct([(r[3] - r[2]) / 100 for r in arr], .5), 2),
+                                      "max": round(max((r[3] - r[2]) / 100 for r in arr), 2)}
+            rec["arrival_atomic_us"] = {"p50": round(_pct([(r[4] - r[3]) / 100 for r in arr], .5), 2),
+                                        "max": round(max((r[4] - r[3]) / 100 for r in arr), 2)}
+            mg = [r for r in arr if r[7] > 0]
+            if mg:
+                rec["merge_us"] = {"p50": round(_pct([(r[5] - r[4]) / 100 for r in mg], .5), 2),
+                                   "max": round(max((r[5] - r[4]) / 100 for r in mg), 2), "merging_waves": len(mg)}
+                rec["merge_start_us"] = {"p10": round(_pct([us(r[4]) for r in mg], .1), 2),
+                                         "p50": round(_pct([us(r[4]) for r in mg], .5), 2),
+                                         "max": round(max(us(r[4]) for r in mg), 2)}
+        xcd = {}
+        for r in ran:
+            xcd.setdefault(int(r[6]), []).append(us(r[2]))
+        rec["stream_end_p50_by_xcd_us"] = {str(x): round(_pct(v_, .5), 2) for x, v_ in sorted(xcd.items())}
+        print(json.dumps(rec), flush=True)
+
+
+def read_mode(args) -> None:
+    """The HBM read ceiling for the decode kernel's bytes: the probes of
+    attention_amd/lib/libqd_attention_diag.so (stream_probe.hip) over the
+    config's own K/V pools (head_dim 128, 16-bit), rotated as in the decode
+    bench.  `paged`: the decode kernel's loads without its math, partition
+    or merge (one workgroup of kv_heads waves per CU, whole 16-token groups
+    of the shuffled pages, two groups in flight, nontemporal 16-byte loads);
+    `linear`: a contiguous read of the same pools.  Median of 5 samples; the
+    decode floor is the decode call's algorithmic bytes at the paged rate."""
+    import ctypes
+    from attention_amd import _build
+    from attention_amd.cases import CONFIGS, algorithmic_bytes
+
+    L = ctypes.CDLL(_build.DIAG_LIB)
+    V, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    L.qd_diag_stream_read.argtypes = [V, V, V, I64, I, I, I, I, I, V, V]
+    cfg = CONFIGS[args.config]
+    if cfg.head_dim != 128 or cfg.dtype not in (torch.float16, torch.bfloat16):
+        raise SystemExit("--mode read covers 16-bit caches with head_dim 128")
+    dev = torch.device("cuda:0")
+    lengths = cfg.lengths()
+    case = (cfg.make(device=dev, device_gen=True, lengths=lengths) if args.device_gen
+            else tuple(x.to(dev) for x in cfg.make(device="cpu", lengths=lengths)))
+    q, k, v, table, lens = case
+    kv_bytes = 2 * k.numel() * k.element_size()
+    pools = args.pools or max(2, math.ceil(768e6 / kv_bytes))
+    ks, vs = [k], [v]
+    for i in range(1, pools):
+        ks.append(k.roll(i, dims=0).contiguous())
+        vs.append(v.roll(i, dims=0).contiguous())
+    # Every page of the exact pool, in the page table's order (sequence by
+    # sequence): the shuffled physical order the decode kernel visits.
+    used = [table[b, :math.ceil(n / cfg.block_size)] for b, n in enumerate(lengths) if n > 0]
+    pages = torch.cat(used).to(torch.int32).contiguous()
+    npages = pages.numel()
+    assert int(pages.min()) >= 0 and int(pages.max()) < k.shape[0]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    waves = min(cfg.kv_heads, 8)
+    wgs = cus
+    sink = torch.empty(wgs * waves * 64, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    probe_bytes = 2 * npages * cfg.block_size * cfg.kv_heads * cfg.head_dim * k.element_size()
+    res = {}
+    for name, mode in (("paged", 0), ("linear", 1)):
+        def step(i, mode=mode):
+            rc = L.qd_diag_stream_read(ks[i % pools].data_ptr(), vs[i % pools].data_ptr(), pages.data_ptr(),
+                                       npages, cfg.block_size, cfg.kv_heads, wgs, waves, mode, sink.data_ptr(),
+                                       stream.cuda_stream)
+            if rc:
+                raise RuntimeError(f"qd_diag_stream_read failed: {rc}")
+        samples = time_samples(step, args.steps, args.warmup, stream)
+        ms = statistics.median(samples)
+        res[name] = {"us_per_launch": round(ms * 1e3, 3), "tbs": round(probe_bytes / (ms * 1e-3) / 1e12, 4),
+                     "samples_us": [round(x * 1e3, 3) for x in samples]}
+        log(f"{name}: {ms * 1e3:.2f} us, {probe_bytes / (ms * 1e-3) / 1e12:.3f} TB/s")
+    alg = algorithmic_bytes(lengths, cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size,
+                            q.element_size())
+    rate = res["paged"]["tbs"] * 1e12
+    print(json.dumps({"mode": "read", "config": cfg.name, "bytes_read_per_launch": probe_bytes,
+                      "pages": npages, "workgroups": wgs, "waves_per_workgroup": waves, "pools_rotated": pools,
+                      "paged": res["paged"], "linear": res["linear"], "peak_tbs": PEAK_HBM_GBS / 1e3,
+                      "decode_algorithmic_bytes": alg,
+                      "decode_floor_us_at_paged_rate": round(alg / rate * 1e6, 2),
+                      "target_us_at_80pct_of_peak": round(alg / (0.8 * PEAK_HBM_GBS * 1e9) * 1e6, 2)}), flush=True)
 
 
 def cpu_threads() -> tuple[int, dict]:
@@ -397,6 +598,12 @@ def main() -> None:
     if args.mode == "copy":
         copy_mode(args)
         return
+    if args.mode == "stamps":
+        stamps_mode(args)
+        return
+    if args.mode == "read":
+        read_mode(args)
+        return
     if args.op == "kv_append":
         kv_append_mode(args)
         return
@@ -483,11 +690,13 @@ def main() -> None:
         kname = "decode_mfma_kernel" if kind == 1 else "decode_generic_kernel"
         kernels = kname + ("+combine_kernel" if splits > 1 else "")
     log(f"path: {path}; kernels {kernels}; waves={auto_waves} splits={splits} chunk_pages={chunk}; "
-        f"warmup {args.warmup}, steps {args.steps}")
-    ms = time_loop(step, args.steps, args.warmup, stream)
+        f"warmup {args.warmup}, {SAMPLES} samples of {args.steps} steps")
+    call_ms = time_samples(step, args.steps, args.warmup, stream)
+    ms = statistics.median(call_ms)
     us = ms * 1e3
     gbs = alg_bytes / (ms * 1e-3) / 1e9
-    log(f"{us:.2f} us/call, {gbs:.1f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of peak)")
+    log(f"{us:.2f} us/call (median of {SAMPLES} samples; min {min(call_ms) * 1e3:.2f}, max "
+        f"{max(call_ms) * 1e3:.2f}), {gbs:.1f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of peak)")
 
     # Roofline of the dominant kernel alone: the decode stage of the same
     # call (qd_gqa_decode_auto_stages), timed with HIP events on its stream.
@@ -504,9 +713,10 @@ def main() -> None:
             if rc:
                 raise RuntimeError(cabi.error_string(rc))
 
-        k_ms = time_loop(decode_stage, args.steps, args.warmup, stream)
+        k_ms = statistics.median(time_samples(decode_stage, args.steps, args.warmup, stream))
         rk_note = ("achieved = algorithmic bytes per call / average duration of the decode kernel "
-                   "alone (decode stage of qd_gqa_decode_auto_stages, HIP events on its stream)")
+                   "alone (decode stage of qd_gqa_decode_auto_stages, HIP events on its stream, median of "
+                   f"{SAMPLES} samples)")
     else:
         rk_name, k_ms = kernels, ms
         rk_note = "achieved = algorithmic bytes per call / HIP-event time per call (all launches)"
@@ -519,9 +729,16 @@ def main() -> None:
         "value": round(gbs, 2),
         "unit": "GB/s",
         "us_per_call": round(us, 3),
+        "us_per_call_samples": [round(x * 1e3, 3) for x in call_ms],
+        "us_per_call_min": round(min(call_ms) * 1e3, 3),
+        "us_per_call_max": round(max(call_ms) * 1e3, 3),
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "n_gpus": 1,
         "steps": args.steps,
+        "samples": SAMPLES,
+        "timing": (f"{args.warmup} warmup calls, then {SAMPLES} samples of {args.steps} calls each bracketed "
+                   "by synchronizations and HIP events; value and ms_per_step are the median sample "
+                   "(reference benchmarks/measure_decode.py:47-57)"),
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define QD_ATTENTION_ABI_VERSION 1
+#define QD_ATTENTION_ABI_VERSION 2
 
 /* Element type codes shared by every entry point. */
 enum {
@@ -149,20 +149,29 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  *     group size <= 16 and batch <= 4096: the (sequence, 16-token group)
  *     space is cut into cost-balanced ranges, one per resident workgroup;
  *     a sequence split across workgroups leaves one partial per workgroup,
- *     which a second kernel on the same stream folds (log-sum-exp);
+ *     folded (log-sum-exp) either inside the same kernel by the last
+ *     workgroup to finish a piece of it (the fused merge, when the merge is
+ *     short: see qd_gqa_decode_auto_info) or by a second kernel on the same
+ *     stream;
  *   - otherwise: the split layout of qd_gqa_decode_launch with the plan of
  *     qd_gqa_decode_plan.
- * The workspace is device scratch, 16-byte aligned, of at least
- * qd_gqa_decode_auto_workspace_bytes() bytes (which also covers
- * QD_STAGE_VALU below).  Its contents need no
- * initialization: every call writes what it reads (the partial slots and,
- * for every sequence, its span entry).  Calls that may run concurrently
- * (different streams, or replays of captured graphs on different streams)
- * need different workspaces.  Workspace size and partition depend on the
- * current device (hipGetDevice), so query and launch with the same device
- * current.  Does not allocate or synchronize. */
+ * The workspace is device memory, 16-byte aligned, of at least
+ * qd_gqa_decode_auto_workspace_bytes() bytes.  Its first
+ * qd_gqa_decode_auto_counter_bytes() bytes are the fused merge's arrival
+ * counters: they must be zero before the workspace's first use (zero the
+ * whole workspace once when allocating it), and every call leaves them
+ * zero, so a workspace is reused as it is.  The rest needs no
+ * initialization: every call writes what it reads.  Calls that may run
+ * concurrently (different streams, or replays of captured graphs on
+ * different streams) need different workspaces.  Workspace size and
+ * partition depend on the current device (hipGetDevice), so query and
+ * launch with the same device current.  Does not allocate or synchronize. */
 size_t qd_gqa_decode_auto_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
                                           int block_size, int max_pages, int dtype);
+
+/* Bytes of arrival counters at the start of every automatic-path workspace
+ * (fixed: 256 KiB). */
+size_t qd_gqa_decode_auto_counter_bytes(void);
 
 int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
                        const int32_t* block_table, const int32_t* context_lens, void* out,
@@ -172,15 +181,22 @@ int qd_gqa_decode_auto(const void* q, const void* k_cache, const void* v_cache,
 
 /* The automatic path's kernels, for callers that time or schedule them
  * separately (the balanced MFMA path only; the split path needs
- * QD_STAGE_ALL).  QD_STAGE_DECODE alone leaves split sequences unmerged;
- * a following QD_STAGE_MERGE call with the same arguments and workspace on
- * the same stream completes the output. */
+ * QD_STAGE_ALL).  With the fused merge, QD_STAGE_DECODE is the whole call
+ * and QD_STAGE_MERGE alone does nothing.  Otherwise QD_STAGE_DECODE alone
+ * leaves split sequences unmerged, and a following QD_STAGE_MERGE call with
+ * the same arguments and workspace on the same stream completes the
+ * output. */
 enum { QD_STAGE_DECODE = 1, QD_STAGE_MERGE = 2, QD_STAGE_ALL = 3 };
 /* OR'ed into `stages` for measurement only: run the balanced path's decode
  * kernel with VALU math (packed dot products and fp32 FMAs) in place of the
- * MFMA instructions, same loads and partition.  Head_dim 128, group size
- * <= 8, one kv-head per wave; other shapes are rejected. */
+ * MFMA instructions, same loads and partition (never fused).  Head_dim 128,
+ * group size <= 8, one kv-head per wave; other shapes are rejected. */
 enum { QD_STAGE_VALU = 4 };
+/* OR'ed into `stages` for measurement only: merge split sequences with the
+ * separate merge kernel (QD_STAGE_UNFUSED) or inside the decode kernel
+ * (QD_STAGE_FUSED; batch * kv_heads <= 65536 and the partial slots below
+ * 2 GiB) whatever the plan chose. */
+enum { QD_STAGE_UNFUSED = 8, QD_STAGE_FUSED = 16 };
 
 int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_table, const int32_t* context_lens, void* out,
@@ -207,9 +223,10 @@ int qd_gqa_decode_auto_noalloc(const void* q, const void* k_cache, const void* v
                                int64_t num_blocks, int dtype, float scale, void* stream);
 
 /* Describes the automatic path's choice (assuming aligned pointers):
- * returns 1 for the balanced MFMA path (*waves = its total wave count), 0 for
- * the split path (*splits, *chunk_pages), -1 for invalid shapes.  Any
- * output pointer may be NULL. */
+ * returns 2 for the balanced MFMA path with the fused merge, 1 for it with
+ * the separate merge kernel (*waves = its total wave count), 0 for the split
+ * path (*splits, *chunk_pages), -1 for invalid shapes.  Any output pointer
+ * may be NULL. */
 int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, int block_size,
                             int max_pages, int dtype, int* waves, int* splits, int* chunk_pages);
 

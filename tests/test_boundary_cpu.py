@@ -25,7 +25,7 @@ def test_library_exports_every_header_symbol():
     L = ctypes.CDLL(cabi.LIB_PATH)
     for n in names:
         assert hasattr(L, n), n
-    assert cabi.lib().qd_abi_version() == 1
+    assert cabi.lib().qd_abi_version() == 2
 
 
 def good():
@@ -159,16 +159,27 @@ def test_auto_wave_shape_by_capacity():
     workgroup is a capacity of 524288 tokens."""
     bf16 = cabi.DTYPE[torch.bfloat16]
     # cfg2 (131072 tokens) and cfg5 (262144): one kv-head per wave.
-    assert cabi.auto_info(32, 32, 8, 128, 16, 256, bf16)[:2] == (1, 256 * 8)
-    assert cabi.auto_info(256, 40, 8, 128, 32, 32, cabi.DTYPE[torch.float16])[:2] == (1, 256 * 8)
+    assert cabi.auto_info(32, 32, 8, 128, 16, 256, bf16)[1] == 256 * 8
+    assert cabi.auto_info(256, 40, 8, 128, 32, 32, cabi.DTYPE[torch.float16])[1] == 256 * 8
     # cfg4 (1048576 tokens): two kv-heads per wave.
-    assert cabi.auto_info(8, 64, 8, 128, 16, 8192, bf16)[:2] == (1, 256 * 4)
+    assert cabi.auto_info(8, 64, 8, 128, 16, 8192, bf16)[1] == 256 * 4
     # The threshold itself, and just below it.
-    assert cabi.auto_info(8, 64, 8, 128, 16, 4096, bf16)[:2] == (1, 256 * 4)
-    assert cabi.auto_info(8, 64, 8, 128, 16, 4095, bf16)[:2] == (1, 256 * 8)
+    assert cabi.auto_info(8, 64, 8, 128, 16, 4096, bf16)[1] == 256 * 4
+    assert cabi.auto_info(8, 64, 8, 128, 16, 4095, bf16)[1] == 256 * 8
     # Two kv-heads per wave needs 8+ (an even number of) kv-heads and D <= 128.
-    assert cabi.auto_info(8, 28, 4, 128, 16, 8192, bf16)[:2] == (1, 256 * 4)  # 4 kv-heads: 4 waves
-    assert cabi.auto_info(8, 64, 8, 256, 16, 8192, bf16)[:2] == (1, 256 * 4)  # D 256: 4 waves, one each
+    assert cabi.auto_info(8, 28, 4, 128, 16, 8192, bf16)[1] == 256 * 4  # 4 kv-heads: 4 waves
+    assert cabi.auto_info(8, 64, 8, 256, 16, 8192, bf16)[1] == 256 * 4  # D 256: 4 waves, one each
+
+
+def test_auto_plan_uses_the_merge_kernel():
+    """The automatic plan merges split sequences with the separate merge
+    kernel (kind 1) for every benchmark shape; the fused merge is a
+    measurement option only (QD_STAGE_FUSED)."""
+    bf16, f16 = cabi.DTYPE[torch.bfloat16], cabi.DTYPE[torch.float16]
+    for shape in [(32, 32, 8, 128, 16, 256, bf16), (64, 28, 4, 128, 16, 512, bf16), (256, 40, 8, 128, 32, 32, f16),
+                  (4, 8, 2, 64, 16, 32, f16), (8, 64, 8, 128, 16, 8192, bf16)]:
+        assert cabi.auto_info(*shape)[0] == 1, shape
+
 
 
 def test_plan_rejects_bad_shapes():
@@ -240,13 +251,14 @@ def test_auto_plan_for_configs(name):
     dt = {torch.float16: F16, torch.bfloat16: BF16}[cfg.dtype]
     kind, waves, splits, chunk = cabi.auto_info(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
                                                 cfg.block_size, max_pages, dt)
-    assert kind == 1                                   # every benchmark config takes the MFMA path
+    assert kind in (1, 2)                              # every benchmark config takes the MFMA path
     assert waves > 0 and waves % min(cfg.kv_heads, 8) == 0
     nbytes = cabi.auto_workspace_bytes(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
                                        cfg.block_size, max_pages, dt)
     wgs = waves // min(cfg.kv_heads, 8)
     slots = (wgs + cfg.batch) * cfg.q_heads * (cfg.head_dim + 2) * 4
-    assert nbytes >= slots + 8 * cfg.batch
+    assert cabi.auto_counter_bytes() == 256 << 10
+    assert nbytes >= cabi.auto_counter_bytes() + slots + 8 * cfg.batch
 
 
 def test_auto_plan_falls_back_to_splits():
@@ -259,7 +271,7 @@ def test_auto_plan_falls_back_to_splits():
 def test_auto_waves_per_workgroup_divide_kv_heads():
     for hkv, per_wg in [(1, 1), (2, 2), (4, 4), (8, 8), (12, 6), (16, 8), (7, 7), (9, 3)]:
         kind, waves, _, _ = cabi.auto_info(4, hkv, hkv, 64, 16, 64, F16)
-        assert kind == 1 and waves % per_wg == 0, (hkv, waves)
+        assert kind in (1, 2) and waves % per_wg == 0, (hkv, waves)
 
 
 def _auto_args(**over):

@@ -40,7 +40,7 @@ def test_noalloc_matches_auto_entry_point(gpu):
         need = cabi.auto_workspace_bytes(B, Hq, Hkv, D, P, table.shape[1], cabi.DTYPE[q.dtype])
         say(f"no-alloc vs auto: {name} B={B} workspace {need} bytes")
         assert need <= cabi.lib().qd_gqa_decode_noalloc_scratch_bytes()
-        ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=gpu)
+        ws = cabi.auto_workspace(B, Hq, Hkv, D, P, table.shape[1], cabi.DTYPE[q.dtype], gpu, fill=0xFF)
         ref = torch.full_like(q, float("nan"))
         rc = cabi.auto_launch(q, k, v, table, lens, ref, scale=1 / math.sqrt(D), workspace=ws)
         assert rc == 0, cabi.error_string(rc)
