@@ -119,6 +119,23 @@ CONFIGS: dict[str, DecodeConfig] = {
                          description="high-batch short-context decode"),
 }
 
+# Measurement-only shapes (bench.py --config), not BASELINE configs: cfg2's
+# lengths with 64 query heads, the group size 8 of cfg4 at cfg2's bytes per
+# kv-head, for the MFMA-versus-VALU comparison.
+EXTRA_CONFIGS: dict[str, DecodeConfig] = {
+    "cfg2-g8": DecodeConfig("cfg2-g8", 32, 64, 8, 128, 16, torch.bfloat16, 1, len_range=(512, 4096),
+                            description="cfg2 lengths with 64 q-heads (group 8)"),
+}
+
+
+def get_config(name: str) -> DecodeConfig:
+    """A BASELINE config (CONFIGS) or a measurement-only one (EXTRA_CONFIGS)."""
+    if name in CONFIGS:
+        return CONFIGS[name]
+    if name in EXTRA_CONFIGS:
+        return EXTRA_CONFIGS[name]
+    raise KeyError(f"unknown config {name!r}; known: {sorted(CONFIGS) + sorted(EXTRA_CONFIGS)}")
+
 
 def algorithmic_bytes(lengths, batch, q_heads, kv_heads, head_dim, block_size, elem_bytes) -> int:
     """K+V of valid tokens + q + out + lengths + used table entries.

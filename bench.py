@@ -62,9 +62,10 @@ def parse():
     ap.add_argument("--merge", choices=["auto", "fused", "unfused"], default="auto",
                     help="where split sequences are merged (C ABI path, QD_STAGE_FUSED/UNFUSED)")
     ap.add_argument("--launches", type=int, default=6, help="--mode stamps: launches recorded")
-    ap.add_argument("--op", choices=["decode", "kv_append", "mla"], default="decode",
+    ap.add_argument("--op", choices=["decode", "kv_append", "mla", "sweep"], default="decode",
                     help="kv_append: time the paged cache append on the config's shapes instead; "
-                         "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config")
+                         "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config; "
+                         "sweep: the reference's decode sweep (benchmarks/measure_decode.py:43-57)")
     ap.add_argument("--mla-config", default="mla-h128")
     ap.add_argument("--mla-kernel", choices=["auto", "wave", "staged"], default="auto",
                     help="--op mla: attention kernel of the timed attention stage (comparison)")
@@ -140,7 +141,7 @@ def stamps_mode(args) -> None:
     with the phase times in microseconds from the first wave's entry."""
     import ctypes
     from attention_amd import _build, cabi
-    from attention_amd.cases import CONFIGS
+    from attention_amd.cases import get_config
 
     L = ctypes.CDLL(_build.DIAG_LIB)
     V, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -148,7 +149,7 @@ def stamps_mode(args) -> None:
     L.qd_gqa_decode_auto_stages.argtypes = [V] * 7 + [ctypes.c_size_t] + [I] * 6 + [I64, I, F, I, V]
     L.qd_gqa_decode_auto_info.argtypes = [I] * 7 + [ctypes.POINTER(I)] * 3
     L.qd_error_string.restype = ctypes.c_char_p
-    cfg = CONFIGS[args.config]
+    cfg = get_config(args.config)
     dev = torch.device("cuda:0")
     lengths = cfg.lengths()
     case = (cfg.make(device=dev, device_gen=True, lengths=lengths) if args.device_gen
@@ -241,12 +242,12 @@ def read_mode(args) -> None:
     decode floor is the decode call's algorithmic bytes at the paged rate."""
     import ctypes
     from attention_amd import _build
-    from attention_amd.cases import CONFIGS, algorithmic_bytes
+    from attention_amd.cases import algorithmic_bytes, get_config
 
     L = ctypes.CDLL(_build.DIAG_LIB)
     V, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     L.qd_diag_stream_read.argtypes = [V, V, V, I64, I, I, I, I, I, V, V]
-    cfg = CONFIGS[args.config]
+    cfg = get_config(args.config)
     if cfg.head_dim != 128 or cfg.dtype not in (torch.float16, torch.bfloat16):
         raise SystemExit("--mode read covers 16-bit caches with head_dim 128")
     dev = torch.device("cuda:0")
@@ -331,7 +332,51 @@ def _time_cpu(fn, repeats: int, min_s: float, max_s: float) -> list[float]:
     return times
 
 
-def cpu_baseline(case_cpu, cfg, repeats: int) -> dict:
+def _rss_gb() -> float:
+    import resource
+    return resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1e6  # ru_maxrss is in KiB on Linux
+
+
+def other_cpu_configs(skip: str) -> dict:
+    """One timed call of the reference CPU path on each other BASELINE config
+    (the baseline plan's cfg2-cfg5 once each): cfg3 and cfg5 on their whole
+    batches; cfg4 on its first sequence only, because the path materializes
+    about len*Hq*D*4 bytes each for repeated K and V in fp32 (up to 4.3 GB
+    each per sequence) and the whole batch would take about a minute of the
+    bench.  Peak host memory (max RSS) is logged after each."""
+    from oracle.cpu_path import reference_cpu_path
+    from attention_amd.cases import CONFIGS, algorithmic_bytes, make_decode_case
+
+    out = {}
+    for name in ("cfg3", "cfg5", "cfg4"):
+        if name == skip:
+            continue
+        c = CONFIGS[name]
+        lengths = c.lengths()
+        note = "whole batch"
+        if name == "cfg4":
+            lengths = lengths[:1]
+            note = (f"first sequence only ({lengths[0]} tokens of the batch's {sum(c.lengths())}): the whole "
+                    "batch would materialize up to 8.6 GB of fp32 K/V per sequence for about a minute")
+            case = make_decode_case(lengths=lengths, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
+                                    block_size=c.block_size, dtype=c.dtype, seed=c.seed, exact_pool=True,
+                                    k_scale=c.k_scale)
+        else:
+            case = c.make(device="cpu", lengths=lengths)
+        t0 = time.perf_counter()
+        reference_cpu_path(*case)
+        t = time.perf_counter() - t0
+        nbytes = algorithmic_bytes(lengths, len(lengths), c.q_heads, c.kv_heads, c.head_dim, c.block_size,
+                                   case[0].element_size())
+        out[name] = {"us_per_call": round(t * 1e6, 1), "gb_s": round(nbytes / t / 1e9, 3), "sequences": len(lengths),
+                     "tokens": sum(lengths), "sample": note, "max_rss_gb": round(_rss_gb(), 2)}
+        log(f"cpu baseline {name}: {t * 1e3:.1f} ms ({note}), {nbytes / t / 1e9:.3f} GB/s, "
+            f"max RSS {_rss_gb():.1f} GB")
+        del case
+    return out
+
+
+def cpu_baseline(case_cpu, cfg, repeats: int, other_configs: bool = True) -> dict:
     """Times the reference CPU path (oracle/cpu_path.py, the torch CPU ops of
     reference attention/reference/gqa.py:21-44) on the host cores: the whole
     batch of the benchmark config, and cfg1 (the reference's own
@@ -350,9 +395,11 @@ def cpu_baseline(case_cpu, cfg, repeats: int) -> dict:
     c1 = CONFIGS["cfg1"]
     case1 = c1.make(device="cpu")
     t1 = statistics.median(_time_cpu(lambda: reference_cpu_path(*case1), 50, 2.0, 10.0))
+    others = other_cpu_configs(skip=cfg.name) if other_configs else {}
     return {"value": round(b_full / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "us_per_call": round(t * 1e6, 1),
             "cfg1_us_per_call": round(t1 * 1e6, 1),
+            "other_configs": others,
             "sample": (f"oracle/cpu_path.reference_cpu_path (torch CPU ops of reference "
                        f"attention/reference/gqa.py:21-44) on the whole {cfg.name} batch "
                        f"({len(lens_l)} sequences, {sum(lens_l)} tokens, the same input as the GPU "
@@ -384,9 +431,9 @@ def kv_append_mode(args) -> None:
     pools above the Infinity Cache size).  Bytes = key+value read and the
     two cache rows written per sequence, plus the table entry and position."""
     import attention_amd
-    from attention_amd.cases import CONFIGS
+    from attention_amd.cases import get_config
 
-    cfg = CONFIGS[args.config]
+    cfg = get_config(args.config)
     dev = torch.device("cuda:0")
     lengths = cfg.lengths()
     _, k, v, table, lens = cfg.make(device=dev, device_gen=True, lengths=lengths)
@@ -432,6 +479,46 @@ def kv_append_mode(args) -> None:
         "cpu_baseline": {"value": round(nbytes / t_cpu / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
                          "kind": "port", "sample": f"torch indexed assignment on CPU, median {t_cpu * 1e6:.1f} us"},
     }), flush=True)
+
+
+def sweep_mode(args) -> None:
+    """The reference's own decode measurement (benchmarks/measure_decode.py:
+    43-57): attention.gqa_decode on make_decode_case(lengths=[L]*B,
+    Hq32/Hkv8/D128/P16, seed 42, pool B*max_pages blocks) for fp32, fp16 and
+    bf16, B in {1, 4, 16}, L in {128, 1024, 4096}; 20 warmup calls, then 5
+    samples of 10 calls (HIP events, output allocation included), median
+    us per call.  The inputs are not rotated, as in the reference, so the
+    smaller points are served partly from the Infinity Cache.  One JSON line
+    per point, then a summary line."""
+    import attention_amd
+    from attention_amd import cabi
+    from attention_amd.cases import algorithmic_bytes, make_decode_case
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    rows = []
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        for batch in (1, 4, 16):
+            for length in (128, 1024, 4096):
+                inputs = make_decode_case(lengths=[length] * batch, q_heads=32, kv_heads=8, head_dim=128,
+                                          block_size=16, dtype=dtype, device=dev)
+                kind = cabi.auto_info(batch, 32, 8, 128, 16, inputs[3].shape[1], cabi.DTYPE[dtype])[0]
+                samples = time_samples(lambda i: attention_amd.gqa_decode(*inputs), 10, 20, stream)
+                med = statistics.median(samples)
+                nbytes = algorithmic_bytes([length] * batch, batch, 32, 8, 128, 16, inputs[0].element_size())
+                row = {"dtype": DT_NAME[dtype], "batch": batch, "length": length, "hq": 32, "hkv": 8,
+                       "head_dim": 128, "block_size": 16, "median_us": round(med * 1e3, 3),
+                       "min_us": round(min(samples) * 1e3, 3), "max_us": round(max(samples) * 1e3, 3),
+                       "gb_s": round(nbytes / (med * 1e-3) / 1e9, 1),
+                       "path": {1: "balanced MFMA + merge", 2: "balanced MFMA, fused merge",
+                                0: "split layout"}.get(kind, "?")}
+                rows.append(row)
+                print(json.dumps(row), flush=True)
+                del inputs
+    print(json.dumps({"op": "sweep", "points": len(rows),
+                      "method": "20 warmup, 5 samples x 10 calls, median (measure_decode.py:47-57)",
+                      "median_us": {f"{r['dtype']}/B{r['batch']}/L{r['length']}": r["median_us"] for r in rows}}),
+          flush=True)
 
 
 PEAK_MFMA_BF16_TFLOPS = 2500.0
@@ -610,14 +697,17 @@ def main() -> None:
     if args.op == "mla":
         mla_mode(args)
         return
+    if args.op == "sweep":
+        sweep_mode(args)
+        return
 
     import attention_amd
     from attention_amd import cabi
-    from attention_amd.cases import CONFIGS, algorithmic_bytes, algorithmic_flops
+    from attention_amd.cases import algorithmic_bytes, algorithmic_flops, get_config
 
     if not attention_amd.is_cuda_extension_loaded():
         raise RuntimeError("HIP op library not loaded; run __graft_entry__.build()")
-    cfg = CONFIGS[args.config]
+    cfg = get_config(args.config)
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
     lengths = cfg.lengths()
