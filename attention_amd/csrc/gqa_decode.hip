@@ -74,22 +74,25 @@ struct DecodeParams {
   int* meta;      // stream-K path: per sequence {first workgroup, workgroups}
   int wg_waves;   // stream-K path: waves per workgroup
   uint32_t* ctr;  // fused stream-K path: arrival counter per (sequence, kv-head), zero between calls
+  int stage_bytes;  // stream-K path: LDS bytes per wave for result rows held until the range ends
 #ifdef QD_STAMPS
   uint64_t* stamps;  // diagnostic build: per-wave timestamps (stamp_wave)
 #endif
 };
 
 #ifdef QD_STAMPS
-// Diagnostic build only (-DQD_STAMPS): 8 words per wave of the stream-K
-// kernel, at stamps[(workgroup * waves + wave) * 8]: s_memrealtime (100 MHz)
+// Diagnostic build only (-DQD_STAMPS): 16 words per wave of the stream-K
+// kernel, at stamps[(workgroup * waves + wave) * 16]: s_memrealtime (100 MHz)
 // at entry [0], after the partition search [1], at the end of streaming [2],
 // after the partial stores retired [3], after the arrival atomics returned
-// [4], after the last merge [5]; the XCD id [6]; merges done [7].
+// [4], after the last merge [5]; the XCD id [6]; merges done [7]; the shader
+// clock counter (s_memtime) at entry [8] and at the end of streaming [9].
 __device__ __forceinline__ void stamp_wave(const DecodeParams& p, int slot, uint64_t value) {
   if (p.stamps && (threadIdx.x & 63) == 0)
-    p.stamps[(static_cast<int64_t>(blockIdx.x) * p.wg_waves + (threadIdx.x >> 6)) * 8 + slot] = value;
+    p.stamps[(static_cast<int64_t>(blockIdx.x) * p.wg_waves + (threadIdx.x >> 6)) * 16 + slot] = value;
 }
 __device__ __forceinline__ uint64_t stamp_now() { return __builtin_amdgcn_s_memrealtime(); }
+__device__ __forceinline__ uint64_t stamp_clock() { return __builtin_amdgcn_s_memtime(); }
 __device__ __forceinline__ uint64_t stamp_xcc() {
   uint32_t x;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
@@ -99,6 +102,10 @@ __device__ __forceinline__ uint64_t stamp_xcc() {
 #else
 #define QD_STAMP(p, slot, value) ((void)0)
 #endif
+
+// Bytes of item records at the start of a wave's result staging area
+// (MfmaWave::stage_*): 8 records of 16 bytes.
+constexpr int kStageRecordBytes = 128;
 
 // Valid tokens of a sequence: lengths are clamped to the table capacity
 // max_pages*block_size so that a length beyond the table never reads past
@@ -394,6 +401,10 @@ struct MfmaWave {
     lane = threadIdx.x & 63;  // lane within the wave (workgroups may hold several)
     r16 = lane & 15;
     q4 = lane >> 4;
+    res_lds = nullptr;
+    res_cap = 0;
+    res_used = 0;
+    res_items = 0;
   }
 
   // Starts item (b, kvh0..) whose run() begins at group g_first.  The page
@@ -576,6 +587,113 @@ struct MfmaWave {
   __device__ float total_l(int j) const {
     float l = l_run[j] + __shfl_xor(l_run[j], 16);
     return l + __shfl_xor(l, 32);
+  }
+
+  // Result rows held back until the range ends.  On gfx950 a store counts
+  // in vmcnt with the loads and vmcnt retires in issue order, so every
+  // load issued after a store waits for the store's acknowledgement, and
+  // while the K/V stream saturates HBM the memory system acknowledges
+  // writes late.  Stores between items therefore stalled the following
+  // item's loads (and, through the lockstep barrier, the workgroup) by
+  // microseconds: on cfg5 (256 short sequences, an output or partial per
+  // item) the decode kernel took 91 us with its stores removed against 103
+  // us with them, and stores moved behind the next item's first loads or
+  // merged into contiguous chunks changed nothing.  So an item's rows go to
+  // this wave's LDS area in their memory layout (stage_direct /
+  // stage_partial), and flush_results copies them out with contiguous 16-
+  // or 8-byte stores when the range ends (or when the area is full).  The
+  // area starts with kStageMaxItems 16-byte records {destination, bytes,
+  // chunk} (in LDS, so that nothing more stays live in registers across
+  // the streaming loop); the rows follow.
+  static constexpr int kStageMaxItems = kStageRecordBytes / 16;
+  static constexpr int kStageHeader = kStageRecordBytes;
+  char* res_lds;     // this wave's area (header, then rows)
+  int res_cap;       // bytes for rows after the header
+  int res_used;      // row bytes staged so far (16-byte multiples)
+  int res_items;     // items staged
+
+  __device__ static int round16(int x) { return (x + 15) & ~15; }
+
+  // Makes room for `bytes` more, flushing what is staged if needed; returns
+  // the LDS address the item's rows go to.
+  __device__ char* stage_slot(int bytes) {
+    if (res_used + round16(bytes) > res_cap || res_items == kStageMaxItems) flush_results();
+    return res_lds + kStageHeader + res_used;
+  }
+
+  __device__ void stage_direct(const DecodeParams& p, char* area, int jk, float l_tot) {
+    using S = typename Elem<DT>::S;
+    if (r16 >= p.g) return;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    S* o = reinterpret_cast<S*>(area) + (jk * p.g + r16) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t wv[DV / 2];
+#pragma unroll
+      for (int j = 0; j < DV; j += 2)
+        wv[j / 2] = Ops::pack2(l_tot > 0.f ? acc[jk][j][i] * inv : 0.f,
+                               l_tot > 0.f ? acc[jk][j + 1][i] * inv : 0.f);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(o + DV * (4 * q4 + i));
+#pragma unroll
+      for (int t = 0; t < DV / 2; ++t) dst[t] = wv[t];
+    }
+  }
+
+  __device__ void stage_partial(const DecodeParams& p, char* area, int jk, float l_tot) {
+    if (r16 >= p.g) return;
+    float* w = reinterpret_cast<float*>(area) + (jk * p.g + r16) * (D + 2);
+    if (q4 == 0) {
+      w[0] = m_run[jk] * kLn2;
+      w[1] = l_tot;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float* dst = w + 2 + DV * (4 * q4 + i);
+#pragma unroll
+      for (int j = 0; j < DV; ++j) dst[j] = acc[jk][j][i];
+    }
+  }
+
+  // Records the item just staged at stage_slot(bytes): `bytes` to `dst`
+  // in `chunk`-byte stores (16 for output rows, 8 for partial rows).
+  __device__ void stage_commit(char* dst, int bytes, int chunk) {
+    if (lane == 0) {
+      const uint64_t d = reinterpret_cast<uint64_t>(dst);
+      *reinterpret_cast<u32x4*>(res_lds + 16 * res_items) =
+          u32x4{static_cast<uint32_t>(d), static_cast<uint32_t>(d >> 32), static_cast<uint32_t>(bytes),
+                static_cast<uint32_t>(chunk)};
+    }
+    res_used += round16(bytes);
+    ++res_items;
+  }
+
+  __device__ void flush_results() {
+    if (res_items == 0) return;
+    // The staged rows and records were written by other lanes of this
+    // wave: the LDS writes complete first, and nothing is reordered across
+    // this point.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    int off = 0;
+    for (int t = 0; t < res_items; ++t) {
+      const u32x4 rec = *reinterpret_cast<const u32x4*>(res_lds + 16 * t);  // same address in every lane
+      const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(rec[0])));
+      const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(rec[1])));
+      const int bytes = __builtin_amdgcn_readfirstlane(static_cast<int>(rec[2]));
+      const int chunk = __builtin_amdgcn_readfirstlane(static_cast<int>(rec[3]));
+      char* dst = reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
+      const char* src = res_lds + kStageHeader + off;
+      if (chunk == 16) {
+        for (int c = lane; c < bytes / 16; c += 64)
+          *reinterpret_cast<u32x4*>(dst + 16 * c) = *reinterpret_cast<const u32x4*>(src + 16 * c);
+      } else {
+        for (int c = lane; c < bytes / 8; c += 64)
+          *reinterpret_cast<u32x2*>(dst + 8 * c) = *reinterpret_cast<const u32x2*>(src + 8 * c);
+      }
+      off += round16(bytes);
+    }
+    asm volatile("" ::: "memory");
+    res_items = 0;
+    res_used = 0;
   }
 
   // out[b, (kvh0+jk)*g + r16, :] = acc / l (zeros when l == 0), one rounding.
@@ -1194,8 +1312,9 @@ __device__ __forceinline__ uint32_t arrive(const DecodeParams& p, int b, int kvh
 // that completes a counter (the nwg-th) merges that item's heads from all
 // nwg slots and resets the counter to zero.  No wave ever waits for
 // another, and the counters are left as they were found (zero).
-template <int D, int DT, int PF, int NKV, int GV = 0, bool FUSED = false>
+template <int D, int DT, int PF, int NKV, int GV = 0, bool FUSED = false, bool HOLD = false>
 __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_mfma_sk_kernel(DecodeParams p) {
+  static_assert(!(HOLD && (FUSED || GV > 0)), "results are held only by the MFMA kernel with the merge kernel");
   using S = typename Elem<DT>::S;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -1205,6 +1324,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
   const int B = p.B;
   __shared__ __align__(16) char ktile[sk_max_waves<D, NKV, GV, PF>()][KTile<D>::kBytes];
   QD_STAMP(p, 0, stamp_now());
+  QD_STAMP(p, 8, stamp_clock());
   QD_STAMP(p, 6, stamp_xcc());
 
   // Prologue, one memory round trip for B <= 64*kRegChunks: every lane loads
@@ -1321,13 +1441,17 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
   // workgroups}; the second is used when the range ends inside a sequence.
   int sp_b0 = -1, sp_f0 = 0, sp_n0 = 0, sp_b1 = -1, sp_f1 = 0, sp_n1 = 0;
   bool sp_stashed = false;  // the first split sequence's partials wait in LDS
-  // This wave's stash area (dynamic LDS, FUSED only): one item per kv-head
-  // group the wave serves.
+  // Dynamic LDS, per wave: FUSED, the stash (one item per kv-head group the
+  // wave serves); otherwise the staged result rows (NKV*g rows of D+2
+  // floats).
+  extern __shared__ __align__(16) float qd_dyn_lds[];
   float* stash = nullptr;
   if constexpr (FUSED && GV == 0) {
-    extern __shared__ __align__(16) float qd_stash[];
     const int items = (p.Hkv + nw * NKV - 1) / (nw * NKV);
-    stash = qd_stash + static_cast<int64_t>(wid) * items * NKV * Wave::kStashFields * 64;
+    stash = qd_dyn_lds + static_cast<int64_t>(wid) * items * NKV * Wave::kStashFields * 64;
+  } else if constexpr (HOLD) {
+    wv.res_cap = p.stage_bytes - Wave::kStageHeader;
+    wv.res_lds = reinterpret_cast<char*>(qd_dyn_lds) + static_cast<int64_t>(wid) * p.stage_bytes;
   }
   while (true) {
     const int len = len_first >= 0 ? len_first : clamp_len(p, p.lens[b]);
@@ -1348,18 +1472,44 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
         // Every wave runs exactly one item here when the workgroup's waves
         // cover the kv-heads once, so all reach the same barriers.
         wv.run(p, i0, i1, ktile[wid], p.Hkv == nw * NKV);
-        if constexpr (GV == 0) {
+        if constexpr (GV == 0 && FUSED) {
 #pragma unroll
           for (int j = 0; j < NKV; ++j) {
             const float l_tot = wv.total_l(j);
             if (whole)
               wv.store_direct(p, b, kvh0, j, l_tot);
-            else if (FUSED && mid_range)
+            else if (mid_range)
               wv.stash_partial(j, stash + ((kvh0 - wid * NKV) / (nw * NKV)) * NKV * Wave::kStashFields * 64, l_tot);
             else
-              wv.template store_partial<FUSED>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
-                                                D + 2, l_tot);
+              wv.template store_partial<true>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
+                                               D + 2, l_tot);
           }
+        } else if constexpr (GV == 0 && !HOLD) {
+#pragma unroll
+          for (int j = 0; j < NKV; ++j) {
+            const float l_tot = wv.total_l(j);
+            if (whole)
+              wv.store_direct(p, b, kvh0, j, l_tot);
+            else
+              wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2), D + 2, l_tot);
+          }
+        } else if constexpr (HOLD) {
+          const int bytes = whole ? NKV * p.g * D * static_cast<int>(sizeof(S)) : NKV * p.g * (D + 2) * 4;
+          char* area = wv.stage_slot(bytes);
+#pragma unroll
+          for (int j = 0; j < NKV; ++j) {
+            const float l_tot = wv.total_l(j);
+            if (whole)
+              wv.stage_direct(p, area, j, l_tot);
+            else
+              wv.stage_partial(p, area, j, l_tot);
+          }
+          if (whole)
+            wv.stage_commit(reinterpret_cast<char*>(static_cast<S*>(p.out) +
+                                                    (static_cast<int64_t>(b) * p.Hq + kvh0 * p.g) * D),
+                            bytes, 16);
+          else
+            wv.stage_commit(reinterpret_cast<char*>(slot + static_cast<int64_t>(kvh0) * p.g * (D + 2)), bytes, 8);
         } else {
           wv.finish_item();
           if (whole)
@@ -1385,11 +1535,19 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
       } else {
         // The workgroup holding a sequence's first group records which
         // workgroups span it, for merge_sk_kernel (also for a whole sequence,
-        // so that nothing from an earlier call survives).
-        if (i0 == 0 && threadIdx.x == 0) {
+        // so that nothing from an earlier call survives); wave 0 holds the
+        // entry back with its result rows.
+        if (i0 == 0 && wid == 0) {
           const int first = wg_of(x0);
-          p.meta[2 * b] = first;
-          p.meta[2 * b + 1] = wg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
+          const int count = wg_of(x0 + kSkGroupCost * (nb - 1)) - first + 1;
+          if constexpr (HOLD) {
+            char* area = wv.stage_slot(8);
+            if (lane == 0) *reinterpret_cast<int2*>(area) = make_int2(first, count);
+            wv.stage_commit(reinterpret_cast<char*>(p.meta + 2 * b), 8, 8);
+          } else if (lane == 0) {
+            p.meta[2 * b] = first;
+            p.meta[2 * b + 1] = count;
+          }
         }
       }
     }
@@ -1400,7 +1558,9 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
     } while (b < B && p.lens[b] <= 0);
     if (b >= B) break;  // unreachable when C is consistent
   }
+  if constexpr (HOLD) wv.flush_results();  // the range's held items
   QD_STAMP(p, 2, stamp_now());
+  QD_STAMP(p, 9, stamp_clock());
 
   if constexpr (FUSED && GV == 0) {
     if (sp_b0 >= 0) {
@@ -1662,28 +1822,34 @@ constexpr int kPrefetchDual = QD_PREFETCH_DUAL;
 // with 3 or 4 in flight and one workgroup per CU).
 constexpr int kSkWidePrefetch = 3;
 
-template <int DT, bool FUSED>
+template <int DT, bool FUSED, bool HOLD>
 KernelFn pick_mfma_sk(int D, int nkv, bool wide) {
-  if (wide) return decode_mfma_sk_kernel<128, DT, kSkWidePrefetch, 1, 0, FUSED>;
+  if (wide) return decode_mfma_sk_kernel<128, DT, kSkWidePrefetch, 1, 0, FUSED, HOLD>;
   if (nkv == 2) {
     switch (D) {
-      case 64: return decode_mfma_sk_kernel<64, DT, kPrefetchDual, 2, 0, FUSED>;
-      default: return decode_mfma_sk_kernel<128, DT, kPrefetchDual, 2, 0, FUSED>;
+      case 64: return decode_mfma_sk_kernel<64, DT, kPrefetchDual, 2, 0, FUSED, HOLD>;
+      default: return decode_mfma_sk_kernel<128, DT, kPrefetchDual, 2, 0, FUSED, HOLD>;
     }
   }
   switch (D) {
-    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch, 1, 0, FUSED>;
-    case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch, 1, 0, FUSED>;
-    default: return decode_mfma_sk_kernel<256, DT, 2, 1, 0, FUSED>;
+    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch, 1, 0, FUSED, HOLD>;
+    case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch, 1, 0, FUSED, HOLD>;
+    default: return decode_mfma_sk_kernel<256, DT, 2, 1, 0, FUSED, HOLD>;
   }
 }
 
-KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv, bool wide = false, bool fused = false) {
+// fused: the fused-merge kernel; hold: the kernel that holds its result rows
+// in LDS until its range ends (never both).
+KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv, bool wide = false, bool fused = false, bool hold = false) {
+  const bool f16 = dtype == QD_DTYPE_F16;
   if (fused)
-    return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16, true>(D, nkv, wide)
-                                 : pick_mfma_sk<QD_DTYPE_BF16, true>(D, nkv, wide);
-  return dtype == QD_DTYPE_F16 ? pick_mfma_sk<QD_DTYPE_F16, false>(D, nkv, wide)
-                               : pick_mfma_sk<QD_DTYPE_BF16, false>(D, nkv, wide);
+    return f16 ? pick_mfma_sk<QD_DTYPE_F16, true, false>(D, nkv, wide)
+               : pick_mfma_sk<QD_DTYPE_BF16, true, false>(D, nkv, wide);
+  if (hold)
+    return f16 ? pick_mfma_sk<QD_DTYPE_F16, false, true>(D, nkv, wide)
+               : pick_mfma_sk<QD_DTYPE_BF16, false, true>(D, nkv, wide);
+  return f16 ? pick_mfma_sk<QD_DTYPE_F16, false, false>(D, nkv, wide)
+             : pick_mfma_sk<QD_DTYPE_BF16, false, false>(D, nkv, wide);
 }
 
 // One wave per SIMD needs exactly 4 single-kv-head waves per workgroup;
@@ -1783,15 +1949,45 @@ int resident_blocks(KernelFn fn, int threads, size_t dyn_lds = 0) {
   return blocks;
 }
 
-// Dynamic LDS of the fused kernel at most (the partials a workgroup keeps
-// until its range ends; with the K tiles well inside gfx950's 160 KiB).
+// Dynamic LDS of the stream-K kernels at most: the staged result rows
+// (stage_lds_bytes) or the fused kernel's partials kept until the range
+// ends; with the K tiles well inside gfx950's 160 KiB.
 constexpr size_t kFusedMaxStash = 96 << 10;
+
+// Result rows are held in LDS until a workgroup's range ends (instead of
+// stored after each item) when the batch has at least one sequence per
+// kHoldWgsPerSeq workgroups: then ranges cross sequence boundaries often
+// and every store between items stalls the loads behind it.  Measured on
+// the decode kernel: cfg5 (256 sequences, 256 workgroups) 101-102 -> 92-96
+// us; cfg3 (64 sequences) 78-80 -> 82-87 us, cfg2 (32) unchanged, so the
+// shorter batches keep the stores after each item.
+constexpr int64_t kHoldWgsPerSeq = 2;
+
+bool hold_results(int batch, int64_t wgs) { return static_cast<int64_t>(batch) * kHoldWgsPerSeq >= wgs; }
+
+// LDS per wave for the result rows a wave holds until its range ends
+// (MfmaWave::stage_*): room for kStageItems items of NKV*g partial rows of
+// D+2 floats (an output row needs less), as many as fit in kFusedMaxStash
+// per workgroup, at least one.  A range with more items flushes early.
+constexpr int kStageItems = 4;
+
+int stage_wave_bytes(int g, int head_dim, int nkv, int wg_waves) {
+  const int item = (nkv * g * (head_dim + 2) * 4 + 15) & ~15;
+  int items = static_cast<int>(kFusedMaxStash / static_cast<size_t>(wg_waves) - kStageRecordBytes) / item;
+  if (items > kStageItems) items = kStageItems;
+  if (items < 1) items = 1;
+  return kStageRecordBytes + items * item;
+}
+
+size_t stage_lds_bytes(int g, int head_dim, int nkv, int wg_waves) {
+  return static_cast<size_t>(wg_waves) * stage_wave_bytes(g, head_dim, nkv, wg_waves);
+}
 
 // Raises `fn`'s dynamic LDS limit to kFusedMaxStash (above the default
 // 64 KiB), once per (device, kernel); false when HIP refuses.  Without a
 // device (plans made for sizing only, as resident_blocks' fallback) it
 // reports true.
-bool allow_fused_stash(KernelFn fn) {
+bool allow_dyn_lds(KernelFn fn) {
   struct Entry {
     int device;
     KernelFn fn;
@@ -1878,6 +2074,7 @@ struct AutoPlan {
   bool wide;        // stream-K: one wave per SIMD, kSkWidePrefetch groups in flight
   bool fused;       // stream-K: split sequences merged inside the decode kernel
   size_t stash_bytes;  // fused: dynamic LDS per workgroup for mid-range partials
+  size_t stage_bytes;  // otherwise: dynamic LDS per workgroup for staged result rows
   int splits;       // explicit-split path
   int chunk_pages;
   size_t ws_bytes;  // scratch bytes (kCounterBytes of counters first)
@@ -1912,27 +2109,39 @@ bool fused_applies(int batch, int q_heads, int kv_heads, int head_dim, int nkv, 
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
               int dtype, bool aligned, AutoPlan* ap, bool valu = false) {
-  *ap = AutoPlan{false, 0, 1, 1, false, false, 0, 1, 0, kCounterBytes, 0};
+  *ap = AutoPlan{false, 0, 1, 1, false, false, 0, 0, 1, 0, kCounterBytes, 0};
   if (batch <= 0) return QD_OK;
   if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
     int nkv = 1;
     const bool wide = !valu && sk_wide_applies(kv_heads, head_dim);
     int nw = sk_wg_waves(kv_heads, nkv, head_dim, valu, wide);
-    int resident = resident_blocks(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads)
-                                        : pick_mfma_sk_dt(dtype, head_dim, nkv, wide),
-                                   64 * nw);
+    const int g = q_heads / kv_heads;
+    KernelFn fn = valu ? pick_valu_sk_dt(dtype, g) : pick_mfma_sk_dt(dtype, head_dim, nkv, wide);
+    int resident = resident_blocks(fn, 64 * nw);
     if (!valu && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
       nkv = 2;
       nw = sk_wg_waves(kv_heads, nkv, head_dim);
-      resident = resident_blocks(pick_mfma_sk_dt(dtype, head_dim, nkv), 64 * nw);
+      fn = pick_mfma_sk_dt(dtype, head_dim, nkv);
+      resident = resident_blocks(fn, 64 * nw);
     }
     const int64_t gmax = static_cast<int64_t>(batch) *
                          ((static_cast<int64_t>(max_pages) * block_size + 15) / 16);
-    int64_t w = static_cast<int64_t>(resident) * kSkOversubscribe;
     const int64_t by_work = (gmax + kSkMinGroups - 1) / kSkMinGroups;
-    if (w > by_work) w = by_work;
-    if (w < 1) w = 1;
+    auto grid = [&](int res) {
+      int64_t w = static_cast<int64_t>(res) * kSkOversubscribe;
+      if (w > by_work) w = by_work;
+      return w < 1 ? int64_t{1} : w;
+    };
+    int64_t w = grid(resident);
+    // Result rows held in LDS until the range ends: the kernel's occupancy
+    // with that LDS sets the grid.
+    if (!valu && hold_results(batch, w)) {
+      const KernelFn hfn = pick_mfma_sk_dt(dtype, head_dim, nkv, wide && nkv == 1, false, true);
+      ap->stage_bytes = stage_lds_bytes(g, head_dim, nkv, nw);
+      if (!allow_dyn_lds(hfn)) return fail(QD_ERR_INVALID_VALUE, "dynamic LDS limit not raised");
+      w = grid(resident_blocks(hfn, 64 * nw, ap->stage_bytes));
+    }
     if (valu) {
       // The comparison variant runs on the product plan's grid (and fits its
       // workspace).
@@ -1948,7 +2157,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     ap->stash_bytes = fused_stash_bytes(kv_heads, head_dim, nkv, nw);
     const KernelFn ffn = pick_mfma_sk_dt(dtype, head_dim, nkv, ap->wide, true);
     if (kFusedByDefault && !valu && fused_applies(batch, q_heads, kv_heads, head_dim, nkv, w) &&
-        ap->stash_bytes <= kFusedMaxStash && allow_fused_stash(ffn)) {
+        ap->stash_bytes <= kFusedMaxStash && allow_dyn_lds(ffn)) {
       // The fused kernel's own occupancy (registers and the stash) bounds
       // the grid; without waits between workgroups a larger grid would
       // still be correct, only slower.
@@ -2020,6 +2229,7 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.meta = nullptr;
   prm.wg_waves = 1;
   prm.ctr = nullptr;
+  prm.stage_bytes = 0;
 #ifdef QD_STAMPS
   prm.stamps = g_stamps;
 #endif
@@ -2298,7 +2508,7 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   if (unfused) fused = false;
   if (force_fused) {
     if (valu || !fused_fits(batch, q_heads, kv_heads, head_dim, ap.wgs) || ap.stash_bytes > kFusedMaxStash ||
-        !allow_fused_stash(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, true)))
+        !allow_dyn_lds(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, true)))
       return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_FUSED needs MFMA math, batch * kv_heads <= 65536 and "
                                         "partial slots below 2 GiB");
     fused = true;
@@ -2309,6 +2519,7 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   prm.meta = reinterpret_cast<int*>(scratch + ap.meta_offset);
   prm.ctr = reinterpret_cast<uint32_t*>(scratch);
   prm.wg_waves = ap.wg_waves;
+  prm.stage_bytes = ap.stage_bytes ? static_cast<int>(ap.stage_bytes / ap.wg_waves) : 0;
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (fused) {
@@ -2319,8 +2530,9 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
     return launch_error();
   }
   if (stages & QD_STAGE_DECODE)
-    hipLaunchKernelGGL(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads) : pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide),
-                       dim3(ap.wgs), dim3(64 * ap.wg_waves), 0, stm, prm);
+    hipLaunchKernelGGL(valu ? pick_valu_sk_dt(dtype, q_heads / kv_heads)
+                            : pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, false, ap.stage_bytes > 0),
+                       dim3(ap.wgs), dim3(64 * ap.wg_waves), ap.stage_bytes, stm, prm);
   if (stages & QD_STAGE_MERGE) {
     const bool one_head = merge_one_head_per_wave(batch, q_heads);
     hipLaunchKernelGGL(pick_merge_sk_dt(dtype, head_dim, one_head),

@@ -9,9 +9,11 @@
 //                        the pool), 16-token groups in order; wave j reads
 //                        kv-heads j, j+waves, ... of each group (K: four 1 KiB
 //                        coalesced loads, V: four 16-byte row loads per lane,
-//                        head_dim 128), PF groups in flight, nontemporal
-//                        16-byte loads, a workgroup barrier every PF groups
-//                        (the decode kernel's lockstep).
+//                        head_dim 128), PF groups in flight (2 as the decode
+//                        kernel, or 1-4), nontemporal 16-byte loads, a
+//                        workgroup barrier every PF groups (the decode
+//                        kernel's lockstep), optionally a chain of dependent
+//                        multiply-adds per group in place of the decode math.
 //   probe_linear_kernel  a plain contiguous read of the same bytes (K pool
 //                        then V pool), W workgroups of `waves` waves, each
 //                        a contiguous 1/W share, nontemporal 16-byte loads,
@@ -28,7 +30,6 @@
 namespace {
 
 constexpr int kProbeD = 128;       // head_dim of the paged probe (16-bit elements)
-constexpr int kProbePf = 2;        // groups in flight per wave, as the decode kernel
 constexpr int kProbeMaxWaves = 8;
 
 struct ProbeGroup {
@@ -56,12 +57,32 @@ __device__ __forceinline__ uint32_t probe_fold(const ProbeGroup& g) {
   return x;
 }
 
+// Optional per-wave stamps (stamps != nullptr): {entry, end, XCD id} as
+// s_memrealtime ticks (100 MHz) at stamps[(workgroup * waves + wave) * 4].
+__device__ __forceinline__ uint64_t probe_xcc() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x;
+}
+
+// A dependent chain of `n` VALU multiply-adds on the group's data, standing
+// in for the decode kernel's math per group (the wave is busy, its next
+// loads wait); n = 0 leaves only the XOR fold.
+__device__ __forceinline__ uint32_t probe_work(uint32_t x, int n) {
+  float f = __uint_as_float((x & 0x007FFFFFu) | 0x3F800000u);  // in [1, 2)
+  for (int i = 0; i < n; ++i) f = fmaf(f, 0.999f, 0.001f);
+  return x ^ __float_as_uint(f);
+}
+
+template <int PF>
 __global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_paged_kernel(const char* k, const char* v,
                                                                           const int32_t* pages, int64_t npages,
-                                                                          int P, int Hkv, int waves,
-                                                                          uint32_t* sink) {
+                                                                          int P, int Hkv, int waves, int work,
+                                                                          uint32_t* sink, uint64_t* stamps) {
+  constexpr int kProbePf = PF;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
+  const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
   const int64_t W = gridDim.x;
   const int64_t p0 = blockIdx.x * npages / W;
   const int64_t p1 = (blockIdx.x + 1) * npages / W;
@@ -86,7 +107,7 @@ __global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_paged_kernel(const 
       for (int u = 0; u < kProbePf; ++u) {
         const int64_t nx = i + u + kProbePf - 1;
         probe_issue(buf[(u + kProbePf - 1) % kProbePf], base(nx, k), base(nx, v), row_bytes, lane);
-        acc ^= probe_fold(buf[u]);
+        acc ^= probe_work(probe_fold(buf[u]), work);
       }
     }
     for (; i < ngroups; i += kProbePf) {
@@ -94,11 +115,17 @@ __global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_paged_kernel(const 
       for (int u = 0; u < kProbePf; ++u) {
         const int64_t nx = i + u + kProbePf - 1;
         if (nx < ngroups) probe_issue(buf[(u + kProbePf - 1) % kProbePf], base(nx, k), base(nx, v), row_bytes, lane);
-        if (i + u < ngroups) acc ^= probe_fold(buf[u]);
+        if (i + u < ngroups) acc ^= probe_work(probe_fold(buf[u]), work);
       }
     }
   }
   sink[static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc;
+  if (stamps && lane == 0) {
+    uint64_t* s = stamps + (static_cast<int64_t>(blockIdx.x) * waves + wid) * 4;
+    s[0] = t_entry;
+    s[1] = __builtin_amdgcn_s_memrealtime();
+    s[2] = probe_xcc();
+  }
 }
 
 __global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_linear_kernel(const char* a, const char* b,
@@ -132,19 +159,26 @@ __global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_linear_kernel(const
 extern "C" {
 
 // mode 0: probe_paged_kernel over pages[0, npages) of k and v ([N, P, Hkv,
-// 128] 16-bit pools, P a multiple of 16); mode 1: probe_linear_kernel over
-// npages*P*Hkv*128*2 bytes of each pool.  `sink` holds wgs*waves*64 words.
-// Returns 0, or a HIP error (invalid shapes: QD_ERR_INVALID_VALUE).
+// 128] 16-bit pools, P a multiple of 16) with `pf` (1-4) groups in flight
+// per wave and `work` dependent multiply-adds per group, and per-wave
+// stamps when `stamps` (wgs*waves*4 words) is not NULL; mode 1:
+// probe_linear_kernel over npages*P*Hkv*128*2 bytes of each pool.  `sink`
+// holds wgs*waves*64 words.  Returns 0, or a HIP error (invalid shapes:
+// QD_ERR_INVALID_VALUE).
 int qd_diag_stream_read(const void* k, const void* v, const int32_t* pages, int64_t npages, int P, int Hkv,
-                        int wgs, int waves, int mode, void* sink, void* stream) {
+                        int wgs, int waves, int mode, int pf, int work, void* sink, void* stamps, void* stream) {
   if (!k || !v || !sink || npages <= 0 || P <= 0 || P % 16 != 0 || Hkv <= 0 || wgs <= 0 || waves <= 0 ||
-      waves > kProbeMaxWaves || (mode == 0 && !pages) || (mode != 0 && mode != 1))
+      waves > kProbeMaxWaves || (mode == 0 && !pages) || (mode != 0 && mode != 1) || pf < 1 || pf > 4 ||
+      work < 0 || work > 100000)
     return QD_ERR_INVALID_VALUE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (mode == 0) {
-    hipLaunchKernelGGL(probe_paged_kernel, dim3(wgs), dim3(64 * waves), 0, st, static_cast<const char*>(k),
-                       static_cast<const char*>(v), pages, npages, P, Hkv, waves, static_cast<uint32_t*>(sink));
+    auto fn = pf == 1 ? probe_paged_kernel<1> : pf == 2 ? probe_paged_kernel<2> : pf == 3 ? probe_paged_kernel<3>
+                                                                                        : probe_paged_kernel<4>;
+    hipLaunchKernelGGL(fn, dim3(wgs), dim3(64 * waves), 0, st, static_cast<const char*>(k),
+                       static_cast<const char*>(v), pages, npages, P, Hkv, waves, work,
+                       static_cast<uint32_t*>(sink), static_cast<uint64_t*>(stamps));
   } else {
     const int64_t bytes = npages * P * static_cast<int64_t>(Hkv) * kProbeD * 2;
     hipLaunchKernelGGL(probe_linear_kernel, dim3(wgs), dim3(64 * waves), 0, st, static_cast<const char*>(k),

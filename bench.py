@@ -62,6 +62,9 @@ def parse():
     ap.add_argument("--merge", choices=["auto", "fused", "unfused"], default="auto",
                     help="where split sequences are merged (C ABI path, QD_STAGE_FUSED/UNFUSED)")
     ap.add_argument("--launches", type=int, default=6, help="--mode stamps: launches recorded")
+    ap.add_argument("--probe-pf", type=int, default=2, help="--mode read: groups in flight per wave (1-4)")
+    ap.add_argument("--probe-work", type=int, default=0,
+                    help="--mode read: dependent multiply-adds per group standing in for the decode math")
     ap.add_argument("--op", choices=["decode", "kv_append", "mla", "sweep"], default="decode",
                     help="kv_append: time the paged cache append on the config's shapes instead; "
                          "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config; "
@@ -173,7 +176,7 @@ def stamps_mode(args) -> None:
     ws = cabi.auto_workspace(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size,
                              table.shape[1], dt, dev)
     out = torch.empty_like(q)
-    buf = torch.zeros(waves * 8, dtype=torch.int64, device=dev)
+    buf = torch.zeros(waves * 16, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream(dev)
     scale = 1.0 / math.sqrt(cfg.head_dim)
 
@@ -196,7 +199,7 @@ def stamps_mode(args) -> None:
         torch.cuda.synchronize()
         launch(n, True)
         torch.cuda.synchronize()
-        s = buf.view(waves, 8).cpu().tolist()
+        s = buf.view(waves, 16).cpu().tolist()
         t0 = min(r[0] for r in s)
         us = lambda x: (x - t0) / 100.0  # noqa: E731  (100 MHz ticks)
         ran = [r for r in s if r[1]]  # waves that held work
@@ -228,6 +231,13 @@ def stamps_mode(args) -> None:
         for r in ran:
             xcd.setdefault(int(r[6]), []).append(us(r[2]))
         rec["stream_end_p50_by_xcd_us"] = {str(x): round(_pct(v_, .5), 2) for x, v_ in sorted(xcd.items())}
+        # Shader clock of each XCD over its waves' streaming: s_memtime ticks
+        # per s_memrealtime tick (100 MHz), in MHz.
+        clk = {}
+        for r in ran:
+            if r[2] > r[0] and r[9] > r[8]:
+                clk.setdefault(int(r[6]), []).append((r[9] - r[8]) / ((r[2] - r[0]) / 100.0))
+        rec["shader_mhz_by_xcd"] = {str(x): round(_pct(v_, .5), 1) for x, v_ in sorted(clk.items())}
         print(json.dumps(rec), flush=True)
 
 
@@ -246,7 +256,7 @@ def read_mode(args) -> None:
 
     L = ctypes.CDLL(_build.DIAG_LIB)
     V, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
-    L.qd_diag_stream_read.argtypes = [V, V, V, I64, I, I, I, I, I, V, V]
+    L.qd_diag_stream_read.argtypes = [V, V, V, I64, I, I, I, I, I, I, I, V, V, V]
     cfg = get_config(args.config)
     if cfg.head_dim != 128 or cfg.dtype not in (torch.float16, torch.bfloat16):
         raise SystemExit("--mode read covers 16-bit caches with head_dim 128")
@@ -277,8 +287,8 @@ def read_mode(args) -> None:
     for name, mode in (("paged", 0), ("linear", 1)):
         def step(i, mode=mode):
             rc = L.qd_diag_stream_read(ks[i % pools].data_ptr(), vs[i % pools].data_ptr(), pages.data_ptr(),
-                                       npages, cfg.block_size, cfg.kv_heads, wgs, waves, mode, sink.data_ptr(),
-                                       stream.cuda_stream)
+                                       npages, cfg.block_size, cfg.kv_heads, wgs, waves, mode, args.probe_pf,
+                                       args.probe_work, sink.data_ptr(), None, stream.cuda_stream)
             if rc:
                 raise RuntimeError(f"qd_diag_stream_read failed: {rc}")
         samples = time_samples(step, args.steps, args.warmup, stream)
@@ -286,10 +296,36 @@ def read_mode(args) -> None:
         res[name] = {"us_per_launch": round(ms * 1e3, 3), "tbs": round(probe_bytes / (ms * 1e-3) / 1e12, 4),
                      "samples_us": [round(x * 1e3, 3) for x in samples]}
         log(f"{name}: {ms * 1e3:.2f} us, {probe_bytes / (ms * 1e-3) / 1e12:.3f} TB/s")
+    # Per-wave end stamps of single paged launches, one per pool: the spread
+    # of the workgroups' end times by XCD with no decode work at all.
+    stamps = torch.zeros(wgs * waves * 4, dtype=torch.int64, device=dev)
+    by_pool = []
+    for i in range(pools):
+        stamps.zero_()
+        torch.cuda.synchronize()
+        rc = L.qd_diag_stream_read(ks[i].data_ptr(), vs[i].data_ptr(), pages.data_ptr(), npages, cfg.block_size,
+                                   cfg.kv_heads, wgs, waves, 0, args.probe_pf, args.probe_work, sink.data_ptr(),
+                                   stamps.data_ptr(), stream.cuda_stream)
+        if rc:
+            raise RuntimeError(f"qd_diag_stream_read failed: {rc}")
+        torch.cuda.synchronize()
+        s = stamps.view(-1, 4).cpu().tolist()
+        t0 = min(r[0] for r in s)
+        ends = [(r[1] - t0) / 100.0 for r in s]
+        xcd = {}
+        for r, e in zip(s, ends):
+            xcd.setdefault(int(r[2]), []).append(e)
+        by_pool.append({"pool": i, "end_us": {"p10": round(_pct(ends, .1), 2), "p50": round(_pct(ends, .5), 2),
+                                              "max": round(max(ends), 2)},
+                        "end_p50_by_xcd_us": {str(x): round(_pct(v_, .5), 2) for x, v_ in sorted(xcd.items())}})
+        log(f"paged probe, pool {i}: end p50 {by_pool[-1]['end_us']['p50']} max {by_pool[-1]['end_us']['max']} us; "
+            f"by XCD {by_pool[-1]['end_p50_by_xcd_us']}")
+    res["paged"]["stamps_by_pool"] = by_pool
     alg = algorithmic_bytes(lengths, cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size,
                             q.element_size())
     rate = res["paged"]["tbs"] * 1e12
     print(json.dumps({"mode": "read", "config": cfg.name, "bytes_read_per_launch": probe_bytes,
+                      "probe_groups_in_flight": args.probe_pf, "probe_work_per_group": args.probe_work,
                       "pages": npages, "workgroups": wgs, "waves_per_workgroup": waves, "pools_rotated": pools,
                       "paged": res["paged"], "linear": res["linear"], "peak_tbs": PEAK_HBM_GBS / 1e3,
                       "decode_algorithmic_bytes": alg,

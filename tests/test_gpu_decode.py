@@ -822,3 +822,34 @@ def test_torch_op_on_concurrent_streams(gpu):
     for i in range(2):
         for j, o in enumerate(outs[i]):
             assert torch.equal(o, refs[i]), (i, j)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_held_results_flush_when_full(gpu, dtype):
+    """Batches with at least one sequence per two workgroups hold each
+    wave's result rows in LDS until its range ends.  3000 one- and
+    two-group sequences (and some empty ones) give every wave more items
+    than its LDS area and record table hold, so the area is flushed
+    early, repeatedly; every row must match the oracle, and the -1 padded
+    wide table must not matter."""
+    rng = np.random.default_rng(91)
+    lengths = [int(x) for x in rng.integers(1, 33, size=3000)]
+    for i in (0, 7, 1500, 2999):
+        lengths[i] = 0
+    say(f"held results, many items per wave: {DT_NAME[dtype]} B={len(lengths)}")
+    q, k, v, table, lens = make_decode_case(lengths=lengths, q_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                                            dtype=dtype, seed=92, exact_pool=True)
+    case = to_dev((q, k, v, table, lens), gpu)
+    kind, waves, _, _ = cabi.auto_info(len(lengths), 32, 8, 128, 16, table.shape[1], cabi.DTYPE[dtype])
+    assert kind == 1
+    ref, rows = oracle_rows(case)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    assert_close(out, ref, DT_NAME[dtype], rows, "held results")
+    # Same bits through the C ABI on a NaN-filled workspace.
+    ws = cabi.auto_workspace(len(lengths), 32, 8, 128, 16, table.shape[1], cabi.DTYPE[dtype], gpu, fill=0xFF)
+    out_c = torch.full_like(case[0], float("nan"))
+    rc = cabi.auto_launch(*case, out_c, scale=1 / math.sqrt(128), workspace=ws)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_c)
