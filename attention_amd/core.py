@@ -42,12 +42,18 @@ def is_cuda_extension_loaded() -> bool:
     return _LOAD_ERROR is None
 
 
-def _require_extension() -> None:
+def _require_extension(detail: bool = False) -> None:
+    """The reference's missing-extension errors (``core.py:31-35`` for
+    ``gqa_decode``, ``:51`` and ``:62`` for the others): a ``RuntimeError``
+    with the reference's first sentence (PyTorch-ROCm calls the HIP device
+    "CUDA") and the load error as its cause.  ``detail`` adds the build hint,
+    in place of the reference's pip/nvcc one."""
     if _LOAD_ERROR is not None:
-        raise RuntimeError(
-            "qd_attention HIP extension was not loaded. Build it in-tree with "
-            "`python -m attention_amd._build` on a ROCm machine with hipcc."
-        ) from _LOAD_ERROR
+        msg = "qd_attention CUDA extension was not loaded"
+        if detail:
+            msg += (". Build it in-tree with `python -m attention_amd._build` on a machine with hipcc "
+                    "and a ROCm-enabled PyTorch build.")
+        raise RuntimeError(msg) from _LOAD_ERROR
 
 
 def gqa_decode(
@@ -67,7 +73,7 @@ def gqa_decode(
     q's dtype.  The context-split count comes from the library's launch plan
     (static shapes only, no host synchronization); forward only.
     """
-    _require_extension()
+    _require_extension(detail=True)
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     return torch.ops.qd_attention.gqa_decode(
@@ -118,6 +124,5 @@ def kv_append(key, value, k_cache, v_cache, block_table, positions):
     ``(block_table[b, pos // P], pos % P)``.  Destinations are caller-owned
     and must be distinct; a position or page id outside the table or the
     pool is skipped rather than written."""
-    if _LOAD_ERROR is not None:
-        raise RuntimeError("qd_attention HIP extension was not loaded") from _LOAD_ERROR
+    _require_extension()
     torch.ops.qd_attention.kv_append(key, value, k_cache, v_cache, block_table, positions)

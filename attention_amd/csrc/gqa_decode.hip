@@ -2192,8 +2192,15 @@ int check_launch_shapes(int batch, int q_heads, int kv_heads, int head_dim, int 
   if (dtype != QD_DTYPE_F32 && dtype != QD_DTYPE_F16 && dtype != QD_DTYPE_BF16)
     return fail(QD_ERR_INVALID_VALUE, "q/k/v must be float32/float16/bfloat16");
   if (!(isfinite(scale) && scale > 0.f)) return fail(QD_ERR_INVALID_VALUE, "scale must be positive and finite");
-  if (batch > 65535 || kv_heads > 65535 || q_heads > 65535)
-    return fail(QD_ERR_INVALID_VALUE, "batch and head counts must be <= 65535 (grid limit)");
+  // The split and merge grids put the batch (and the explicit split layout
+  // the kv-heads) in a grid dimension limited to 65535.  The reference
+  // validates these sizes only up to INT_MAX (gqa_decode.cu:133-138) and a
+  // launch beyond the grid fails with "gqa_decode kernel launch failed:
+  // <error>" (:179-181); the same error and text are reported here before
+  // any launch.
+  if (batch > 65535 || kv_heads > 65535)
+    return fail(static_cast<int>(hipErrorInvalidConfiguration),
+                std::string("gqa_decode kernel launch failed: ") + hipGetErrorString(hipErrorInvalidConfiguration));
   return QD_OK;
 }
 

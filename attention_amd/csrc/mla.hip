@@ -398,6 +398,15 @@ struct MlaParams {
   float sl2;        // scale * log2(e)
 };
 
+// Scale s of a half-precision partial block: the values are stored as o / s
+// in fp16.  s is the block's largest |o|, clamped up to the smallest normal
+// float when it is below it (1 / s must stay finite: a subnormal s would
+// overflow 1 / s to inf, and a zero column then stores 0 * inf = NaN), and 1
+// for an all-zero block.
+__device__ __forceinline__ float half_partial_scale(float amax) {
+  return amax >= __FLT_MIN__ ? amax : (amax > 0.f ? __FLT_MIN__ : 1.f);
+}
+
 // Two floats as fp16, round to nearest even, lo in the low half.
 __device__ __forceinline__ uint32_t pack_f16_rne(float lo, float hi) {
   const f16x2 v = __builtin_convertvector(f32x2{lo, hi}, f16x2);
@@ -1485,8 +1494,7 @@ __global__ __launch_bounds__(kAttendThreads) void mla_attend_wave_kernel(MlaPara
         } else {
           // Half-precision partial row (kHalfHeader): block bb as fp16
           // values o / s_bb, s_bb the block's largest |o| for the head.
-          const float sbb0 = fmaxf(amax, ml[(wv ^ 1) * 16 + r16]);
-          const float sbb = sbb0 > 0.f ? sbb0 : 1.f;
+          const float sbb = half_partial_scale(fmaxf(amax, ml[(wv ^ 1) * 16 + r16]));
           const float isc = 1.f / sbb;
           float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kHalfPst);
           if (q4 == 0 && eh == 0) {
@@ -2148,7 +2156,7 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
                                        fmaxf(fabsf(acc[cb][2]), fabsf(acc[cb][3]))));
             amax = fmaxf(amax, __shfl_xor(amax, 16));
             amax = fmaxf(amax, __shfl_xor(amax, 32));
-            sk[k] = amax > 0.f ? amax : 1.f;
+            sk[k] = half_partial_scale(amax);
           }
           float* pr = p.part + ((static_cast<int64_t>(w) + r) * p.H + h) * static_cast<int64_t>(kHalfPst);
           if (q4 == 0) {

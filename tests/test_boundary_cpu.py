@@ -227,12 +227,15 @@ def _launch_args(**over):
     (dict(splits=0), "splits must be in [1, 65535]"),
     (dict(splits=4, chunk=2), "splits * chunk_pages must cover max_pages"),
     (dict(splits=4), "workspace too small for [B,Hq,splits,D+2] float32"),
-    (dict(B=70000), "batch and head counts must be <= 65535 (grid limit)"),
+    (dict(B=70000), "gqa_decode kernel launch failed: invalid configuration argument"),
+    (dict(Hq=70000, Hkv=70000), "gqa_decode kernel launch failed: invalid configuration argument"),
     (dict(q=None), "null tensor pointer"),
 ])
 def test_launch_argument_errors(over, msg):
     rc = cabi.lib().qd_gqa_decode_launch(*_launch_args(**over))
-    assert rc == 1
+    # Argument errors are hipErrorInvalidValue (1); a grid beyond the launch
+    # limits is the launch error itself, hipErrorInvalidConfiguration (9).
+    assert rc == (9 if msg.startswith("gqa_decode kernel launch failed") else 1)
     assert cabi.error_string(rc) == msg
 
 
@@ -395,10 +398,14 @@ def test_public_api_surface():
 def test_missing_extension_raises_runtime_error(monkeypatch):
     monkeypatch.setattr(core, "_LOAD_ERROR", OSError("libqd_attention_torch.so: missing"))
     q = torch.zeros(1, 8, 64)
-    with pytest.raises(RuntimeError, match="HIP extension was not loaded"):
+    # The reference's texts (core.py:31-35, :51, :62): the first sentence is
+    # the same, gqa_decode adds a build hint.
+    with pytest.raises(RuntimeError, match=r"^qd_attention CUDA extension was not loaded\. Build it in-tree"):
         attention_amd.gqa_decode(q, q, q, q, q)
-    with pytest.raises(RuntimeError, match="HIP extension was not loaded"):
+    with pytest.raises(RuntimeError, match=r"^qd_attention CUDA extension was not loaded$"):
         attention_amd.gqa_decode_split(q, q, q, q, q)
+    with pytest.raises(RuntimeError, match=r"^qd_attention CUDA extension was not loaded$"):
+        attention_amd.kv_append(q, q, q, q, q, q)
     assert not attention_amd.is_cuda_extension_loaded()
 
 

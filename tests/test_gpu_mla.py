@@ -454,3 +454,73 @@ def test_mla_validation_messages_on_device(gpu):
     empty = attention_amd.mla_latent_attention(qa[:0], c["q_rope"][:0], c["cache"], c["table"][:0],
                                                c["lens"][:0], c["positions"][:0], scale=0.1)
     assert empty.shape == (0, 1, 4, 32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_WAVE), (16, 0)], ids=["shared-h64", "wave-h64", "wave-h16"])
+def test_mla_attend_subnormal_partial_block(gpu, dtype, heads, flags):
+    """Split rows stored as half-precision blocks scaled by each block's
+    largest |value|: here the tokens that carry the softmax (even ones) have
+    an all-zero first 128-column latent block, and the only nonzero values
+    of that block come from tokens weighted about 2^-140 below them, so the
+    block's accumulator maximum is subnormal (or flushed to zero).  The scale
+    must keep 1/scale finite: the output is finite and matches the oracle."""
+    say(f"mla_attend subnormal partial block {ODT[dtype]} heads={heads} flags={flags}")
+    c = _case(gpu, lengths=[3000, 1700], q_len=1, heads=heads, block_size=64, dtype=dtype, seed=13)
+    Dc = c["w_uk"].shape[-1]
+    Dr = c["q_rope"].shape[-1]
+    scale = default_mla_scale(c["q_nope"].shape[-1], Dr)
+    # Scores from the rope part only: q_rope = e_0 for every head, rope key
+    # dim 0 = `high` for even tokens and 0 for odd ones, 140 / log2(e) apart
+    # after scaling; the latent query is zero.
+    high = float(torch.tensor(140.0 / (scale * 1.4426950408889634)).to(dtype))
+    cache = c["cache"].float()
+    ids = torch.arange(cache.shape[0] * cache.shape[1], device=cache.device).view(cache.shape[0], cache.shape[1])
+    even = (ids % 2 == 0)
+    cache[..., Dc:] = 0.0
+    cache[..., Dc] = torch.where(even, torch.full_like(cache[..., Dc], high), torch.zeros_like(cache[..., Dc]))
+    block0 = cache[..., :128]
+    cache[..., :128] = torch.where(even[..., None], torch.zeros_like(block0), block0 * 0.01)
+    c["cache"] = cache.to(dtype)
+    qr = torch.zeros_like(c["q_rope"].float())
+    qr[..., 0] = 1.0
+    c["q_rope"] = qr.to(dtype)
+    qa = torch.zeros(c["q_nope"].shape[:3] + (Dc,), dtype=dtype, device=gpu)
+    out = torch.empty_like(qa)
+    rc = cabi.mla_attend(qa, c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"], out, scale=scale,
+                         splits=3, flags=flags)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _close(out, _oracle_attend(c, qa, scale, dtype=dtype), dtype, "subnormal partial block")
+
+
+@pytest.mark.parametrize("heads,flags", [(64, 0), (64, QD_FLAG_MLA_WAVE), (16, 0)], ids=["shared-h64", "wave-h64", "wave-h16"])
+def test_mla_attend_fp16_partial_error_bound(gpu, heads, flags):
+    """The half-precision partials keep each value to 2^-12 of its
+    128-column block's largest |value|, so on fp16 the split run (rows over
+    three workgroups, merged from fp16 partials) may differ from the unsplit
+    run (no partials) by 2^-12 of each row's block maximum, weighted; the
+    rows' block maxima exceed the merged block's by about sqrt(3) on these
+    random inputs, so the test allows 4 * 2^-12 of the merged block's
+    largest |output| per element, plus the two outputs' own rounding (half
+    an fp16 ulp each)."""
+    say(f"mla_attend fp16 partial error bound heads={heads} flags={flags}")
+    c = _case(gpu, lengths=[3000, 700, 2000, 1500], q_len=1, heads=heads, block_size=64, dtype=torch.float16, seed=17)
+    qa = _absorbed(c, torch.float16).to(torch.float16).to(gpu)
+    scale = default_mla_scale(c["q_nope"].shape[-1], c["q_rope"].shape[-1])
+    outs = {}
+    for splits in (1, 3):
+        out = torch.empty_like(qa)
+        rc = cabi.mla_attend(qa, c["q_rope"], c["cache"], c["table"], c["lens"], c["positions"], out, scale=scale,
+                             splits=splits, flags=flags)
+        assert rc == 0, cabi.error_string(rc)
+        torch.cuda.synchronize()
+        outs[splits] = out.float().cpu()
+    one, three = outs[1], outs[3]
+    blocks = one.view(*one.shape[:-1], -1, 128)
+    bmax = blocks.abs().amax(dim=-1, keepdim=True).expand_as(blocks).reshape(one.shape)
+    ulp = lambda x: 2.0 ** (torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -14))) - 10)  # noqa: E731
+    bound = 4 * 2.0 ** -12 * bmax + 0.5 * ulp(one) + 0.5 * ulp(three) + 2.0 ** -24
+    diff = (three - one).abs()
+    assert torch.all(diff <= bound), f"max excess {(diff - bound).max().item():.3e}"
