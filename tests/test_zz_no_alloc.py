@@ -1,8 +1,10 @@
 """The no-allocation entry point (qd_gqa_decode_auto_noalloc): the same
 output as the automatic entry point with a caller workspace, bit for bit,
 on two calls in a row (the second with a smaller input, so the scratch
-holds the first call's leftovers), and a clear error, before anything is
-enqueued, for shapes whose scratch does not fit."""
+holds the first call's leftovers), also when its first call on the device is
+made inside a HIP graph capture and the graph is replayed between other
+calls, and a clear error, before anything is enqueued, for shapes whose
+scratch does not fit."""
 from __future__ import annotations
 
 import math
@@ -25,6 +27,56 @@ def test_noalloc_rejects_oversized_shapes():
     assert rc == 1
     assert "more than the no-allocation scratch holds" in cabi.error_string(rc)
     assert cabi.lib().qd_gqa_decode_noalloc_scratch_bytes() == 16 << 20
+
+
+def _decode_case(lengths, seed, gpu):
+    case = make_decode_case(lengths=lengths, q_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                            dtype=torch.bfloat16, seed=seed)
+    return [x.to(gpu) for x in case]
+
+
+def _auto_reference(q, k, v, table, lens, gpu):
+    B, Hq, D = q.shape
+    _, P, Hkv, _ = k.shape
+    ws = cabi.auto_workspace(B, Hq, Hkv, D, P, table.shape[1], cabi.DTYPE[q.dtype], gpu, fill=0xFF)
+    ref = torch.full_like(q, float("nan"))
+    rc = cabi.auto_launch(q, k, v, table, lens, ref, scale=1 / math.sqrt(D), workspace=ws)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    return ref
+
+
+# Placed first among this file's GPU tests, which hold the only no-alloc
+# calls of the suite: in a full run (and alone) the call captured here is the
+# process's first on the device, the one that looks up the scratch address.
+@pytest.mark.gpu
+def test_noalloc_first_call_inside_graph_capture(gpu):
+    q, k, v, table, lens = _decode_case([1, 700, 0, 33, 2500, 129], seed=11, gpu=gpu)
+    D = q.shape[2]
+    out = torch.full_like(q, float("nan"))
+    say(f"no-alloc captured in a graph: B={q.shape[0]}")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = cabi.auto_noalloc_launch(q, k, v, table, lens, out, scale=1 / math.sqrt(D))
+    assert rc == 0, cabi.error_string(rc)
+    # Other work between replays: eager no-alloc calls on another shape
+    # (which leave their partials in the shared scratch), and new queries
+    # written into the captured input.
+    other = _decode_case([5000, 1, 900], seed=12, gpu=gpu)
+    other_out = torch.full_like(other[0], float("nan"))
+    gen = torch.Generator(device="cpu").manual_seed(13)
+    for replay in range(4):
+        if replay:
+            q.copy_(torch.randn(q.shape, generator=gen).to(q.dtype))
+        ref = _auto_reference(q, k, v, table, lens, gpu)
+        rc = cabi.auto_noalloc_launch(*other, other_out, scale=1 / math.sqrt(D))
+        assert rc == 0, cabi.error_string(rc)
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        say(f"replay {replay}")
+        assert torch.equal(out, ref), f"replay {replay}"
+        assert torch.equal(other_out, _auto_reference(*other, gpu)), f"eager call after replay {replay}"
 
 
 @pytest.mark.gpu
