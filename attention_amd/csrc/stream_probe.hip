@@ -14,6 +14,11 @@
 //                        workgroup barrier every PF groups (the decode
 //                        kernel's lockstep), optionally a chain of dependent
 //                        multiply-adds per group in place of the decode math.
+//                        With `split` 2 the waves come in two sets that take
+//                        alternate groups of the range (waves = 2 * kv-head
+//                        waves): twice the waves per CU for caches with few
+//                        kv-heads; a set with one group fewer re-reads its
+//                        last group so that both meet the same barriers.
 //   probe_linear_kernel  a plain contiguous read of the same bytes (K pool
 //                        then V pool), W workgroups of `waves` waves, each
 //                        a contiguous 1/W share, nontemporal 16-byte loads,
@@ -78,7 +83,8 @@ template <int PF>
 __global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_paged_kernel(const char* k, const char* v,
                                                                           const int32_t* pages, int64_t npages,
                                                                           int P, int Hkv, int waves, int work,
-                                                                          uint32_t* sink, uint64_t* stamps) {
+                                                                          int split, uint32_t* sink,
+                                                                          uint64_t* stamps) {
   constexpr int kProbePf = PF;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -87,12 +93,17 @@ __global__ __launch_bounds__(64 * kProbeMaxWaves) void probe_paged_kernel(const 
   const int64_t p0 = blockIdx.x * npages / W;
   const int64_t p1 = (blockIdx.x + 1) * npages / W;
   const int gpp = P / 16;
-  const int64_t ngroups = (p1 - p0) * gpp;
+  const int64_t ngroups_all = (p1 - p0) * gpp;
+  const int hw = waves / split;   // waves per set
+  const int par = wid / hw;       // this wave's set: groups par, par + split, ...
+  const int64_t ngroups = (ngroups_all + split - 1) / split;
   const int64_t row_bytes = static_cast<int64_t>(Hkv) * kProbeD * 2;
-  const bool lockstep = Hkv == waves;
+  const bool lockstep = Hkv == hw;
   uint32_t acc = 0;
-  for (int kvh = wid; kvh < Hkv; kvh += waves) {
-    auto base = [&](int64_t gi, const char* pool) {
+  for (int kvh = wid % hw; kvh < Hkv; kvh += hw) {
+    auto base = [&](int64_t gk, const char* pool) {
+      int64_t gi = gk * split + par;
+      gi = gi < ngroups_all ? gi : ngroups_all - 1;
       const int64_t page = pages[p0 + gi / gpp];
       return pool + (page * P + 16 * (gi % gpp)) * row_bytes + static_cast<int64_t>(kvh) * kProbeD * 2;
     };
@@ -160,16 +171,18 @@ extern "C" {
 
 // mode 0: probe_paged_kernel over pages[0, npages) of k and v ([N, P, Hkv,
 // 128] 16-bit pools, P a multiple of 16) with `pf` (1-4) groups in flight
-// per wave and `work` dependent multiply-adds per group, and per-wave
+// per wave, `work` dependent multiply-adds per group, `split` (1 or 2,
+// dividing `waves`) sets of waves on alternate groups, and per-wave
 // stamps when `stamps` (wgs*waves*4 words) is not NULL; mode 1:
 // probe_linear_kernel over npages*P*Hkv*128*2 bytes of each pool.  `sink`
 // holds wgs*waves*64 words.  Returns 0, or a HIP error (invalid shapes:
 // QD_ERR_INVALID_VALUE).
 int qd_diag_stream_read(const void* k, const void* v, const int32_t* pages, int64_t npages, int P, int Hkv,
-                        int wgs, int waves, int mode, int pf, int work, void* sink, void* stamps, void* stream) {
+                        int wgs, int waves, int mode, int pf, int work, int split, void* sink, void* stamps,
+                        void* stream) {
   if (!k || !v || !sink || npages <= 0 || P <= 0 || P % 16 != 0 || Hkv <= 0 || wgs <= 0 || waves <= 0 ||
       waves > kProbeMaxWaves || (mode == 0 && !pages) || (mode != 0 && mode != 1) || pf < 1 || pf > 4 ||
-      work < 0 || work > 100000)
+      work < 0 || work > 100000 || (split != 1 && split != 2) || waves % split != 0)
     return QD_ERR_INVALID_VALUE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
@@ -177,7 +190,7 @@ int qd_diag_stream_read(const void* k, const void* v, const int32_t* pages, int6
     auto fn = pf == 1 ? probe_paged_kernel<1> : pf == 2 ? probe_paged_kernel<2> : pf == 3 ? probe_paged_kernel<3>
                                                                                         : probe_paged_kernel<4>;
     hipLaunchKernelGGL(fn, dim3(wgs), dim3(64 * waves), 0, st, static_cast<const char*>(k),
-                       static_cast<const char*>(v), pages, npages, P, Hkv, waves, work,
+                       static_cast<const char*>(v), pages, npages, P, Hkv, waves, work, split,
                        static_cast<uint32_t*>(sink), static_cast<uint64_t*>(stamps));
   } else {
     const int64_t bytes = npages * P * static_cast<int64_t>(Hkv) * kProbeD * 2;

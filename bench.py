@@ -63,6 +63,8 @@ def parse():
                     help="where split sequences are merged (C ABI path, QD_STAGE_FUSED/UNFUSED)")
     ap.add_argument("--launches", type=int, default=6, help="--mode stamps: launches recorded")
     ap.add_argument("--probe-pf", type=int, default=2, help="--mode read: groups in flight per wave (1-4)")
+    ap.add_argument("--probe-split", type=int, default=1, choices=(1, 2),
+                    help="--mode read: sets of waves taking alternate groups (2: twice the waves per CU)")
     ap.add_argument("--probe-work", type=int, default=0,
                     help="--mode read: dependent multiply-adds per group standing in for the decode math")
     ap.add_argument("--op", choices=["decode", "kv_append", "mla", "sweep"], default="decode",
@@ -256,7 +258,7 @@ def read_mode(args) -> None:
 
     L = ctypes.CDLL(_build.DIAG_LIB)
     V, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
-    L.qd_diag_stream_read.argtypes = [V, V, V, I64, I, I, I, I, I, I, I, V, V, V]
+    L.qd_diag_stream_read.argtypes = [V, V, V, I64, I, I, I, I, I, I, I, I, V, V, V]
     cfg = get_config(args.config)
     if cfg.head_dim != 128 or cfg.dtype not in (torch.float16, torch.bfloat16):
         raise SystemExit("--mode read covers 16-bit caches with head_dim 128")
@@ -278,7 +280,9 @@ def read_mode(args) -> None:
     npages = pages.numel()
     assert int(pages.min()) >= 0 and int(pages.max()) < k.shape[0]
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    waves = min(cfg.kv_heads, 8)
+    waves = min(cfg.kv_heads, 8) * args.probe_split
+    if waves > 8:
+        raise SystemExit("--probe-split 2 needs at most 4 kv-heads")
     wgs = cus
     sink = torch.empty(wgs * waves * 64, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
@@ -288,7 +292,8 @@ def read_mode(args) -> None:
         def step(i, mode=mode):
             rc = L.qd_diag_stream_read(ks[i % pools].data_ptr(), vs[i % pools].data_ptr(), pages.data_ptr(),
                                        npages, cfg.block_size, cfg.kv_heads, wgs, waves, mode, args.probe_pf,
-                                       args.probe_work, sink.data_ptr(), None, stream.cuda_stream)
+                                       args.probe_work, args.probe_split, sink.data_ptr(), None,
+                                       stream.cuda_stream)
             if rc:
                 raise RuntimeError(f"qd_diag_stream_read failed: {rc}")
         samples = time_samples(step, args.steps, args.warmup, stream)
@@ -304,8 +309,8 @@ def read_mode(args) -> None:
         stamps.zero_()
         torch.cuda.synchronize()
         rc = L.qd_diag_stream_read(ks[i].data_ptr(), vs[i].data_ptr(), pages.data_ptr(), npages, cfg.block_size,
-                                   cfg.kv_heads, wgs, waves, 0, args.probe_pf, args.probe_work, sink.data_ptr(),
-                                   stamps.data_ptr(), stream.cuda_stream)
+                                   cfg.kv_heads, wgs, waves, 0, args.probe_pf, args.probe_work, args.probe_split,
+                                   sink.data_ptr(), stamps.data_ptr(), stream.cuda_stream)
         if rc:
             raise RuntimeError(f"qd_diag_stream_read failed: {rc}")
         torch.cuda.synchronize()
@@ -326,6 +331,7 @@ def read_mode(args) -> None:
     rate = res["paged"]["tbs"] * 1e12
     print(json.dumps({"mode": "read", "config": cfg.name, "bytes_read_per_launch": probe_bytes,
                       "probe_groups_in_flight": args.probe_pf, "probe_work_per_group": args.probe_work,
+                      "probe_split": args.probe_split,
                       "pages": npages, "workgroups": wgs, "waves_per_workgroup": waves, "pools_rotated": pools,
                       "paged": res["paged"], "linear": res["linear"], "peak_tbs": PEAK_HBM_GBS / 1e3,
                       "decode_algorithmic_bytes": alg,
