@@ -28,11 +28,12 @@ ARCH = "gfx950"
 
 HIP_LIB = os.path.join(LIB_DIR, "libqd_attention.so")
 TORCH_LIB = os.path.join(LIB_DIR, "libqd_attention_torch.so")
-# Diagnostic library, loaded only by bench.py --mode stamps / --mode read:
-# a copy of the decode kernels with per-wave timestamps (gqa_decode.hip
-# built with -DQD_STAMPS) and the streaming-read probes (stream_probe.hip).
+# Diagnostic library, loaded only by bench.py --mode stamps / read /
+# mla-stamps: copies of the decode and MLA kernels with per-wave timestamps
+# (gqa_decode.hip and mla.hip built with -DQD_STAMPS) and the streaming-read
+# probes (stream_probe.hip).
 DIAG_LIB = os.path.join(LIB_DIR, "libqd_attention_diag.so")
-DIAG_SOURCES = ["gqa_decode", "stream_probe"]
+DIAG_SOURCES = ["gqa_decode", "stream_probe", "mla"]
 
 # Packed-fp32 VALU forms are disabled for every HIP compile.
 HIP_FLAGS = [
@@ -134,13 +135,13 @@ def build(verbose: bool = False, incremental: bool = False) -> None:
 
 
 def build_diag(verbose: bool = False) -> None:
-    """The diagnostic library: gqa_decode.hip with -DQD_STAMPS and the
-    streaming-read probes."""
+    """The diagnostic library: gqa_decode.hip and mla.hip with -DQD_STAMPS
+    and the streaming-read probes."""
     os.makedirs(LIB_DIR, exist_ok=True)
     os.makedirs(OBJ_DIR, exist_ok=True)
     objs = [os.path.join(OBJ_DIR, f"{n}_diag.o") for n in DIAG_SOURCES]
     with ThreadPoolExecutor(max_workers=len(objs)) as ex:
-        futs = [ex.submit(_run, [_hipcc(), *HIP_FLAGS, "-DQD_STAMPS", f"-I{INCLUDE}", "-c",
+        futs = [ex.submit(_run, [_hipcc(), *HIP_FLAGS, *SOURCE_FLAGS.get(n, []), "-DQD_STAMPS", f"-I{INCLUDE}", "-c",
                                  os.path.join(CSRC, f"{n}.hip"), "-o", o], verbose)
                 for n, o in zip(DIAG_SOURCES, objs)]
         for f in futs:

@@ -2596,7 +2596,7 @@ int qd_gqa_decode_auto_info(int batch, int q_heads, int kv_heads, int head_dim, 
 
 #ifdef QD_STAMPS
 // Diagnostic build only: per-wave timestamps of the stream-K kernel go to
-// `buffer` (8 words per wave, the grid's waves in order) for the launches
+// `buffer` (16 words per wave, the grid's waves in order) for the launches
 // that follow, until called again (NULL stops them).
 int qd_diag_set_stamps(void* buffer) {
   g_stamps = static_cast<uint64_t*>(buffer);

@@ -396,7 +396,35 @@ struct MlaParams {
   int64_t* gtotal;  // MFMA kernel: tiles G of the batch (merge: skips empty ranges)
   int64_t num_blocks;
   float sl2;        // scale * log2(e)
+#ifdef QD_STAMPS
+  uint64_t* stamps;  // diagnostic build: per-wave timestamps of the shared-tile kernel (mla_stamp)
+#endif
 };
+
+#ifdef QD_STAMPS
+// Diagnostic build only (-DQD_STAMPS): 16 words per wave of
+// mla_attend_shared_kernel at stamps[(block * 4 + wave) * 16]: s_memrealtime
+// (100 MHz) at entry [0], after the prologue [1], when the loop starts (first
+// tile and query landed) [2], after the last tile [3], at the end [4]; the XCD
+// id [5]; tiles of the range [6]; shader clocks (s_memtime) spent in row ends
+// [7]; s_memtime at entry [8] and after the last tile [9]; the workgroup's
+// range [10] and head group [11]; row ends [12].  Only workgroups with tiles
+// write.
+__device__ __forceinline__ void mla_stamp(const MlaParams& p, int slot, uint64_t value) {
+  if (p.stamps && (threadIdx.x & 63) == 0)
+    p.stamps[(static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 16 + slot] = value;
+}
+__device__ __forceinline__ uint64_t mla_xcc() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x;
+}
+#define QD_MLA_STAMP(slot, value) mla_stamp(p, (slot), (value))
+#define QD_MLA_STAMPS_ON 1
+#else
+#define QD_MLA_STAMP(slot, value) ((void)0)
+#define QD_MLA_STAMPS_ON 0
+#endif
 
 // Scale s of a half-precision partial block: the values are stored as o / s
 // in fp16.  s is the block's largest |o|, clamped up to the smallest normal
@@ -1804,6 +1832,10 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, q4 = lane >> 4;
+  [[maybe_unused]] const uint64_t st_entry = QD_MLA_STAMPS_ON ? __builtin_amdgcn_s_memrealtime() : 0;
+  [[maybe_unused]] const uint64_t st_clk0 = QD_MLA_STAMPS_ON ? __builtin_amdgcn_s_memtime() : 0;
+  [[maybe_unused]] uint64_t st_rowend = 0;
+  [[maybe_unused]] int st_rowends = 0;
 
   const int L = blockIdx.x;
   const int hg = (L >> 3) % p.head_groups;
@@ -1917,6 +1949,8 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   const int n = *nreal;
   __syncthreads();  // every wave has read the count before the ring is written
   if (n == 0) return;  // whole workgroup: uniform
+  QD_MLA_STAMP(0, st_entry);
+  QD_MLA_STAMP(1, __builtin_amdgcn_s_memrealtime());
 
   // --- Main loop ------------------------------------------------------------
   // DMA of tile t from its list entry e (past the end a placeholder: a
@@ -1985,6 +2019,7 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
   i32x4 e_cur = ctl[0], e_dma = ctl[kShBufs - 1];
   int r_nxt = ctl[1][3];
   wait_vm_all();
+  QD_MLA_STAMP(2, __builtin_amdgcn_s_memrealtime());
   int row = -1;
   for (int t = 0; t < n; ++t) {
     dma_ring_barrier<(kShBufs - 2) * kShDma>();  // tile t in LDS; tile t-1 done by every wave
@@ -2130,6 +2165,7 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
     });
 
     if (last) {
+      [[maybe_unused]] const uint64_t st_re0 = QD_MLA_STAMPS_ON ? __builtin_amdgcn_s_memtime() : 0;
       // This wave's heads for the row segment, then the next row's query;
       // one wait covers the stores, the query and the tiles in flight.
       const float Lt = sum_over_lane_groups(l_run);
@@ -2174,10 +2210,26 @@ __global__ __launch_bounds__(kShThreads) void mla_attend_shared_kernel(MlaParams
       }
       if (t + 1 < n) load_q(r1);
       wait_vm_all();
+      if constexpr (QD_MLA_STAMPS_ON) {
+        st_rowend += __builtin_amdgcn_s_memtime() - st_re0;
+        ++st_rowends;
+      }
     }
   }
+  QD_MLA_STAMP(3, __builtin_amdgcn_s_memrealtime());
+  QD_MLA_STAMP(9, __builtin_amdgcn_s_memtime());
   // Drain the placeholder loads before the workgroup's LDS is released.
   __builtin_amdgcn_s_waitcnt(0);
+#ifdef QD_STAMPS
+  QD_MLA_STAMP(4, __builtin_amdgcn_s_memrealtime());
+  QD_MLA_STAMP(5, mla_xcc());
+  QD_MLA_STAMP(6, static_cast<uint64_t>(n));
+  QD_MLA_STAMP(7, st_rowend);
+  QD_MLA_STAMP(8, st_clk0);
+  QD_MLA_STAMP(10, static_cast<uint64_t>(w));
+  QD_MLA_STAMP(11, static_cast<uint64_t>(hg));
+  QD_MLA_STAMP(12, static_cast<uint64_t>(st_rowends));
+#endif
 }
 
 // ----------------------------------------------------------------------------
@@ -2661,6 +2713,10 @@ PartialRefs partial_refs(const AttendShape& a, const AttendPlan& pl, void* part_
   return {static_cast<float*>(part_ws), reinterpret_cast<int64_t*>(meta), reinterpret_cast<int*>(meta + sizeof(int64_t))};
 }
 
+#ifdef QD_STAMPS
+uint64_t* g_mla_stamps = nullptr;  // diagnostic build: qd_diag_set_mla_stamps
+#endif
+
 // skip_merge: the caller merges the split rows itself (mla_decode's value
 // projection, MFMA kernels with half-precision partials only).
 int run_attend(const AttendShape& a, const void* q, const void* qr, const void* cache, const int32_t* table,
@@ -2668,6 +2724,9 @@ int run_attend(const AttendShape& a, const void* q, const void* qr, const void* 
                float scale, void* out, void* part_ws, size_t part_bytes, const AttendPlan& pl, hipStream_t st,
                bool skip_merge = false) {
   MlaParams prm{};
+#ifdef QD_STAMPS
+  prm.stamps = g_mla_stamps;
+#endif
   prm.q = q;
   prm.qr = qr;
   prm.cache = cache;
@@ -3127,5 +3186,13 @@ int qd_mla_decode(const void* q_nope, const void* q_rope, const void* cache, con
     launch_project_merge<QD_DTYPE_F16>(prm, st);
   return launch_status("mla_decode value projection");
 }
+
+#ifdef QD_STAMPS
+// Diagnostic build only: per-wave timestamps of mla_attend_shared_kernel go
+// to `buffer` (16 words per wave, 4 waves per workgroup, the grid's
+// workgroups in order) for the launches that follow, until called again
+// (NULL stops them).
+void qd_diag_set_mla_stamps(void* buffer) { g_mla_stamps = static_cast<uint64_t*>(buffer); }
+#endif
 
 }  // extern "C"

@@ -57,7 +57,8 @@ def parse():
     ap.add_argument("--cpu-repeats", type=int, default=5)
     ap.add_argument("--mode", choices=["decode", "copy", "stamps", "read"], default="decode",
                     help="copy: HBM copy of known size (counter calibration); stamps: per-wave timestamps "
-                         "of the balanced decode kernel; read: streaming-read ceiling of the decode access "
+                         "of the balanced decode kernel (with --op mla: of the MLA shared-tile attention "
+                         "kernel on --mla-config); read: streaming-read ceiling of the decode access "
                          "pattern (both from the diagnostic library)")
     ap.add_argument("--merge", choices=["auto", "fused", "unfused"], default="auto",
                     help="where split sequences are merged (C ABI path, QD_STAGE_FUSED/UNFUSED)")
@@ -240,6 +241,97 @@ def stamps_mode(args) -> None:
             if r[2] > r[0] and r[9] > r[8]:
                 clk.setdefault(int(r[6]), []).append((r[9] - r[8]) / ((r[2] - r[0]) / 100.0))
         rec["shader_mhz_by_xcd"] = {str(x): round(_pct(v_, .5), 1) for x, v_ in sorted(clk.items())}
+        print(json.dumps(rec), flush=True)
+
+
+def mla_stamps_mode(args) -> None:
+    """Per-wave s_memrealtime stamps (100 MHz) of mla_attend_shared_kernel
+    from attention_amd/lib/libqd_attention_diag.so (mla.hip built with
+    -DQD_STAMPS) on --mla-config: entry, end of the prologue (partition and
+    tile list), loop start (first tile and query landed), end of the last
+    tile, and the XCD; tiles per range and the shader clocks spent in row
+    ends.  The attention stage (qd_mla_attend: kernel + merge) is timed from
+    the same library with the stamps off (median of 5 samples), then
+    --launches launches are recorded one at a time over rotated caches; one
+    JSON line per launch, microseconds from the first wave's entry."""
+    import ctypes
+    import attention_amd
+    from attention_amd import _build, cabi
+    from attention_amd.cases import MLA_CONFIGS
+
+    L = ctypes.CDLL(_build.DIAG_LIB)
+    V, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    L.qd_diag_set_mla_stamps.argtypes = [V]
+    L.qd_mla_attend.argtypes = [V] * 9 + [ctypes.c_size_t] + [I] * 7 + [I64, I, I, I, F, I, I, V]
+    L.qd_mla_attend_workspace_bytes.restype = ctypes.c_size_t
+    L.qd_mla_attend_workspace_bytes.argtypes = [I] * 11
+    L.qd_mla_attend_info.argtypes = [I] * 11 + [ctypes.POINTER(I)] * 2
+    L.qd_error_string.restype = ctypes.c_char_p
+    cfg = MLA_CONFIGS[args.mla_config]
+    dev = torch.device("cuda:0")
+    c = {k: (v.to(dev) if v is not None else None) for k, v in cfg.make(device="cpu").items()}
+    B, H = cfg.batch, cfg.heads
+    Dn, Dc, Dr, P = cfg.nope_dim, cfg.latent_dim, cfg.rope_dim, cfg.block_size
+    dt = cabi.DTYPE[cfg.dtype]
+    table, lens, pos = c["table"], c["lens"], c["positions"]
+    s_, g_ = I(), I()
+    kind = L.qd_mla_attend_info(B, 1, H, Dc, Dr, P, table.shape[1], -1, dt, 0, 0, ctypes.byref(s_), ctypes.byref(g_))
+    if kind != 3:
+        raise SystemExit(f"{cfg.name} does not take the shared-tile kernel (kind {kind})")
+    esz = c["cache"].element_size()
+    pools = args.pools or max(2, math.ceil(768e6 / (c["cache"].numel() * esz)))
+    caches = [c["cache"]] + [c["cache"].roll(i, dims=0).contiguous() for i in range(1, pools)]
+    scale = 1.0 / math.sqrt(Dn + Dr)
+    qa = attention_amd.mla_query_absorb(c["q_nope"], c["w_uk"])
+    out = torch.empty(B, 1, H, Dc, dtype=cfg.dtype, device=dev)
+    need = L.qd_mla_attend_workspace_bytes(B, 1, H, Dc, Dr, P, table.shape[1], -1, dt, 0, 0)
+    ws = torch.empty(max(16, need), dtype=torch.uint8, device=dev)
+    grid = ((s_.value + 7) // 8) * 8 * g_.value
+    buf = torch.zeros(grid * 4 * 16, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def attend(i):
+        rc = L.qd_mla_attend(qa.data_ptr(), c["q_rope"].data_ptr(), caches[i % pools].data_ptr(), table.data_ptr(),
+                             lens.data_ptr(), pos.data_ptr(), None, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                             B, 1, H, Dc, Dr, P, table.shape[1], caches[0].shape[0], -1, 1, dt, scale, 0, 0,
+                             stream.cuda_stream)
+        if rc:
+            raise RuntimeError(L.qd_error_string(rc).decode())
+
+    L.qd_diag_set_mla_stamps(None)
+    samples = time_samples(attend, args.steps, args.warmup, stream)
+    log(f"mla stamps: {cfg.name} workgroups={s_.value} head_groups={g_.value} pools={pools}; attention stage "
+        f"(stamps off) {statistics.median(samples) * 1e3:.2f} us median of {len(samples)} samples")
+    for n in range(args.launches):
+        buf.zero_()
+        L.qd_diag_set_mla_stamps(buf.data_ptr())
+        torch.cuda.synchronize()
+        attend(n)
+        torch.cuda.synchronize()
+        L.qd_diag_set_mla_stamps(None)
+        rows = [r for r in buf.view(-1, 16).cpu().tolist() if r[0]]
+        t0 = min(r[0] for r in rows)
+        us = lambda x: (x - t0) / 100.0  # noqa: E731  (100 MHz ticks)
+        mhz = statistics.median([(r[9] - r[8]) / ((r[3] - r[0]) / 100.0) for r in rows if r[3] > r[0]])
+        loop_tile = [((r[3] - r[2]) / 100.0 - r[7] / mhz) / max(1, r[6]) for r in rows]
+        xcd = {}
+        for r in rows:
+            xcd.setdefault(int(r[5]), []).append(us(r[3]))
+
+        def pct(key, qs):
+            vals = [key(r) for r in rows]
+            return {q_: round(_pct(vals, x), 2) for q_, x in qs}
+        rec = {"launch": n, "config": cfg.name, "waves": len(rows), "shader_mhz": round(mhz, 1),
+               "prologue_end_us": pct(lambda r: us(r[1]), (("p50", .5), ("p90", .9))),
+               "loop_start_us": pct(lambda r: us(r[2]), (("p50", .5), ("p90", .9))),
+               "loop_end_us": pct(lambda r: us(r[3]), (("p10", .1), ("p50", .5), ("p90", .9), ("max", 1.0))),
+               "kernel_end_max_us": round(max(us(r[4]) for r in rows), 2),
+               "tiles_per_range": {"min": min(r[6] for r in rows), "p50": round(_pct([r[6] for r in rows], .5)),
+                                   "max": max(r[6] for r in rows)},
+               "row_end_us_per_wave": pct(lambda r: r[7] / mhz, (("p50", .5), ("max", 1.0))),
+               "loop_us_per_tile_excluding_row_ends": {"p50": round(_pct(loop_tile, .5), 3),
+                                                       "cycles": round(_pct(loop_tile, .5) * mhz)},
+               "loop_end_p50_by_xcd_us": {str(x): round(_pct(v_, .5), 2) for x, v_ in sorted(xcd.items())}}
         print(json.dumps(rec), flush=True)
 
 
@@ -728,7 +820,7 @@ def main() -> None:
         copy_mode(args)
         return
     if args.mode == "stamps":
-        stamps_mode(args)
+        (mla_stamps_mode if args.op == "mla" else stamps_mode)(args)
         return
     if args.mode == "read":
         read_mode(args)
