@@ -853,3 +853,45 @@ def test_held_results_flush_when_full(gpu, dtype):
     assert rc == 0, cabi.error_string(rc)
     torch.cuda.synchronize()
     assert torch.equal(out, out_c)
+
+
+# (q_heads, kv_heads, head_dim, dtype, waves per workgroup of the plan, lengths)
+HELD_LAYOUTS = [
+    # head_dim 64, 2 kv-heads: 2 single-kv-head waves per workgroup, several workgroups per CU
+    (16, 2, 64, torch.float16, 2, _fused_lengths(1200, 1, 300, 93)),
+    # head_dim 256: 4 waves, one per SIMD
+    (16, 4, 256, torch.bfloat16, 4, _fused_lengths(300, 1, 200, 94)),
+    # 4 kv-heads at head_dim 128: one wave per SIMD, 3 groups in flight
+    (28, 4, 128, torch.bfloat16, 4, _fused_lengths(300, 1, 400, 95)),
+    # two kv-heads per wave: a wide table (one long sequence) among short ones
+    (32, 8, 128, torch.float16, 4, [3500] + _fused_lengths(299, 1, 100, 96)),
+]
+
+
+@pytest.mark.parametrize("shape", HELD_LAYOUTS,
+                         ids=lambda s: f"{DT_NAME[s[3]]}-Hq{s[0]}-Hkv{s[1]}-D{s[2]}-B{len(s[5])}")
+def test_held_results_every_layout(gpu, shape):
+    """The held-results kernels (result rows kept in LDS until a range ends,
+    chosen when the batch has at least one sequence per two workgroups) in
+    each wave layout the plan can pair them with: the batch is large enough
+    for the hold (2 B >= W), every row matches the oracle, and the torch op
+    and the C ABI on a NaN-filled workspace give the same bits."""
+    hq, hkv, d, dtype, wg_waves, lengths = shape
+    B = len(lengths)
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=16,
+                                   dtype=dtype, seed=97, exact_pool=True), gpu)
+    q, k, v, table, lens = case
+    kind, waves, _, _ = cabi.auto_info(B, hq, hkv, d, 16, table.shape[1], cabi.DTYPE[dtype])
+    say(f"held results: {DT_NAME[dtype]} Hq{hq} Hkv{hkv} D{d} B{B} kind={kind} waves={waves}")
+    assert kind == 1 and waves % wg_waves == 0
+    assert 2 * B >= waves // wg_waves, "the batch does not take the held-results kernel"
+    ref, rows = oracle_rows(case)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    assert_close(out, ref, DT_NAME[dtype], rows, "held results")
+    ws = cabi.auto_workspace(B, hq, hkv, d, 16, table.shape[1], cabi.DTYPE[dtype], gpu, fill=0xFF)
+    out_c = torch.full_like(q, float("nan"))
+    rc = cabi.auto_launch(*case, out_c, scale=1 / math.sqrt(d), workspace=ws)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_c)
