@@ -895,3 +895,44 @@ def test_held_results_every_layout(gpu, shape):
     assert rc == 0, cabi.error_string(rc)
     torch.cuda.synchronize()
     assert torch.equal(out, out_c)
+
+
+@pytest.mark.parametrize("merge", ["unfused", "fused"])
+@pytest.mark.parametrize("shape", [(32, 8, 128, torch.bfloat16, _fused_lengths(32, 512, 4096, 98)),
+                                   (40, 8, 128, torch.float16, _fused_lengths(300, 1, 600, 99))],
+                         ids=["cfg2-like", "held-results"])
+def test_stages_separately_match_whole_call(gpu, shape, merge):
+    """qd_gqa_decode_auto_stages as the header documents it: QD_STAGE_DECODE
+    then QD_STAGE_MERGE (same arguments and workspace, same stream) give the
+    bits of one QD_STAGE_ALL call; with the fused merge the decode stage is
+    the whole call and QD_STAGE_MERGE alone changes nothing."""
+    hq, hkv, d, dtype, lengths = shape
+    B = len(lengths)
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=16,
+                                   dtype=dtype, seed=100, exact_pool=True), gpu)
+    q = case[0]
+    maxp = case[3].shape[1]
+    flag = cabi.QD_STAGE_FUSED if merge == "fused" else cabi.QD_STAGE_UNFUSED
+    say(f"stages separately: {DT_NAME[dtype]} Hq{hq} Hkv{hkv} B{B} merge={merge}")
+    ws = cabi.auto_workspace(B, hq, hkv, d, 16, maxp, cabi.DTYPE[dtype], gpu, fill=0xFF)
+
+    def run(stages, out):
+        rc = cabi.auto_launch(*case, out, scale=1 / math.sqrt(d), workspace=ws, stages=stages | flag)
+        assert rc == 0, cabi.error_string(rc)
+
+    whole = torch.full_like(q, float("nan"))
+    run(cabi.QD_STAGE_ALL, whole)
+    parts = torch.full_like(q, float("nan"))
+    run(cabi.QD_STAGE_DECODE, parts)
+    if merge == "fused":
+        torch.cuda.synchronize()
+        before = parts.clone()
+        run(cabi.QD_STAGE_MERGE, parts)
+        torch.cuda.synchronize()
+        assert torch.equal(parts, before), "QD_STAGE_MERGE alone changed a fused call's output"
+    else:
+        run(cabi.QD_STAGE_MERGE, parts)
+    torch.cuda.synchronize()
+    assert torch.equal(parts, whole)
+    ref, rows = oracle_rows(case)
+    assert_close(whole, ref, DT_NAME[dtype], rows, "whole call")
