@@ -82,9 +82,13 @@ def test_noalloc_first_call_inside_graph_capture(gpu):
 @pytest.mark.gpu
 def test_noalloc_matches_auto_entry_point(gpu):
     cfg = CONFIGS["cfg2"]
+    held = [int(x) for x in torch.randint(1, 600, (300,), generator=torch.Generator().manual_seed(4))]
     cases = [("cfg2", cfg.make(device="cpu")),
              ("small", make_decode_case(lengths=[1, 300, 0, 17, 2000], q_heads=32, kv_heads=8, head_dim=128,
-                                        block_size=16, dtype=torch.bfloat16, seed=3))]
+                                        block_size=16, dtype=torch.bfloat16, seed=3)),
+             # 300 short sequences: the plan holds result rows in LDS
+             ("held", make_decode_case(lengths=held, q_heads=40, kv_heads=8, head_dim=128, block_size=16,
+                                       dtype=torch.float16, seed=5))]
     for name, case_cpu in cases:
         q, k, v, table, lens = (x.to(gpu) for x in case_cpu)
         B, Hq, D = q.shape
