@@ -155,6 +155,12 @@ __device__ __forceinline__ int clamp_page(int32_t phys, int64_t num_blocks) {
 
 constexpr int kGenericHeads = 8;
 
+// Fewest tokens in a split of the explicit split plan (qd_gqa_decode_plan).
+#ifndef QD_PLAN_MIN_TOKENS
+#define QD_PLAN_MIN_TOKENS 32
+#endif
+constexpr int kPlanMinTokens = QD_PLAN_MIN_TOKENS;
+
 // grid: (splits * head_chunks, Hkv, B), block 64.
 // Lane layout: row = lane/16 is one of 4 token slots, col = lane%16 owns
 // elements [col*EPL, col*EPL + EPL) of head_dim.  Each row keeps its own
@@ -208,22 +214,8 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
 
   const int64_t rs = static_cast<int64_t>(p.Hkv) * D;
   const int32_t* __restrict__ trow = p.table + static_cast<int64_t>(b) * p.maxP;
-  for (int t0 = ci.tb; t0 < ci.te; t0 += 4) {
-    const int t = t0 + row;
-    const bool valid = t < ci.te;
-    const int tt = valid ? t : ci.te - 1;
-    const int page = tt / p.P;
-    const int slot = tt - page * p.P;
-    const int phys = clamp_page(trow[page], p.num_blocks);
-    const int64_t base = (static_cast<int64_t>(phys) * p.P + slot) * rs +
-                         static_cast<int64_t>(kvh) * D + e0;
-    float kf[EPL], vf[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const bool ok = FULL || (e0 + e < D);
-      kf[e] = ok ? E::to_f(kc[base + e]) : 0.f;
-      vf[e] = ok ? E::to_f(vc[base + e]) : 0.f;
-    }
+  // One 4-token step: row `row` of the wave adds its token (when valid).
+  auto token_step = [&](bool valid, const float* kf, const float* vf) {
     float s[GH];
 #pragma unroll
     for (int h = 0; h < GH; ++h) {
@@ -243,6 +235,65 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(acc[h][e], alpha, pr * vf[e]);
       m[h] = mn;
+    }
+  };
+  if constexpr (EPL <= 8) {
+    // Head_dim <= 128.  The tokens go in windows of 64 pages: lane l holds
+    // the table entry of page wb + l, so a token's page id is a lane read,
+    // not a dependent load.  Within a window two 4-token steps are in
+    // flight: the next step's K and V rows are loaded before this step's
+    // math.  A row past the window re-reads the window's last token and is
+    // masked, so every load is unconditional (the compiler's wait then
+    // covers only the step in use).
+    auto load = [&](int w_hi, int wb, int tblv, int t0, float* kf, float* vf) {
+      const int t = t0 + row;
+      const int tt = t < w_hi ? t : w_hi - 1;
+      const int page = tt / p.P;
+      const int slot = tt - page * p.P;
+      const int phys = clamp_page(__shfl(tblv, page - wb), p.num_blocks);
+      const int64_t base = (static_cast<int64_t>(phys) * p.P + slot) * rs + static_cast<int64_t>(kvh) * D + e0;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const bool ok = FULL || (e0 + e < D);
+        kf[e] = ok ? E::to_f(kc[base + e]) : 0.f;
+        vf[e] = ok ? E::to_f(vc[base + e]) : 0.f;
+      }
+    };
+    float kA[EPL], vA[EPL], kB[EPL], vB[EPL];
+    for (int w_lo = ci.tb; w_lo < ci.te;) {
+      const int wb = w_lo / p.P;
+      const int tblv = lane < p.maxP - wb ? trow[wb + lane] : 0;
+      const int64_t w_end = static_cast<int64_t>(wb + 64) * p.P;
+      const int w_hi = w_end < ci.te ? static_cast<int>(w_end) : ci.te;
+      load(w_hi, wb, tblv, w_lo, kA, vA);
+      for (int t0 = w_lo; t0 < w_hi; t0 += 8) {
+        load(w_hi, wb, tblv, t0 + 4, kB, vB);
+        token_step(t0 + row < w_hi, kA, vA);
+        load(w_hi, wb, tblv, t0 + 8, kA, vA);
+        token_step(t0 + 4 + row < w_hi, kB, vB);
+      }
+      w_lo = w_hi;
+    }
+  } else {
+    // Head_dim 256: one step at a time (a second buffer does not fit the
+    // register file).
+    for (int t0 = ci.tb; t0 < ci.te; t0 += 4) {
+      const int t = t0 + row;
+      const bool valid = t < ci.te;
+      const int tt = valid ? t : ci.te - 1;
+      const int page = tt / p.P;
+      const int slot = tt - page * p.P;
+      const int phys = clamp_page(trow[page], p.num_blocks);
+      const int64_t base = (static_cast<int64_t>(phys) * p.P + slot) * rs +
+                           static_cast<int64_t>(kvh) * D + e0;
+      float kf[EPL], vf[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const bool ok = FULL || (e0 + e < D);
+        kf[e] = ok ? E::to_f(kc[base + e]) : 0.f;
+        vf[e] = ok ? E::to_f(vc[base + e]) : 0.f;
+      }
+      token_step(valid, kf, vf);
     }
   }
 
@@ -2386,13 +2437,16 @@ int qd_gqa_decode_plan(int batch, int q_heads, int kv_heads, int head_dim, int b
   const int64_t cus = cu_count > 0 ? cu_count : 256;
   // Work items are (sequence, kv-head) pairs; each split of one item is a
   // wave.  Aim for ~8 resident waves per CU, and keep every split at least
-  // 256 tokens and at most 64 pages so that split partials stay a small
-  // fraction of the K/V bytes.
+  // kPlanMinTokens tokens and at most 64 pages, so that split partials stay
+  // a small fraction of the K/V bytes (for 32 tokens and 4 heads per
+  // kv-head: 2 KB of fp32 partials against 16-32 KB of K/V).  Short
+  // sequences get many short splits: a wave streams its split's tokens in
+  // order.
   const int64_t items = static_cast<int64_t>(batch) * kv_heads;
   const int64_t target_waves = cus * 8;
   int64_t want = items > 0 ? (target_waves + items - 1) / items : 1;
   if (want < 1) want = 1;
-  const int64_t min_pages = (256 + block_size - 1) / block_size;
+  const int64_t min_pages = (kPlanMinTokens + block_size - 1) / block_size;
   int64_t cp = (max_pages + want - 1) / want;
   if (cp < min_pages) cp = min_pages;
   if (cp > 64) cp = 64;

@@ -136,7 +136,7 @@ def test_plan_covers_capacity(name):
     assert 1 <= s <= 65535 and 1 <= c <= 64 or (s == 1 and c == max_pages)
     assert s * c >= max_pages
     if s > 1:
-        assert c * cfg.block_size >= 256 or c == max_pages
+        assert c * cfg.block_size >= 32 or c == max_pages
 
 
 def test_plan_values_for_configs():
