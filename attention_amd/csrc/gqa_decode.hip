@@ -68,7 +68,7 @@ struct DecodeParams {
   int B, Hq, Hkv, D, P, maxP, g;
   int splits;       // launched splits per (sequence, kv-head); waves W on the stream-K path
   int chunk_pages;  // 0: ceil(npages / splits) per sequence, else fixed
-  int head_chunks;  // generic kernel: ceil(g / kGenericHeads)
+  int head_chunks;  // generic kernel: ceil(g / generic_heads(g))
   int64_t num_blocks;
   float sl2;  // scale * log2(e)
   int* meta;      // stream-K path: per sequence {first workgroup, workgroups}
@@ -155,6 +155,11 @@ __device__ __forceinline__ int clamp_page(int32_t phys, int64_t num_blocks) {
 
 constexpr int kGenericHeads = 8;
 
+// Heads per wave of the generic kernel: 4 for groups of at most 4 q-heads
+// (half the query and accumulator registers, so twice the resident waves),
+// else kGenericHeads.
+__host__ __device__ constexpr int generic_heads(int g) { return g <= 4 ? 4 : kGenericHeads; }
+
 // Fewest tokens in a split of the explicit split plan (qd_gqa_decode_plan).
 #ifndef QD_PLAN_MIN_TOKENS
 #define QD_PLAN_MIN_TOKENS 32
@@ -166,11 +171,10 @@ constexpr int kPlanMinTokens = QD_PLAN_MIN_TOKENS;
 // elements [col*EPL, col*EPL + EPL) of head_dim.  Each row keeps its own
 // streaming softmax state over the tokens it visits; rows are merged at the
 // end with the log-sum-exp rule.
-template <int DT, int EPL, bool FULL>
+template <int DT, int EPL, bool FULL, int GH = kGenericHeads>
 __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
   using E = Elem<DT>;
   using S = typename E::S;
-  constexpr int GH = kGenericHeads;
   const int lane = threadIdx.x;
   const int row = lane >> 4;
   const int col = lane & 15;
@@ -1948,13 +1952,18 @@ KernelFn pick_merge_sk_dt(int dtype, int D, bool one_head) {
   return dtype == QD_DTYPE_F16 ? pick_merge_sk<QD_DTYPE_F16, 8, 1>(D) : pick_merge_sk<QD_DTYPE_BF16, 8, 1>(D);
 }
 
+template <int DT, int GH>
+KernelFn pick_generic_gh(int D) {
+  if (D <= 16) return D == 16 ? decode_generic_kernel<DT, 1, true, GH> : decode_generic_kernel<DT, 1, false, GH>;
+  if (D <= 32) return D == 32 ? decode_generic_kernel<DT, 2, true, GH> : decode_generic_kernel<DT, 2, false, GH>;
+  if (D <= 64) return D == 64 ? decode_generic_kernel<DT, 4, true, GH> : decode_generic_kernel<DT, 4, false, GH>;
+  if (D <= 128) return D == 128 ? decode_generic_kernel<DT, 8, true, GH> : decode_generic_kernel<DT, 8, false, GH>;
+  return D == 256 ? decode_generic_kernel<DT, 16, true, GH> : decode_generic_kernel<DT, 16, false, GH>;
+}
+
 template <int DT>
-KernelFn pick_generic(int D) {
-  if (D <= 16) return D == 16 ? decode_generic_kernel<DT, 1, true> : decode_generic_kernel<DT, 1, false>;
-  if (D <= 32) return D == 32 ? decode_generic_kernel<DT, 2, true> : decode_generic_kernel<DT, 2, false>;
-  if (D <= 64) return D == 64 ? decode_generic_kernel<DT, 4, true> : decode_generic_kernel<DT, 4, false>;
-  if (D <= 128) return D == 128 ? decode_generic_kernel<DT, 8, true> : decode_generic_kernel<DT, 8, false>;
-  return D == 256 ? decode_generic_kernel<DT, 16, true> : decode_generic_kernel<DT, 16, false>;
+KernelFn pick_generic(int D, int g) {
+  return generic_heads(g) == 4 ? pick_generic_gh<DT, 4>(D) : pick_generic_gh<DT, kGenericHeads>(D);
 }
 
 KernelFn pick_combine(int dtype) {
@@ -2281,7 +2290,7 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.g = q_heads / kv_heads;
   prm.splits = splits;
   prm.chunk_pages = chunk_pages;
-  prm.head_chunks = (prm.g + kGenericHeads - 1) / kGenericHeads;
+  prm.head_chunks = (prm.g + generic_heads(prm.g) - 1) / generic_heads(prm.g);
   prm.num_blocks = num_blocks;
   prm.sl2 = scale * kLog2e;
   prm.meta = nullptr;
@@ -2508,9 +2517,9 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
   } else {
     KernelFn fn;
     switch (dtype) {
-      case QD_DTYPE_F32: fn = pick_generic<QD_DTYPE_F32>(head_dim); break;
-      case QD_DTYPE_F16: fn = pick_generic<QD_DTYPE_F16>(head_dim); break;
-      default: fn = pick_generic<QD_DTYPE_BF16>(head_dim); break;
+      case QD_DTYPE_F32: fn = pick_generic<QD_DTYPE_F32>(head_dim, prm.g); break;
+      case QD_DTYPE_F16: fn = pick_generic<QD_DTYPE_F16>(head_dim, prm.g); break;
+      default: fn = pick_generic<QD_DTYPE_BF16>(head_dim, prm.g); break;
     }
     const int64_t gx = static_cast<int64_t>(splits) * prm.head_chunks;
     if (gx > 2147483647) return fail(QD_ERR_INVALID_VALUE, "splits * head chunks exceed the grid limit");
