@@ -936,3 +936,36 @@ def test_stages_separately_match_whole_call(gpu, shape, merge):
     assert torch.equal(parts, whole)
     ref, rows = oracle_rows(case)
     assert_close(whole, ref, DT_NAME[dtype], rows, "whole call")
+
+
+# (dtype, Hq, Hkv, D, P, lengths): sequences over many 64-page table windows
+# of the generic kernel, window edges inside 4-token steps, both head-chunk
+# widths (4 heads per wave for groups of at most 4, else 8).
+GENERIC_WINDOW_SHAPES = [
+    (torch.float32, 6, 2, 128, 1, [700, 1, 130, 65]),     # P=1: a window is 64 tokens
+    (torch.float32, 40, 5, 100, 3, [1000, 194, 2]),      # 8 heads per group, D not a power of two
+    (torch.bfloat16, 8, 2, 64, 7, [900, 449, 450, 451]),  # 4 heads per group, 7-token pages
+    (torch.float16, 20, 4, 256, 16, [3000, 1025, 17]),   # head_dim 256: one step at a time
+]
+
+
+@pytest.mark.parametrize("shape", GENERIC_WINDOW_SHAPES,
+                         ids=lambda s: f"{DT_NAME[s[0]]}-Hq{s[1]}-Hkv{s[2]}-D{s[3]}-P{s[4]}")
+def test_generic_kernel_table_windows(gpu, shape):
+    """The generic kernel's page-table window (64 pages in the lanes of a
+    wave) and its two steps in flight: every row matches the oracle with one
+    split (a sequence crosses many windows) and with three."""
+    dtype, hq, hkv, d, p, lengths = shape
+    say(f"generic windows {DT_NAME[dtype]} Hq{hq} Hkv{hkv} D{d} P{p} lengths {lengths}")
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
+                                   dtype=dtype, seed=101), gpu)
+    q, k, v, table, lens = case
+    ref, rows = oracle_rows(case)
+    for splits in (1, 3):
+        out = torch.full_like(q, float("nan"))
+        ws = torch.empty(max(1, q.shape[0] * hq * splits * (d + 2)), device=gpu, dtype=torch.float32)
+        rc = cabi.launch(q, k, v, table, lens, out, scale=1 / math.sqrt(d), splits=splits, chunk_pages=0,
+                         workspace=ws if splits > 1 else None, flags=cabi.QD_FLAG_FORCE_GENERIC)
+        assert rc == 0, cabi.error_string(rc)
+        torch.cuda.synchronize()
+        assert_close(out, ref, DT_NAME[dtype], rows, f"splits={splits}")
