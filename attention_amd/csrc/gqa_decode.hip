@@ -48,6 +48,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -1835,15 +1836,30 @@ bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int d
 // against 3; 4 spills).
 constexpr int kPrefetch = QD_PREFETCH;
 
-// Stream-K path limits: each wave scans all lengths, so the batch is capped;
-// a workgroup gets at least kSkMinGroups groups of the largest possible
-// batch.  Small batches are latency-bound: 4 groups per workgroup took a
-// 57-group batch from 10.7 to 6.3 us, and 2 lost that back in the merge.
+// Stream-K path limits: each wave scans all lengths, so the batch is capped.
 constexpr int kSkMaxBatch = 4096;
+// Grid of a batch below the resident workgroups, from static shapes (Gmax
+// groups of the largest possible batch, S = their K/V bytes):
+//   W = min(resident, Gmax / kSkMinGroups,
+//           max(kSkRowsShort * B, min(ceil(S / kSkWgBytes), kSkRowsLong * B))).
+// A sequence split over W/B workgroups leaves that many partial rows per head
+// for the merge (kSkRowsShort of them fold in one round trip per merge wave),
+// and a workgroup's range streams at about 45-60 GB/s until HBM saturates:
+// short batches take as many workgroups as one merge round trip allows, long
+// ones one per kSkWgBytes up to two round trips.  Measured against the
+// earlier floor of 4 groups per workgroup (graph replays, bf16, Hq32 Hkv8
+// D128 P16): B1/L128 12.7 -> 9.8 us, B16/L128 14.8 -> 11.4, B1/L1024 13.6 ->
+// 10.9, B4/L1024 14.3 -> 13.1, B1/L16384 26.2 -> 24.2, head_dim 256 B1/L2048
+// 18.6 -> 16.3; no shape measured slower; batches that fill the resident
+// grid (cfg2-cfg5) are unchanged.  A hard cap of 64 per sequence took
+// B1/L32768 from 35.6 to 51.9 us (too few workgroups to saturate HBM).
 #ifndef QD_SK_MIN_GROUPS
-#define QD_SK_MIN_GROUPS 4
+#define QD_SK_MIN_GROUPS 1
 #endif
 constexpr int64_t kSkMinGroups = QD_SK_MIN_GROUPS;
+constexpr int64_t kSkRowsShort = 64;
+constexpr int64_t kSkRowsLong = 128;
+constexpr int64_t kSkWgBytes = int64_t{256} << 10;
 // Waves launched per resident wave slot.  Above 1 the hardware dispatcher
 // hands the later waves to whichever CUs finish first.
 #ifndef QD_SK_OVERSUB
@@ -2188,9 +2204,13 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     const int64_t gmax = static_cast<int64_t>(batch) *
                          ((static_cast<int64_t>(max_pages) * block_size + 15) / 16);
     const int64_t by_work = (gmax + kSkMinGroups - 1) / kSkMinGroups;
+    const int64_t group_bytes = int64_t{16} * kv_heads * head_dim * 2 * (dtype == QD_DTYPE_F32 ? 4 : 2);
+    const int64_t by_bytes = (gmax * group_bytes + kSkWgBytes - 1) / kSkWgBytes;
+    const int64_t by_rows = std::max(kSkRowsShort * batch, std::min(by_bytes, kSkRowsLong * batch));
     auto grid = [&](int res) {
       int64_t w = static_cast<int64_t>(res) * kSkOversubscribe;
       if (w > by_work) w = by_work;
+      if (w > by_rows) w = by_rows;
       return w < 1 ? int64_t{1} : w;
     };
     int64_t w = grid(resident);

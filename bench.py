@@ -121,6 +121,38 @@ def time_samples(fn, steps: int, warmup: int, stream, samples: int = SAMPLES) ->
     return out
 
 
+def graph_replay_us(enqueue, stream, calls: int = 10, reps: int = 10) -> float:
+    """GPU time per call without host overhead: `calls` calls of `enqueue`
+    (which must allocate nothing and enqueue no memset) captured in one HIP
+    graph, replayed `reps` times per sample between HIP events; median of
+    SAMPLES samples, microseconds per call."""
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            enqueue()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            enqueue()
+    graph.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(SAMPLES):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        out.append(start.elapsed_time(end) / (reps * calls) * 1e3)
+    del graph
+    return statistics.median(out)
+
+
 def copy_mode(args) -> None:
     n = 1 << 30  # bytes per copy
     src = torch.empty(n, dtype=torch.uint8, device="cuda").random_()
@@ -622,8 +654,11 @@ def sweep_mode(args) -> None:
     bf16, B in {1, 4, 16}, L in {128, 1024, 4096}; 20 warmup calls, then 5
     samples of 10 calls (HIP events, output allocation included), median
     us per call.  The inputs are not rotated, as in the reference, so the
-    smaller points are served partly from the Infinity Cache.  One JSON line
-    per point, then a summary line."""
+    smaller points are served partly from the Infinity Cache.  Each point also
+    reports `gpu_us`: the same call through the C entry point on a
+    preallocated workspace, 10 calls captured in a HIP graph and replayed
+    (graph_replay_us), which leaves out the host's per-call cost.  One JSON
+    line per point, then a summary line."""
     import attention_amd
     from attention_amd import cabi
     from attention_amd.cases import algorithmic_bytes, make_decode_case
@@ -636,22 +671,35 @@ def sweep_mode(args) -> None:
             for length in (128, 1024, 4096):
                 inputs = make_decode_case(lengths=[length] * batch, q_heads=32, kv_heads=8, head_dim=128,
                                           block_size=16, dtype=dtype, device=dev)
-                kind = cabi.auto_info(batch, 32, 8, 128, 16, inputs[3].shape[1], cabi.DTYPE[dtype])[0]
+                maxp = inputs[3].shape[1]
+                kind, waves, _, _ = cabi.auto_info(batch, 32, 8, 128, 16, maxp, cabi.DTYPE[dtype])
                 samples = time_samples(lambda i: attention_amd.gqa_decode(*inputs), 10, 20, stream)
                 med = statistics.median(samples)
+                ws = cabi.auto_workspace(batch, 32, 8, 128, 16, maxp, cabi.DTYPE[dtype], dev)
+                out = torch.empty_like(inputs[0])
+
+                def enqueue():
+                    rc = cabi.auto_launch(*inputs, out, scale=1 / math.sqrt(128), workspace=ws,
+                                          stream=torch.cuda.current_stream(dev).cuda_stream)
+                    if rc != 0:
+                        raise RuntimeError(cabi.error_string(rc))
+
+                gpu_us = graph_replay_us(enqueue, stream)
                 nbytes = algorithmic_bytes([length] * batch, batch, 32, 8, 128, 16, inputs[0].element_size())
                 row = {"dtype": DT_NAME[dtype], "batch": batch, "length": length, "hq": 32, "hkv": 8,
                        "head_dim": 128, "block_size": 16, "median_us": round(med * 1e3, 3),
                        "min_us": round(min(samples) * 1e3, 3), "max_us": round(max(samples) * 1e3, 3),
+                       "gpu_us": round(gpu_us, 3), "waves": waves,
                        "gb_s": round(nbytes / (med * 1e-3) / 1e9, 1),
                        "path": {1: "balanced MFMA + merge", 2: "balanced MFMA, fused merge",
                                 0: "split layout"}.get(kind, "?")}
                 rows.append(row)
                 print(json.dumps(row), flush=True)
-                del inputs
+                del inputs, ws, out
     print(json.dumps({"op": "sweep", "points": len(rows),
                       "method": "20 warmup, 5 samples x 10 calls, median (measure_decode.py:47-57)",
-                      "median_us": {f"{r['dtype']}/B{r['batch']}/L{r['length']}": r["median_us"] for r in rows}}),
+                      "median_us": {f"{r['dtype']}/B{r['batch']}/L{r['length']}": r["median_us"] for r in rows},
+                      "gpu_us": {f"{r['dtype']}/B{r['batch']}/L{r['length']}": r["gpu_us"] for r in rows}}),
           flush=True)
 
 
