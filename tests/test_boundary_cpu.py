@@ -171,6 +171,32 @@ def test_auto_wave_shape_by_capacity():
     assert cabi.auto_info(8, 64, 8, 256, 16, 8192, bf16)[1] == 256 * 4  # D 256: 4 waves, one each
 
 
+@pytest.mark.skipif(torch.cuda.is_available(),
+                    reason="wave counts assume the CPU-only occupancy fallback (256 CUs, one workgroup each)")
+def test_auto_grid_below_resident():
+    """Batches too small to fill the resident grid R: W = min(R, Gmax,
+    max(64 B, min(ceil(S / 256 KiB), 128 B))) workgroups, Gmax the 16-token
+    groups of the largest batch the shapes allow and S their K/V bytes (64 KiB
+    per group at Hkv8/D128 in 16 bits).  At least one group per workgroup, a
+    split sequence's partial rows within one merge round trip (64 per head)
+    unless the bytes need more workgroups, and at most 128 per sequence.
+    8 waves per workgroup here (one kv-head each), 2 for cfg1's 2 kv-heads."""
+    bf16, f16 = cabi.DTYPE[torch.bfloat16], cabi.DTYPE[torch.float16]
+    cases = [
+        ((1, 32, 8, 128, 16, 8), 8),        # B1/L128: one group per workgroup (Gmax = 8)
+        ((16, 32, 8, 128, 16, 8), 128),     # B16/L128: Gmax = 128
+        ((1, 32, 8, 128, 16, 64), 64),      # B1/L1024: Gmax = 64 = 64 B
+        ((1, 32, 8, 128, 16, 256), 64),     # B1/L4096: 64 B (S = 16 MiB is 64 x 256 KiB)
+        ((1, 32, 8, 128, 16, 512), 128),    # B1/L8192: S / 256 KiB = 128
+        ((1, 32, 8, 128, 16, 2048), 128),   # B1/L32768: capped at 128 B
+        ((2, 32, 8, 128, 16, 256), 128),    # B2/L4096: 64 B = S / 256 KiB = 128
+        ((4, 32, 8, 128, 16, 64), 256),     # B4/L1024: 64 B = 256 = R
+    ]
+    for shape, wgs in cases:
+        assert cabi.auto_info(*shape, bf16)[:2] == (1, 8 * wgs), shape
+    assert cabi.auto_info(4, 8, 2, 64, 16, 32, f16)[:2] == (1, 2 * 128)  # cfg1: Gmax = 128
+
+
 def test_auto_plan_uses_the_merge_kernel():
     """The automatic plan merges split sequences with the separate merge
     kernel (kind 1) for every benchmark shape; the fused merge is a
