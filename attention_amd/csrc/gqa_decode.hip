@@ -20,7 +20,9 @@
 //                          (fp32, any head_dim in [1,256], any block_size,
 //                          any group size) on the VALU: 16 lanes per token
 //                          row, DPP row reductions.
-//   combine_kernel         log-sum-exp merge of [B,Hq,S,D+2] partials.
+//   combine_rows_kernel    log-sum-exp merge of [B,Hq,S,D+2] partials (head_dim
+//                          64/128/256, four lane groups per head);
+//   combine_kernel         the same for any head_dim or alignment.
 //
 // MFMA pipeline (one wave): each 16-token group is S^T = K.Q^T with
 // v_mfma_f32_16x16x32 (K rows feed the A operand straight from 16-byte
@@ -166,6 +168,8 @@ __host__ __device__ constexpr int generic_heads(int g) { return g <= 4 ? 4 : kGe
 #define QD_PLAN_MIN_TOKENS 32
 #endif
 constexpr int kPlanMinTokens = QD_PLAN_MIN_TOKENS;
+// Waves per CU the explicit split plan aims for (splits x (sequence, kv-head)).
+constexpr int64_t kPlanWavesPerCu = 4;
 
 // grid: (splits * head_chunks, Hkv, B), block 64.
 // Lane layout: row = lane/16 is one of 4 token slots, col = lane%16 owns
@@ -1064,7 +1068,7 @@ struct ValuWave : MfmaWave<D, DT, PF, 1> {
 // (sequence, kv-head, split)).  Split z of a sequence covers whole pages
 // (chunk_info); a sequence with a single non-empty split is written
 // directly, otherwise every non-empty split writes its partial to
-// ws[b, h, z, :] for combine_kernel.
+// ws[b, h, z, :] for the split merge (combine_rows_kernel / combine_kernel).
 template <int D, int DT, int PF>
 __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p) {
   const int z = blockIdx.x;
@@ -1186,22 +1190,31 @@ struct MergeRows {
     }
   }
 
-  // Writes head j4's output row at out (when the head exists).
+  // Writes head j4's output row at out (when the head exists); out is
+  // 16-byte aligned (8-byte for 16-bit rows of D = 64).
   template <int DT>
   __device__ void store(bool active, typename Elem<DT>::S* out) const {
     if (!active) return;
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    uint32_t wv[EPL / 2];
+    if constexpr (DT == QD_DTYPE_F32) {
+      float* dst = out + c16 * EPL;
 #pragma unroll
-    for (int e = 0; e < EPL; e += 2)
-      wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
-    char* dst = reinterpret_cast<char*>(out + c16 * EPL);
-    if constexpr (EPL == 4) {
-      *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
+      for (int e = 0; e < EPL; e += 4)
+        *reinterpret_cast<f32x4*>(dst + e) = f32x4{L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f,
+                                                   L > 0.f ? acc[e + 2] * inv : 0.f, L > 0.f ? acc[e + 3] * inv : 0.f};
     } else {
+      uint32_t wv[EPL / 2];
 #pragma unroll
-      for (int t = 0; t < EPL / 8; ++t)
-        *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+      for (int e = 0; e < EPL; e += 2)
+        wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
+      char* dst = reinterpret_cast<char*>(out + c16 * EPL);
+      if constexpr (EPL == 4) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
+      } else {
+#pragma unroll
+        for (int t = 0; t < EPL / 8; ++t)
+          *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+      }
     }
   }
 };
@@ -1775,6 +1788,33 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeParams p) {
   merge_rows<DT>(base, D + 2, ci.nch, D, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
 }
 
+// Same merge for head_dim D in {64, 128, 256}, a 16-byte aligned output and
+// an 8-byte aligned workspace: grid (Hq, B), one wave per head.  Lane group
+// j4 folds the partials z = j4, j4 + 4, ... in order (combine_rows<D>()
+// of them per memory round trip each, so 4x that many per wave, against
+// merge_rows' kCombineBatch), then the four group states are combined
+// (SoftmaxState::merge) and group 0 stores the row.
+template <int D>
+constexpr int combine_rows() {
+  return D <= 128 ? 16 : 8;
+}
+
+template <int D, int DT>
+__global__ __launch_bounds__(64) void combine_rows_kernel(DecodeParams p) {
+  using S = typename Elem<DT>::S;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const ChunkInfo ci = chunk_info(p, p.lens[b], 0);
+  if (ci.nch <= 1) return;  // written directly by the decode kernel
+  const int j4 = (threadIdx.x & 63) >> 4;
+  const float* base = p.ws + (static_cast<int64_t>(b) * p.Hq + h) * p.splits * (D + 2);
+  const int nrows = ci.nch > j4 ? (ci.nch - j4 + 3) / 4 : 0;
+  MergeRows<D, combine_rows<D>()> mr;
+  mr.fold_rows(base + static_cast<int64_t>(j4) * (D + 2), 4 * (D + 2), nrows);
+  mr.combine_groups();
+  mr.template store<DT>(j4 == 0, static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D);
+}
+
 // ----------------------------------------------------------------------------
 // Host side
 // ----------------------------------------------------------------------------
@@ -1982,15 +2022,29 @@ KernelFn pick_generic(int D, int g) {
   return generic_heads(g) == 4 ? pick_generic_gh<DT, 4>(D) : pick_generic_gh<DT, kGenericHeads>(D);
 }
 
-KernelFn pick_combine(int dtype) {
-  switch (dtype) {
-    case QD_DTYPE_F32: return combine_kernel<QD_DTYPE_F32>;
-    case QD_DTYPE_F16: return combine_kernel<QD_DTYPE_F16>;
-    default: return combine_kernel<QD_DTYPE_BF16>;
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+template <int DT>
+KernelFn pick_combine_rows(int D) {
+  switch (D) {
+    case 64: return combine_rows_kernel<64, DT>;
+    case 128: return combine_rows_kernel<128, DT>;
+    default: return combine_rows_kernel<256, DT>;
   }
 }
 
-bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+// The split layout's merge: combine_rows_kernel where its vector loads and
+// stores apply (head_dim 64/128/256, 16-byte aligned output, 8-byte aligned
+// workspace), else combine_kernel (any head_dim, element stores).
+KernelFn pick_combine(int dtype, int head_dim, const void* out, const float* ws) {
+  const bool rows = (head_dim == 64 || head_dim == 128 || head_dim == 256) && aligned16(out) &&
+                    (reinterpret_cast<uintptr_t>(ws) & 7u) == 0;
+  switch (dtype) {
+    case QD_DTYPE_F32: return rows ? pick_combine_rows<QD_DTYPE_F32>(head_dim) : combine_kernel<QD_DTYPE_F32>;
+    case QD_DTYPE_F16: return rows ? pick_combine_rows<QD_DTYPE_F16>(head_dim) : combine_kernel<QD_DTYPE_F16>;
+    default: return rows ? pick_combine_rows<QD_DTYPE_BF16>(head_dim) : combine_kernel<QD_DTYPE_BF16>;
+  }
+}
 
 // Resident workgroups of `fn` (block of `threads`) on the current device:
 // CUs x blocks per CU from the HIP occupancy calculator; cached per
@@ -2465,14 +2519,17 @@ int qd_gqa_decode_plan(int batch, int q_heads, int kv_heads, int head_dim, int b
     return fail(QD_ERR_INVALID_VALUE, "invalid shapes for plan");
   const int64_t cus = cu_count > 0 ? cu_count : 256;
   // Work items are (sequence, kv-head) pairs; each split of one item is a
-  // wave.  Aim for ~8 resident waves per CU, and keep every split at least
-  // kPlanMinTokens tokens and at most 64 pages, so that split partials stay
-  // a small fraction of the K/V bytes (for 32 tokens and 4 heads per
+  // wave.  Aim for ~kPlanWavesPerCu waves per CU, and keep every split at
+  // least kPlanMinTokens tokens and at most 64 pages, so that split partials
+  // stay a small fraction of the K/V bytes (for 32 tokens and 4 heads per
   // kv-head: 2 KB of fp32 partials against 16-32 KB of K/V).  Short
   // sequences get many short splits: a wave streams its split's tokens in
-  // order.
+  // order.  Measured on the fp32 sweep shapes (Hq32 Hkv8 D128, every split
+  // count from 8 to 512): the fastest split count gave about 4 waves per CU
+  // at B1/L16384 (S128), B4/L4096 (S32), B16/L1024 and B16/L4096 (S8), where
+  // 8 per CU took 10-27% longer (more split starts, and rows for the merge).
   const int64_t items = static_cast<int64_t>(batch) * kv_heads;
-  const int64_t target_waves = cus * 8;
+  const int64_t target_waves = cus * kPlanWavesPerCu;
   int64_t want = items > 0 ? (target_waves + items - 1) / items : 1;
   if (want < 1) want = 1;
   const int64_t min_pages = (kPlanMinTokens + block_size - 1) / block_size;
@@ -2527,8 +2584,12 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
                                  q_heads, kv_heads, head_dim, block_size, max_pages, num_blocks, scale,
                                  splits, chunk_pages);
   hipStream_t stm = static_cast<hipStream_t>(stream);
+  // The MFMA kernel's vector loads and stores need 16-byte aligned tensors
+  // and an 8-byte aligned workspace (its partials are stored in float pairs);
+  // the generic kernel stores single elements.
   const bool use_mfma = qd_gqa_decode_kernel_kind(q_heads, kv_heads, head_dim, block_size, dtype, flags) &&
-                        aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out);
+                        aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out) &&
+                        (splits <= 1 || (reinterpret_cast<uintptr_t>(workspace) & 7u) == 0);
   (void)hipGetLastError();  // start from a clean error state
   if (use_mfma) {
     const KernelFn fn = dtype == QD_DTYPE_F16 ? pick_mfma<QD_DTYPE_F16>(head_dim)
@@ -2546,7 +2607,7 @@ int qd_gqa_decode_launch(const void* q, const void* k_cache, const void* v_cache
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(gx), kv_heads, batch), dim3(64), 0, stm, prm);
   }
   if (splits > 1) {
-    hipLaunchKernelGGL(pick_combine(dtype), dim3(q_heads, batch), dim3(64), 0, stm, prm);
+    hipLaunchKernelGGL(pick_combine(dtype, head_dim, out, workspace), dim3(q_heads, batch), dim3(64), 0, stm, prm);
   }
   return launch_error();
 }

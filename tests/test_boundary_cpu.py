@@ -140,8 +140,12 @@ def test_plan_covers_capacity(name):
 
 
 def test_plan_values_for_configs():
-    # cfg2: 256 (seq, kv-head) items, 256-page tables -> 8 splits of 32 pages.
-    assert cabi.plan(32, 32, 8, 128, 16, 256) == (8, 32)
+    # cfg2: 256 (seq, kv-head) items for ~4 waves per CU on 256 CUs, 256-page
+    # tables -> 4 splits of 64 pages.
+    assert cabi.plan(32, 32, 8, 128, 16, 256) == (4, 64)
+    # One sequence: 8 items -> 128 splits of 2 pages (32 tokens at least).
+    assert cabi.plan(1, 32, 8, 128, 16, 256) == (128, 2)
+    assert cabi.plan(1, 32, 8, 128, 16, 1024) == (128, 8)
     # cfg4: 64 items, 8192-page tables -> 64-page splits.
     assert cabi.plan(8, 64, 8, 128, 16, 8192) == (128, 64)
     # cfg5: 2048 items already fill the GPU -> one pass.

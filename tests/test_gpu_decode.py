@@ -157,6 +157,35 @@ def test_shapes_cabi(gpu, shape, flags):
 # Split API, workspace contents
 # ----------------------------------------------------------------------------
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_split_merge_alignments(gpu, dtype):
+    """The split layout's merge with a 16-byte aligned output and 8-byte
+    aligned workspace (combine_rows_kernel: four lane groups per head, 16
+    partials per round trip each) and with the output or the workspace one
+    element off that alignment (combine_kernel): every form matches the
+    oracle, with 1 to 300 partials per head (several round trips per lane
+    group at 300)."""
+    hq, hkv, d, p = 32, 8, 128, 16
+    lengths = [1, 16, 17, 1000, 4800, 0]
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
+                                   dtype=dtype, seed=29), gpu)
+    q, k, v, table, lens = case
+    ref, rows = oracle_rows(case)
+    B, maxp = len(lengths), table.shape[1]
+    for splits, chunk in [(maxp, 1), (7, 0), (65, 0)]:
+        n = B * hq * splits * (d + 2)
+        for out_off, ws_off in [(0, 0), (1, 0), (0, 1)]:
+            say(f"split merge {DT_NAME[dtype]} splits={splits} chunk={chunk} out+{out_off} ws+{ws_off}")
+            obuf = torch.full((q.numel() + 8,), float("nan"), dtype=dtype, device=gpu)
+            out = obuf[out_off:out_off + q.numel()].view(q.shape)
+            ws = torch.full((n + 4,), float("nan"), dtype=torch.float32, device=gpu)[ws_off:ws_off + n]
+            rc = cabi.launch(q, k, v, table, lens, out, scale=1 / math.sqrt(d), splits=splits, chunk_pages=chunk,
+                             workspace=ws)
+            assert rc == 0, cabi.error_string(rc)
+            torch.cuda.synchronize()
+            assert_close(out, ref, DT_NAME[dtype], rows, f"splits={splits} out+{out_off} ws+{ws_off}")
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 4, 8, 16, 64])
 def test_split_api(gpu, splits):
     say(f"gqa_decode_split splits={splits}")
