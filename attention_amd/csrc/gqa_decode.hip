@@ -1890,8 +1890,9 @@ constexpr int kSkMaxBatch = 4096;
 // earlier floor of 4 groups per workgroup (graph replays, bf16, Hq32 Hkv8
 // D128 P16): B1/L128 12.7 -> 9.8 us, B16/L128 14.8 -> 11.4, B1/L1024 13.6 ->
 // 10.9, B4/L1024 14.3 -> 13.1, B1/L16384 26.2 -> 24.2, head_dim 256 B1/L2048
-// 18.6 -> 16.3; no shape measured slower; batches that fill the resident
-// grid (cfg2-cfg5) are unchanged.  A hard cap of 64 per sequence took
+// 18.6 -> 16.3; of 34 shapes one slower (B100/L128, 16.9 -> 17.8 us: its old
+// grid of 200 took the held-results kernel, 256 does not); batches that fill
+// the resident grid (cfg2-cfg5) are unchanged.  A hard cap of 64 per sequence took
 // B1/L32768 from 35.6 to 51.9 us (too few workgroups to saturate HBM).
 #ifndef QD_SK_MIN_GROUPS
 #define QD_SK_MIN_GROUPS 1
