@@ -68,10 +68,11 @@ def parse():
                     help="--mode read: sets of waves taking alternate groups (2: twice the waves per CU)")
     ap.add_argument("--probe-work", type=int, default=0,
                     help="--mode read: dependent multiply-adds per group standing in for the decode math")
-    ap.add_argument("--op", choices=["decode", "kv_append", "mla", "sweep"], default="decode",
+    ap.add_argument("--op", choices=["decode", "kv_append", "mla", "sweep", "splits"], default="decode",
                     help="kv_append: time the paged cache append on the config's shapes instead; "
                          "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config; "
-                         "sweep: the reference's decode sweep (benchmarks/measure_decode.py:43-57)")
+                         "sweep: the reference's decode sweep (benchmarks/measure_decode.py:43-57); "
+                         "splits: the split layout by split count on the sweep's fp32 shapes")
     ap.add_argument("--mla-config", default="mla-h128")
     ap.add_argument("--mla-kernel", choices=["auto", "wave", "staged"], default="auto",
                     help="--op mla: attention kernel of the timed attention stage (comparison)")
@@ -703,6 +704,47 @@ def sweep_mode(args) -> None:
           flush=True)
 
 
+def splits_mode(args) -> None:
+    """The split layout (decode_generic_kernel + the split merge) by split
+    count, on fp32 shapes of the reference's sweep (Hq32/Hkv8/D128/P16,
+    make_decode_case seed 42) and a longer one: GPU time per call from graph
+    replays of the C entry point (graph_replay_us) for split counts 8..512
+    (whole pages per split), with the plan's choice (qd_gqa_decode_plan)
+    marked.  One JSON line per shape."""
+    from attention_amd import cabi
+    from attention_amd.cases import make_decode_case
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    f32 = cabi.DTYPE[torch.float32]
+    for batch, length in ((1, 1024), (1, 4096), (4, 1024), (4, 4096), (16, 1024), (16, 4096), (1, 16384)):
+        inputs = make_decode_case(lengths=[length] * batch, q_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                                  dtype=torch.float32, device=dev)
+        maxp = inputs[3].shape[1]
+        plan_s, plan_c = cabi.plan(batch, 32, 8, 128, 16, maxp, f32)
+        out = torch.empty_like(inputs[0])
+        times = {}
+        for want in sorted({plan_s, 8, 16, 32, 64, 128, 256, 512}):
+            if want > maxp:
+                continue
+            chunk = plan_c if want == plan_s else -(-maxp // want)
+            splits = -(-maxp // chunk)
+            ws = torch.empty(batch * 32 * splits * 130, dtype=torch.float32, device=dev)
+
+            def enqueue():
+                rc = cabi.launch(*inputs, out, scale=1 / math.sqrt(128), splits=splits, chunk_pages=chunk,
+                                 workspace=ws, stream=torch.cuda.current_stream(dev).cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(cabi.error_string(rc))
+
+            times[f"S{splits}x{chunk}p"] = round(graph_replay_us(enqueue, stream), 3)
+            del ws
+        best = min(times, key=times.get)
+        print(json.dumps({"dtype": "fp32", "batch": batch, "length": length, "plan": f"S{plan_s}x{plan_c}p",
+                          "gpu_us": times, "fastest": best}), flush=True)
+        del inputs, out
+
+
 PEAK_MFMA_BF16_TFLOPS = 2500.0
 
 
@@ -881,6 +923,9 @@ def main() -> None:
         return
     if args.op == "sweep":
         sweep_mode(args)
+        return
+    if args.op == "splits":
+        splits_mode(args)
         return
 
     import attention_amd
