@@ -78,6 +78,12 @@ struct DecodeParams {
   int wg_waves;   // stream-K path: waves per workgroup
   uint32_t* ctr;  // fused stream-K path: arrival counter per (sequence, kv-head), zero between calls
   int stage_bytes;  // stream-K path: LDS bytes per wave for result rows held until the range ends
+  // Stream-K path, groups of more than kMfmaHeads q-heads: each kv-head is
+  // served as kv_split virtual kv-heads of g = (Hq/kv_rows)/kv_split q-heads
+  // (Hkv = kv_rows * kv_split); virtual kv-head v reads K/V column v /
+  // kv_split of token rows of kv_rows kv-heads.  Otherwise 1 and Hkv.
+  int kv_split;
+  int kv_rows;
 #ifdef QD_STAMPS
   uint64_t* stamps;  // diagnostic build: per-wave timestamps (stamp_wave)
 #endif
@@ -491,8 +497,10 @@ struct MfmaWave {
 #pragma unroll
       for (int d = 0; d < DV; ++d) acc[j][d] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh0) * D * 2;
-    vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh0) * D * 2;
+    // Virtual kv-heads (kv_split > 1) come with one kv-head per wave (NKV 1).
+    const int64_t col = p.kv_split > 1 ? kvh0 / p.kv_split : kvh0;
+    kbase = static_cast<const char*>(p.k) + col * D * 2;
+    vbase = static_cast<const char*>(p.v) + col * D * 2;
     len = valid_tokens;
   }
 
@@ -506,7 +514,7 @@ struct MfmaWave {
     const int pl = gi / gpp;               // page index within the item
     const int row0 = 16 * (gi - pl * gpp);  // first row inside the page
     const int phys = clamp_page(__builtin_amdgcn_readlane(tblv, pl - wbase), p.num_blocks);
-    const int64_t row_bytes = static_cast<int64_t>(p.Hkv) * D * 2;
+    const int64_t row_bytes = static_cast<int64_t>(p.kv_rows) * D * 2;
     const int64_t off = (static_cast<int64_t>(phys) * p.P + row0) * row_bytes;
     const char* kp = kbase + off;
     const char* vp = vbase + off;
@@ -903,8 +911,9 @@ struct ValuWave : MfmaWave<D, DT, PF, 1> {
 #pragma unroll
       for (int e = 0; e < 8; ++e) vacc[h][e] = 0.f;
     }
-    this->kbase = static_cast<const char*>(p.k) + static_cast<int64_t>(kvh) * D * 2;
-    this->vbase = static_cast<const char*>(p.v) + static_cast<int64_t>(kvh) * D * 2;
+    const int64_t col = p.kv_split > 1 ? kvh / p.kv_split : kvh;
+    this->kbase = static_cast<const char*>(p.k) + col * D * 2;
+    this->vbase = static_cast<const char*>(p.v) + col * D * 2;
     this->len = valid_tokens;
   }
 
@@ -2210,7 +2219,23 @@ struct AutoPlan {
   int chunk_pages;
   size_t ws_bytes;  // scratch bytes (kCounterBytes of counters first)
   size_t meta_offset;  // stream-K: byte offset of the meta table in the scratch
+  int kv_split;     // stream-K: virtual kv-heads per kv-head (DecodeParams::kv_split)
 };
+
+// Virtual kv-heads per kv-head for the stream-K path: 1 for groups of at
+// most kMfmaHeads q-heads, else the fewest equal chunks of at most
+// kMfmaHeads q-heads (a group of 48 is 3 x 16, of 40 is 4 x 10), at most
+// kMaxWgWaves of them so that one kv-head's chunks are waves of one
+// workgroup, reading the same K/V rows in the same steps; 0 when no such
+// split exists (groups above 128, or a prime such as 71).
+int kv_split_for(int q_heads, int kv_heads) {
+  if (kv_heads <= 0 || q_heads % kv_heads != 0) return 0;
+  const int g = q_heads / kv_heads;
+  if (g <= kMfmaHeads) return 1;
+  for (int c = 2; c <= kMaxWgWaves; ++c)
+    if (g % c == 0 && g / c <= kMfmaHeads) return c;
+  return 0;
+}
 
 // Shapes the fused merge can address: one counter per (sequence, kv-head)
 // in the counter area, and 32-bit buffer offsets over a sequence's slots.
@@ -2240,17 +2265,26 @@ bool fused_applies(int batch, int q_heads, int kv_heads, int head_dim, int nkv, 
 // whether q/k/v/out are 16-byte aligned (the MFMA kernels' vector loads).
 int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages,
               int dtype, bool aligned, AutoPlan* ap, bool valu = false) {
-  *ap = AutoPlan{false, 0, 1, 1, false, false, 0, 0, 1, 0, kCounterBytes, 0};
+  *ap = AutoPlan{false, 0, 1, 1, false, false, 0, 0, 1, 0, kCounterBytes, 0, 1};
   if (batch <= 0) return QD_OK;
-  if (aligned && mfma_applies(q_heads, kv_heads, head_dim, block_size, dtype) &&
+  const int split = kv_split_for(q_heads, kv_heads);
+  const int vkv = kv_heads * (split > 0 ? split : 1);  // kv-heads as the stream-K kernel serves them
+  if (aligned && split > 0 && (split == 1 || !valu) && mfma_applies(q_heads, vkv, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
     int nkv = 1;
-    const bool wide = !valu && sk_wide_applies(kv_heads, head_dim);
-    int nw = sk_wg_waves(kv_heads, nkv, head_dim, valu, wide);
-    const int g = q_heads / kv_heads;
+    const bool wide = !valu && sk_wide_applies(vkv, head_dim);
+    int nw = sk_wg_waves(vkv, nkv, head_dim, valu, wide);
+    // The chunks of one kv-head in one pass of the workgroup's waves.
+    for (int n = nw; split > 1 && n >= split; --n) {
+      if (vkv % n == 0 && n % split == 0) {
+        nw = n;
+        break;
+      }
+    }
+    const int g = q_heads / vkv;
     KernelFn fn = valu ? pick_valu_sk_dt(dtype, g) : pick_mfma_sk_dt(dtype, head_dim, nkv, wide);
     int resident = resident_blocks(fn, 64 * nw);
-    if (!valu && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
+    if (!valu && split == 1 && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
       nkv = 2;
       nw = sk_wg_waves(kv_heads, nkv, head_dim);
       fn = pick_mfma_sk_dt(dtype, head_dim, nkv);
@@ -2285,13 +2319,14 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
       if (prod.stream_k && w > prod.wgs) w = prod.wgs;
     }
     ap->stream_k = true;
+    ap->kv_split = split;
     ap->wgs = static_cast<int>(w);
     ap->wg_waves = nw;
     ap->kv_per_wave = nkv;
     ap->wide = wide && nkv == 1;
-    ap->stash_bytes = fused_stash_bytes(kv_heads, head_dim, nkv, nw);
+    ap->stash_bytes = fused_stash_bytes(vkv, head_dim, nkv, nw);
     const KernelFn ffn = pick_mfma_sk_dt(dtype, head_dim, nkv, ap->wide, true);
-    if (kFusedByDefault && !valu && fused_applies(batch, q_heads, kv_heads, head_dim, nkv, w) &&
+    if (kFusedByDefault && !valu && fused_applies(batch, q_heads, vkv, head_dim, nkv, w) &&
         ap->stash_bytes <= kFusedMaxStash && allow_dyn_lds(ffn)) {
       // The fused kernel's own occupancy (registers and the stash) bounds
       // the grid; without waits between workgroups a larger grid would
@@ -2299,7 +2334,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
       const int64_t rf = resident_blocks(ffn, 64 * nw, ap->stash_bytes) * kSkOversubscribe;
       if (w > rf) w = rf;
       ap->wgs = static_cast<int>(w);
-      ap->fused = fused_fits(batch, q_heads, kv_heads, head_dim, w);
+      ap->fused = fused_fits(batch, q_heads, vkv, head_dim, w);
     }
     ap->meta_offset = kCounterBytes + static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
     ap->ws_bytes = ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
@@ -2372,6 +2407,8 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.wg_waves = 1;
   prm.ctr = nullptr;
   prm.stage_bytes = 0;
+  prm.kv_split = 1;
+  prm.kv_rows = kv_heads;
 #ifdef QD_STAMPS
   prm.stamps = g_stamps;
 #endif
@@ -2659,7 +2696,7 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   bool fused = ap.fused;
   if (unfused) fused = false;
   if (force_fused) {
-    if (valu || !fused_fits(batch, q_heads, kv_heads, head_dim, ap.wgs) || ap.stash_bytes > kFusedMaxStash ||
+    if (valu || !fused_fits(batch, q_heads, kv_heads * ap.kv_split, head_dim, ap.wgs) || ap.stash_bytes > kFusedMaxStash ||
         !allow_dyn_lds(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, true)))
       return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_FUSED needs MFMA math, batch * kv_heads <= 65536 and "
                                         "partial slots below 2 GiB");
@@ -2672,6 +2709,12 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   prm.ctr = reinterpret_cast<uint32_t*>(scratch);
   prm.wg_waves = ap.wg_waves;
   prm.stage_bytes = ap.stage_bytes ? static_cast<int>(ap.stage_bytes / ap.wg_waves) : 0;
+  if (ap.kv_split > 1) {
+    prm.Hkv = kv_heads * ap.kv_split;
+    prm.g = q_heads / prm.Hkv;
+    prm.kv_split = ap.kv_split;
+    prm.kv_rows = kv_heads;
+  }
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (fused) {

@@ -897,6 +897,61 @@ HELD_LAYOUTS = [
 ]
 
 
+LARGE_GROUP_SHAPES = [
+    # (dtype, Hq, Hkv, D, P, lengths): groups above 16 q-heads, served as equal chunks of <= 16
+    (torch.bfloat16, 48, 1, 128, 16, [1, 17, 300, 2048, 0, 5000]),          # 3 x 16, 3 waves
+    (torch.float16, 32, 1, 64, 32, [33, 1000, 4097, 2]),                    # 2 x 16, D 64
+    (torch.bfloat16, 64, 2, 128, 16, [700, 1, 3000]),                       # 4 virtual kv-heads: one wave per SIMD
+    (torch.bfloat16, 40, 1, 128, 16, [129, 2500]),                          # 4 x 10: padded chunks
+    (torch.float16, 96, 2, 256, 16, [900, 31, 2000]),                       # D 256, 3 x 16
+    (torch.bfloat16, 384, 8, 128, 16, [300, 1200]),                         # 24 virtual kv-heads, 6 waves
+    (torch.bfloat16, 48, 1, 128, 16, _fused_lengths(300, 1, 200, 131)),     # held result rows
+]
+
+
+@pytest.mark.parametrize("shape", LARGE_GROUP_SHAPES,
+                         ids=lambda s: f"{DT_NAME[s[0]]}-Hq{s[1]}-Hkv{s[2]}-D{s[3]}-P{s[4]}-B{len(s[5])}")
+def test_large_groups_balanced_path(gpu, shape):
+    """Groups of more than 16 q-heads per kv-head on the balanced MFMA path:
+    each kv-head is served as equal chunks of at most 16 q-heads by waves of
+    one workgroup reading the same K/V rows.  The plan takes the path (kind
+    1), every row matches the oracle, and the torch op and the C ABI on a
+    NaN-filled workspace give the same bits."""
+    dtype, hq, hkv, d, p, lengths = shape
+    B = len(lengths)
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
+                                   dtype=dtype, seed=133, exact_pool=True), gpu)
+    q, k, v, table, lens = case
+    kind, waves, _, _ = cabi.auto_info(B, hq, hkv, d, p, table.shape[1], cabi.DTYPE[dtype])
+    say(f"large group: {DT_NAME[dtype]} Hq{hq} Hkv{hkv} D{d} P{p} B{B} kind={kind} waves={waves}")
+    assert kind == 1
+    ref, rows = oracle_rows(case)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    assert_close(out, ref, DT_NAME[dtype], rows, "large group")
+    ws = cabi.auto_workspace(B, hq, hkv, d, p, table.shape[1], cabi.DTYPE[dtype], gpu, fill=0xFF)
+    out_c = torch.full_like(q, float("nan"))
+    rc = cabi.auto_launch(*case, out_c, scale=1 / math.sqrt(d), workspace=ws)
+    assert rc == 0, cabi.error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_c)
+
+
+def test_prime_large_group_generic_path(gpu):
+    """A group of 71 q-heads (no split into at most 8 equal chunks of at most
+    16) stays on the split layout's generic kernel and matches the oracle."""
+    hq, hkv, d, p, lengths = 71, 1, 64, 16, [1, 500, 2100]
+    case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
+                                   dtype=torch.bfloat16, seed=134), gpu)
+    kind = cabi.auto_info(len(lengths), hq, hkv, d, p, case[3].shape[1], cabi.DTYPE[torch.bfloat16])[0]
+    say(f"prime group 71: kind={kind}")
+    assert kind == 0
+    ref, rows = oracle_rows(case)
+    out = attention_amd.gqa_decode(*case)
+    torch.cuda.synchronize()
+    assert_close(out, ref, "bf16", rows, "group 71")
+
+
 @pytest.mark.parametrize("shape", HELD_LAYOUTS,
                          ids=lambda s: f"{DT_NAME[s[3]]}-Hq{s[0]}-Hkv{s[1]}-D{s[2]}-B{len(s[5])}")
 def test_held_results_every_layout(gpu, shape):
