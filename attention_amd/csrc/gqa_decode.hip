@@ -79,11 +79,14 @@ struct DecodeParams {
   uint32_t* ctr;  // fused stream-K path: arrival counter per (sequence, kv-head), zero between calls
   int stage_bytes;  // stream-K path: LDS bytes per wave for result rows held until the range ends
   // Stream-K path, groups of more than kMfmaHeads q-heads: each kv-head is
-  // served as kv_split virtual kv-heads of g = (Hq/kv_rows)/kv_split q-heads
-  // (Hkv = kv_rows * kv_split); virtual kv-head v reads K/V column v /
-  // kv_split of token rows of kv_rows kv-heads.  Otherwise 1 and Hkv.
+  // served as kv_split virtual kv-heads (Hkv = kv_rows * kv_split) of up to
+  // g q-heads each, the last one of a kv-head possibly fewer (the real
+  // group is kv_g); virtual kv-head v reads K/V column v / kv_split of token
+  // rows of kv_rows kv-heads (vhead_base, vhead_count).  Otherwise 1, Hkv
+  // and g.
   int kv_split;
   int kv_rows;
+  int kv_g;
 #ifdef QD_STAMPS
   uint64_t* stamps;  // diagnostic build: per-wave timestamps (stamp_wave)
 #endif
@@ -426,6 +429,14 @@ struct KTile {
   __device__ static int col_bytes(int lane) { return 16 * (lane % kLanesPerRow); }
 };
 
+// First q-head and q-head count of (virtual) kv-head v.
+__device__ __forceinline__ int vhead_base(const DecodeParams& p, int v) {
+  return p.kv_split > 1 ? (v / p.kv_split) * p.kv_g + (v % p.kv_split) * p.g : v * p.g;
+}
+__device__ __forceinline__ int vhead_count(const DecodeParams& p, int v) {
+  return p.kv_split > 1 ? min(p.g, p.kv_g - (v % p.kv_split) * p.g) : p.g;
+}
+
 // One wave's decode state for NKV adjacent kv-heads (kvh0 .. kvh0+NKV-1) of
 // one sequence.  Serving two kv-heads from one wave (one wave per SIMD)
 // keeps the K/V streams of a SIMD in one instruction stream: two waves on a
@@ -459,6 +470,7 @@ struct MfmaWave {
   const char* kbase;  // kv-head kvh0; kv-head kvh0+j is 2*D*j bytes further
   const char* vbase;
   const int32_t* trow;
+  int hcount;  // q-heads of each kv-head of the item (vhead_count; p.g unless split)
   int len;    // valid tokens of the item (or of the split)
   int wbase;  // first page of the table window held in tblv
   int tblv;   // table entry (wbase + lane)
@@ -477,15 +489,15 @@ struct MfmaWave {
   // table window of g_first is loaded before the query, so the first K/V
   // loads wait for the table alone; the query is needed only at compute.
   __device__ void begin_item(const DecodeParams& p, int b, int kvh0, int valid_tokens, int g_first) {
-    const int g = p.g;
-    const bool head_ok = r16 < g;
+    hcount = vhead_count(p, kvh0);  // NKV is 1 whenever kv-heads are split
+    const bool head_ok = r16 < hcount;
     trow = p.table + static_cast<int64_t>(b) * p.maxP;
     wbase = g_first / (p.P >> 4);
     tblv = (lane < p.maxP - wbase) ? trow[wbase + lane] : 0;
 #pragma unroll
     for (int j = 0; j < NKV; ++j) {
       const char* qp = static_cast<const char*>(p.q) +
-                       (static_cast<int64_t>(b) * p.Hq + (kvh0 + j) * g + (head_ok ? r16 : 0)) * D * 2;
+                       (static_cast<int64_t>(b) * p.Hq + vhead_base(p, kvh0 + j) + (head_ok ? r16 : 0)) * D * 2;
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
         const u32x4 x = *reinterpret_cast<const u32x4*>(qp + (32 * c + 8 * q4) * 2);
@@ -691,7 +703,7 @@ struct MfmaWave {
 
   __device__ void stage_direct(const DecodeParams& p, char* area, int jk, float l_tot) {
     using S = typename Elem<DT>::S;
-    if (r16 >= p.g) return;
+    if (r16 >= hcount) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     S* o = reinterpret_cast<S*>(area) + (jk * p.g + r16) * D;
 #pragma unroll
@@ -708,7 +720,7 @@ struct MfmaWave {
   }
 
   __device__ void stage_partial(const DecodeParams& p, char* area, int jk, float l_tot) {
-    if (r16 >= p.g) return;
+    if (r16 >= hcount) return;
     float* w = reinterpret_cast<float*>(area) + (jk * p.g + r16) * (D + 2);
     if (q4 == 0) {
       w[0] = m_run[jk] * kLn2;
@@ -764,12 +776,13 @@ struct MfmaWave {
     res_used = 0;
   }
 
-  // out[b, (kvh0+jk)*g + r16, :] = acc / l (zeros when l == 0), one rounding.
+  // out[b, vhead_base(kvh0+jk) + r16, :] = acc / l (zeros when l == 0), one
+  // rounding.
   __device__ void store_direct(const DecodeParams& p, int b, int kvh0, int jk, float l_tot) {
     using S = typename Elem<DT>::S;
-    if (r16 >= p.g) return;
+    if (r16 >= hcount) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + (kvh0 + jk) * p.g + r16) * D;
+    S* o = static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + vhead_base(p, kvh0 + jk) + r16) * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t wv[DV / 2];
@@ -811,7 +824,7 @@ struct MfmaWave {
   // Stores a stashed partial as store_partial<true> stores a live one.
   __device__ void store_stashed(const DecodeParams& p, int jk, const float* stash, float* w,
                                 int64_t head_stride) const {
-    if (r16 >= p.g) return;
+    if (r16 >= hcount) return;
     const float* s = stash + jk * kStashFields * 64 + lane;
     w += r16 * head_stride;
     if (q4 == 0) coherent_store2(w, s[0], s[64]);
@@ -829,7 +842,7 @@ struct MfmaWave {
   // stores, for a merge by another workgroup of the same launch.
   template <bool COH = false>
   __device__ void store_partial(const DecodeParams& p, int jk, float* w, int64_t head_stride, float l_tot) {
-    if (r16 >= p.g) return;
+    if (r16 >= hcount) return;
     w += r16 * head_stride;
     if (q4 == 0) {
       if constexpr (COH) {
@@ -1559,7 +1572,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
             else if (mid_range)
               wv.stash_partial(j, stash + ((kvh0 - wid * NKV) / (nw * NKV)) * NKV * Wave::kStashFields * 64, l_tot);
             else
-              wv.template store_partial<true>(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2),
+              wv.template store_partial<true>(p, j, slot + static_cast<int64_t>(vhead_base(p, kvh0 + j)) * (D + 2),
                                                D + 2, l_tot);
           }
         } else if constexpr (GV == 0 && !HOLD) {
@@ -1569,10 +1582,13 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
             if (whole)
               wv.store_direct(p, b, kvh0, j, l_tot);
             else
-              wv.store_partial(p, j, slot + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2), D + 2, l_tot);
+              wv.store_partial(p, j, slot + static_cast<int64_t>(vhead_base(p, kvh0 + j)) * (D + 2), D + 2, l_tot);
           }
         } else if constexpr (HOLD) {
-          const int bytes = whole ? NKV * p.g * D * static_cast<int>(sizeof(S)) : NKV * p.g * (D + 2) * 4;
+          // The item's heads (fewer than NKV * g for a short last chunk of
+          // a split kv-head): the flush writes exactly these rows.
+          const int nheads = p.kv_split > 1 ? wv.hcount : NKV * p.g;
+          const int bytes = whole ? nheads * D * static_cast<int>(sizeof(S)) : nheads * (D + 2) * 4;
           char* area = wv.stage_slot(bytes);
 #pragma unroll
           for (int j = 0; j < NKV; ++j) {
@@ -1584,16 +1600,17 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
           }
           if (whole)
             wv.stage_commit(reinterpret_cast<char*>(static_cast<S*>(p.out) +
-                                                    (static_cast<int64_t>(b) * p.Hq + kvh0 * p.g) * D),
+                                                    (static_cast<int64_t>(b) * p.Hq + vhead_base(p, kvh0)) * D),
                             bytes, 16);
           else
-            wv.stage_commit(reinterpret_cast<char*>(slot + static_cast<int64_t>(kvh0) * p.g * (D + 2)), bytes, 8);
+            wv.stage_commit(reinterpret_cast<char*>(slot + static_cast<int64_t>(vhead_base(p, kvh0)) * (D + 2)),
+                            bytes, 8);
         } else {
           wv.finish_item();
           if (whole)
             wv.store_direct(p, b, kvh0);
           else
-            wv.store_partial(p, slot + static_cast<int64_t>(kvh0) * p.g * (D + 2));
+            wv.store_partial(p, slot + static_cast<int64_t>(vhead_base(p, kvh0)) * (D + 2));
         }
       }
       if constexpr (FUSED) {
@@ -1648,7 +1665,7 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
           const float* st = stash + ((kvh0 - wid * NKV) / (nw * NKV)) * NKV * Wave::kStashFields * 64;
 #pragma unroll
           for (int j = 0; j < NKV; ++j)
-            wv.store_stashed(p, j, st, slot0 + static_cast<int64_t>(kvh0 + j) * p.g * (D + 2), D + 2);
+            wv.store_stashed(p, j, st, slot0 + static_cast<int64_t>(vhead_base(p, kvh0 + j)) * (D + 2), D + 2);
         }
       }
       wait_memory_retired();  // this wave's sc1 partial stores are visible device-wide
@@ -2223,18 +2240,23 @@ struct AutoPlan {
 };
 
 // Virtual kv-heads per kv-head for the stream-K path: 1 for groups of at
-// most kMfmaHeads q-heads, else the fewest equal chunks of at most
-// kMfmaHeads q-heads (a group of 48 is 3 x 16, of 40 is 4 x 10), at most
-// kMaxWgWaves of them so that one kv-head's chunks are waves of one
-// workgroup, reading the same K/V rows in the same steps; 0 when no such
-// split exists (groups above 128, or a prime such as 71).
+// most kMfmaHeads q-heads, else the fewest chunks of at most kMfmaHeads
+// q-heads, c = ceil(g / kMfmaHeads), of ceil(g / c) q-heads each but the
+// last (48 is 3 x 16, 40 is 3 x 14 with 12 in the last, 71 is 5 x 15 with
+// 11), at most kMaxWgWaves of them so that one kv-head's chunks are waves
+// of one workgroup, reading the same K/V rows in the same steps; 0 for
+// groups above kMaxWgWaves * kMfmaHeads (128).
 int kv_split_for(int q_heads, int kv_heads) {
   if (kv_heads <= 0 || q_heads % kv_heads != 0) return 0;
   const int g = q_heads / kv_heads;
-  if (g <= kMfmaHeads) return 1;
-  for (int c = 2; c <= kMaxWgWaves; ++c)
-    if (g % c == 0 && g / c <= kMfmaHeads) return c;
-  return 0;
+  const int c = (g + kMfmaHeads - 1) / kMfmaHeads;
+  return c <= kMaxWgWaves ? c : 0;
+}
+
+// q-heads per virtual kv-head (the chunk size; the real group when c = 1).
+int kv_chunk_heads(int q_heads, int kv_heads, int c) {
+  const int g = q_heads / kv_heads;
+  return c > 1 ? (g + c - 1) / c : g;
 }
 
 // Shapes the fused merge can address: one counter per (sequence, kv-head)
@@ -2269,7 +2291,8 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
   if (batch <= 0) return QD_OK;
   const int split = kv_split_for(q_heads, kv_heads);
   const int vkv = kv_heads * (split > 0 ? split : 1);  // kv-heads as the stream-K kernel serves them
-  if (aligned && split > 0 && (split == 1 || !valu) && mfma_applies(q_heads, vkv, head_dim, block_size, dtype) &&
+  const int gv = split > 0 ? kv_chunk_heads(q_heads, kv_heads, split) : 0;  // q-heads per one of them, at most
+  if (aligned && split > 0 && (split == 1 || !valu) && mfma_applies(vkv * gv, vkv, head_dim, block_size, dtype) &&
       batch <= kSkMaxBatch) {
     int nkv = 1;
     const bool wide = !valu && sk_wide_applies(vkv, head_dim);
@@ -2281,7 +2304,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
         break;
       }
     }
-    const int g = q_heads / vkv;
+    const int g = gv;
     KernelFn fn = valu ? pick_valu_sk_dt(dtype, g) : pick_mfma_sk_dt(dtype, head_dim, nkv, wide);
     int resident = resident_blocks(fn, 64 * nw);
     if (!valu && split == 1 && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
@@ -2324,9 +2347,9 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     ap->wg_waves = nw;
     ap->kv_per_wave = nkv;
     ap->wide = wide && nkv == 1;
-    ap->stash_bytes = fused_stash_bytes(vkv, head_dim, nkv, nw);
+    ap->stash_bytes = fused_stash_bytes(vkv, head_dim, nkv, nw);  // used by the fused kernel only (split == 1)
     const KernelFn ffn = pick_mfma_sk_dt(dtype, head_dim, nkv, ap->wide, true);
-    if (kFusedByDefault && !valu && fused_applies(batch, q_heads, vkv, head_dim, nkv, w) &&
+    if (kFusedByDefault && !valu && split == 1 && fused_applies(batch, q_heads, kv_heads, head_dim, nkv, w) &&
         ap->stash_bytes <= kFusedMaxStash && allow_dyn_lds(ffn)) {
       // The fused kernel's own occupancy (registers and the stash) bounds
       // the grid; without waits between workgroups a larger grid would
@@ -2334,7 +2357,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
       const int64_t rf = resident_blocks(ffn, 64 * nw, ap->stash_bytes) * kSkOversubscribe;
       if (w > rf) w = rf;
       ap->wgs = static_cast<int>(w);
-      ap->fused = fused_fits(batch, q_heads, vkv, head_dim, w);
+      ap->fused = fused_fits(batch, q_heads, kv_heads, head_dim, w);
     }
     ap->meta_offset = kCounterBytes + static_cast<size_t>(w + batch) * q_heads * (head_dim + 2) * sizeof(float);
     ap->ws_bytes = ap->meta_offset + static_cast<size_t>(batch) * 2 * sizeof(int);
@@ -2409,6 +2432,7 @@ DecodeParams make_params(const void* q, const void* k_cache, const void* v_cache
   prm.stage_bytes = 0;
   prm.kv_split = 1;
   prm.kv_rows = kv_heads;
+  prm.kv_g = prm.g;
 #ifdef QD_STAMPS
   prm.stamps = g_stamps;
 #endif
@@ -2696,10 +2720,11 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   bool fused = ap.fused;
   if (unfused) fused = false;
   if (force_fused) {
-    if (valu || !fused_fits(batch, q_heads, kv_heads * ap.kv_split, head_dim, ap.wgs) || ap.stash_bytes > kFusedMaxStash ||
+    if (valu || ap.kv_split > 1 || !fused_fits(batch, q_heads, kv_heads, head_dim, ap.wgs) ||
+        ap.stash_bytes > kFusedMaxStash ||
         !allow_dyn_lds(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, true)))
-      return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_FUSED needs MFMA math, batch * kv_heads <= 65536 and "
-                                        "partial slots below 2 GiB");
+      return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_FUSED needs MFMA math, at most 16 q-heads per kv-head, "
+                                        "batch * kv_heads <= 65536 and partial slots below 2 GiB");
     fused = true;
   }
   DecodeParams prm = make_params(q, k_cache, v_cache, block_table, context_lens, out, scratch + kCounterBytes,
@@ -2711,9 +2736,10 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   prm.stage_bytes = ap.stage_bytes ? static_cast<int>(ap.stage_bytes / ap.wg_waves) : 0;
   if (ap.kv_split > 1) {
     prm.Hkv = kv_heads * ap.kv_split;
-    prm.g = q_heads / prm.Hkv;
+    prm.g = kv_chunk_heads(q_heads, kv_heads, ap.kv_split);
     prm.kv_split = ap.kv_split;
     prm.kv_rows = kv_heads;
+    prm.kv_g = q_heads / kv_heads;
   }
   hipStream_t stm = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();

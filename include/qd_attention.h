@@ -146,9 +146,9 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  * partition is chosen from static shapes and the device (CU count and
  * kernel occupancy), never from context_lens on the host:
  *   - 16-bit caches with head_dim 64/128/256, block_size a multiple of 16,
- *     group size <= 16 (or up to 128 when it splits into at most 8 equal
- *     chunks of at most 16, each served like a kv-head of its own) and
- *     batch <= 4096: the (sequence, 16-token group)
+ *     group size <= 128 (a group above 16 is served as ceil(g/16) chunks of
+ *     at most 16 q-heads, each like a kv-head of its own) and batch <= 4096:
+ *     the (sequence, 16-token group)
  *     space is cut into cost-balanced ranges, one per resident workgroup;
  *     a sequence split across workgroups leaves one partial per workgroup,
  *     folded (log-sum-exp) either inside the same kernel by the last

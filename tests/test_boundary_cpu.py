@@ -204,16 +204,17 @@ def test_auto_grid_below_resident():
 @pytest.mark.skipif(torch.cuda.is_available(),
                     reason="wave counts assume the CPU-only occupancy fallback (256 CUs, one workgroup each)")
 def test_auto_large_groups():
-    """Groups above 16 q-heads take the balanced path as c virtual kv-heads
-    per kv-head (the fewest equal chunks of at most 16, c <= 8), with one
-    kv-head's chunks in one pass of a workgroup's waves; groups with no such
-    split, and fp32, take the split layout (kind 0)."""
+    """Groups above 16 q-heads take the balanced path as c = ceil(g/16)
+    virtual kv-heads per kv-head (chunks of ceil(g/c) q-heads, the last one
+    shorter), c <= 8, with one kv-head's chunks in one pass of a workgroup's
+    waves; larger groups, and fp32, take the split layout (kind 0)."""
     bf16, f32 = cabi.DTYPE[torch.bfloat16], cabi.DTYPE[torch.float32]
     assert cabi.auto_info(32, 48, 1, 128, 16, 128, bf16)[:2] == (1, 256 * 3)    # 3 x 16
-    assert cabi.auto_info(32, 40, 1, 128, 16, 64, bf16)[:2] == (1, 256 * 4)     # 4 x 10
+    assert cabi.auto_info(32, 40, 1, 128, 16, 64, bf16)[:2] == (1, 256 * 3)     # 14 + 14 + 12
+    assert cabi.auto_info(16, 71, 1, 64, 16, 256, bf16)[:2] == (1, 256 * 5)     # 4 x 15 + 11
     assert cabi.auto_info(32, 64, 2, 128, 16, 128, bf16)[:2] == (1, 256 * 4)    # 2 x 2 x 16
     assert cabi.auto_info(8, 384, 8, 128, 16, 256, bf16)[:2] == (1, 256 * 6)    # 24 virtual, passes of 6
-    assert cabi.auto_info(16, 71, 1, 64, 16, 256, bf16)[0] == 0                  # prime group
+    assert cabi.auto_info(4, 128, 1, 128, 16, 64, bf16)[:2] == (1, 256 * 8)     # 8 x 16, the most
     assert cabi.auto_info(4, 136, 1, 128, 16, 64, bf16)[0] == 0                  # 9 chunks would be needed
     assert cabi.auto_info(32, 48, 1, 128, 16, 128, f32)[0] == 0
 

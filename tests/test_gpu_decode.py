@@ -902,10 +902,13 @@ LARGE_GROUP_SHAPES = [
     (torch.bfloat16, 48, 1, 128, 16, [1, 17, 300, 2048, 0, 5000]),          # 3 x 16, 3 waves
     (torch.float16, 32, 1, 64, 32, [33, 1000, 4097, 2]),                    # 2 x 16, D 64
     (torch.bfloat16, 64, 2, 128, 16, [700, 1, 3000]),                       # 4 virtual kv-heads: one wave per SIMD
-    (torch.bfloat16, 40, 1, 128, 16, [129, 2500]),                          # 4 x 10: padded chunks
+    (torch.bfloat16, 40, 1, 128, 16, [129, 2500]),                          # 14 + 14 + 12: a short last chunk
+    (torch.bfloat16, 71, 1, 64, 16, [1, 500, 2100]),                        # 4 x 15 + 11, D 64
+    (torch.float16, 128, 1, 128, 16, [40, 3000]),                           # 8 x 16, 8 waves
     (torch.float16, 96, 2, 256, 16, [900, 31, 2000]),                       # D 256, 3 x 16
     (torch.bfloat16, 384, 8, 128, 16, [300, 1200]),                         # 24 virtual kv-heads, 6 waves
     (torch.bfloat16, 48, 1, 128, 16, _fused_lengths(300, 1, 200, 131)),     # held result rows
+    (torch.float16, 40, 1, 64, 16, _fused_lengths(300, 1, 120, 132)),      # held rows, short last chunk
 ]
 
 
@@ -937,19 +940,19 @@ def test_large_groups_balanced_path(gpu, shape):
     assert torch.equal(out, out_c)
 
 
-def test_prime_large_group_generic_path(gpu):
-    """A group of 71 q-heads (no split into at most 8 equal chunks of at most
-    16) stays on the split layout's generic kernel and matches the oracle."""
-    hq, hkv, d, p, lengths = 71, 1, 64, 16, [1, 500, 2100]
+def test_group_above_128_generic_path(gpu):
+    """A group of 136 q-heads (more than 8 chunks of 16) stays on the split
+    layout's generic kernel and matches the oracle."""
+    hq, hkv, d, p, lengths = 136, 1, 64, 16, [1, 500, 2100]
     case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
                                    dtype=torch.bfloat16, seed=134), gpu)
     kind = cabi.auto_info(len(lengths), hq, hkv, d, p, case[3].shape[1], cabi.DTYPE[torch.bfloat16])[0]
-    say(f"prime group 71: kind={kind}")
+    say(f"group 136: kind={kind}")
     assert kind == 0
     ref, rows = oracle_rows(case)
     out = attention_amd.gqa_decode(*case)
     torch.cuda.synchronize()
-    assert_close(out, ref, "bf16", rows, "group 71")
+    assert_close(out, ref, "bf16", rows, "group 136")
 
 
 @pytest.mark.parametrize("shape", HELD_LAYOUTS,
