@@ -905,6 +905,8 @@ LARGE_GROUP_SHAPES = [
     (torch.bfloat16, 40, 1, 128, 16, [129, 2500]),                          # 14 + 14 + 12: a short last chunk
     (torch.bfloat16, 71, 1, 64, 16, [1, 500, 2100]),                        # 4 x 15 + 11, D 64
     (torch.float16, 128, 1, 128, 16, [40, 3000]),                           # 8 x 16, 8 waves
+    (torch.bfloat16, 64, 1, 64, 16, [17, 1500, 3000]),                      # 4 x 16, D 64
+    (torch.bfloat16, 64, 1, 128, 16, [700, 1, 3000]),                       # 4 x 16: one wave per SIMD
     (torch.float16, 96, 2, 256, 16, [900, 31, 2000]),                       # D 256, 3 x 16
     (torch.bfloat16, 384, 8, 128, 16, [300, 1200]),                         # 24 virtual kv-heads, 6 waves
     (torch.bfloat16, 48, 1, 128, 16, _fused_lengths(300, 1, 200, 131)),     # held result rows
