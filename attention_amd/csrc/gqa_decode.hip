@@ -389,6 +389,10 @@ __device__ __forceinline__ VRow<D> load_vrow(const char* ptr) {
     const u32x2 x = stream_load8(ptr);
     r.w[0] = x[0];
     r.w[1] = x[1];
+  } else if constexpr (VRow<D>::kWords == 3) {  // head_dim 96: 12 bytes, 4-byte aligned
+    r.w[0] = stream_load4(ptr);
+    r.w[1] = stream_load4(ptr + 4);
+    r.w[2] = stream_load4(ptr + 8);
   } else {
 #pragma unroll
     for (int i = 0; i < VRow<D>::kWords / 4; ++i) {
@@ -403,6 +407,22 @@ __device__ __forceinline__ VRow<D> load_vrow(const char* ptr) {
 }
 
 // Registers for one 16-token group in flight, for NKV kv-heads.
+// Stores NW 32-bit words at dst: one 8-byte store for 2, 16-byte stores for
+// a multiple of 4 (dst aligned to match), else one word at a time.
+template <int NW>
+__device__ __forceinline__ void store_words(char* dst, const uint32_t* wv) {
+  if constexpr (NW == 2) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
+  } else if constexpr (NW % 4 == 0) {
+#pragma unroll
+    for (int t = 0; t < NW / 4; ++t)
+      *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+  } else {
+#pragma unroll
+    for (int t = 0; t < NW; ++t) reinterpret_cast<uint32_t*>(dst)[t] = wv[t];
+  }
+}
+
 template <int D, int NKV>
 struct GroupBuf {
   static constexpr int KC = D / 32;
@@ -422,7 +442,10 @@ template <int D>
 struct KTile {
   static constexpr int kRowBytes = 2 * D;
   static constexpr int kStride = kRowBytes + 32;
-  static constexpr int kLanesPerRow = kRowBytes / 16;  // 8, 16, 32
+  static constexpr int kLanesPerRow = kRowBytes / 16;  // 8, 16, 32 (12 at head_dim 96)
+  // Rows that do not tile a 1 KB load (head_dim 96): K is loaded straight in
+  // the MFMA A layout instead (16 rows x 64 bytes per instruction), no LDS.
+  static constexpr bool kDirect = 64 % kLanesPerRow != 0;
   static constexpr int kRowsPerLoad = 64 / kLanesPerRow;
   static constexpr int kBytes = 16 * kStride;
   __device__ static int row(int c, int lane) { return c * kRowsPerLoad + lane / kLanesPerRow; }
@@ -537,8 +560,13 @@ struct MfmaWave {
     for (int j = 0; j < NKV; ++j) {
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
-        const uint32_t rk = static_cast<uint32_t>(min(KTile<D>::row(c, lane), last));
-        buf.k[j][c] = stream_load16(kp + j * 2 * D + rk * rb32 + kcol);
+        if constexpr (KTile<D>::kDirect) {  // the A layout: row r16, bytes 64c + 16q4
+          const uint32_t rk = static_cast<uint32_t>(min(r16, last));
+          buf.k[j][c] = stream_load16(kp + j * 2 * D + rk * rb32 + 64 * c + 16 * q4);
+        } else {
+          const uint32_t rk = static_cast<uint32_t>(min(KTile<D>::row(c, lane), last));
+          buf.k[j][c] = stream_load16(kp + j * 2 * D + rk * rb32 + kcol);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -556,15 +584,20 @@ struct MfmaWave {
 #pragma unroll
     for (int j = 0; j < NKV; ++j) {
       // Transpose K through LDS into the A layout: lane (r16, q4), chunk c
-      // holds row r16, bytes [64c + 16q4, +16).
-#pragma unroll
-      for (int c = 0; c < KC; ++c)
-        *reinterpret_cast<u32x4*>(ktile + KTile<D>::row(c, lane) * KTile<D>::kStride +
-                                  KTile<D>::col_bytes(lane)) = buf.k[j][c];
+      // holds row r16, bytes [64c + 16q4, +16) (loaded that way when kDirect).
       u32x4 ka[KC];
+      if constexpr (KTile<D>::kDirect) {
 #pragma unroll
-      for (int c = 0; c < KC; ++c)
-        ka[c] = *reinterpret_cast<const u32x4*>(ktile + r16 * KTile<D>::kStride + 64 * c + 16 * q4);
+        for (int c = 0; c < KC; ++c) ka[c] = buf.k[j][c];
+      } else {
+#pragma unroll
+        for (int c = 0; c < KC; ++c)
+          *reinterpret_cast<u32x4*>(ktile + KTile<D>::row(c, lane) * KTile<D>::kStride +
+                                    KTile<D>::col_bytes(lane)) = buf.k[j][c];
+#pragma unroll
+        for (int c = 0; c < KC; ++c)
+          ka[c] = *reinterpret_cast<const u32x4*>(ktile + r16 * KTile<D>::kStride + 64 * c + 16 * q4);
+      }
       f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < KC; ++c) s = Ops::qk(ka[c], qv[j][c], s);
@@ -790,15 +823,7 @@ struct MfmaWave {
       for (int j = 0; j < DV; j += 2)
         wv[j / 2] = Ops::pack2(l_tot > 0.f ? acc[jk][j][i] * inv : 0.f,
                                l_tot > 0.f ? acc[jk][j + 1][i] * inv : 0.f);
-      char* dst = reinterpret_cast<char*>(o + DV * (4 * q4 + i));
-      if constexpr (DV / 2 == 2) {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
-      } else {
-#pragma unroll
-        for (int t = 0; t < DV / 8; ++t)
-          *reinterpret_cast<u32x4*>(dst + 16 * t) =
-              u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
-      }
+      store_words<DV / 2>(reinterpret_cast<char*>(o + DV * (4 * q4 + i)), wv);
     }
   }
 
@@ -1219,6 +1244,7 @@ struct MergeRows {
     if (!active) return;
     const float inv = L > 0.f ? 1.f / L : 0.f;
     if constexpr (DT == QD_DTYPE_F32) {
+      static_assert(EPL % 4 == 0, "fp32 rows: head_dim a multiple of 64");
       float* dst = out + c16 * EPL;
 #pragma unroll
       for (int e = 0; e < EPL; e += 4)
@@ -1229,14 +1255,7 @@ struct MergeRows {
 #pragma unroll
       for (int e = 0; e < EPL; e += 2)
         wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
-      char* dst = reinterpret_cast<char*>(out + c16 * EPL);
-      if constexpr (EPL == 4) {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
-      } else {
-#pragma unroll
-        for (int t = 0; t < EPL / 8; ++t)
-          *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
-      }
+      store_words<EPL / 2>(reinterpret_cast<char*>(out + c16 * EPL), wv);
     }
   }
 };
@@ -1349,14 +1368,8 @@ __device__ void merge_item_fused(const DecodeParams& p, int b, int h_begin, int 
 #pragma unroll
       for (int e = 0; e < EPL; e += 2)
         wv[e / 2] = MfmaOps<DT>::pack2(L > 0.f ? acc[e] * inv : 0.f, L > 0.f ? acc[e + 1] * inv : 0.f);
-      char* dst = reinterpret_cast<char*>(static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D + c16 * EPL);
-      if constexpr (EPL == 4) {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{wv[0], wv[1]};
-      } else {
-#pragma unroll
-        for (int t = 0; t < EPL / 8; ++t)
-          *reinterpret_cast<u32x4*>(dst + 16 * t) = u32x4{wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
-      }
+      store_words<EPL / 2>(
+          reinterpret_cast<char*>(static_cast<S*>(p.out) + (static_cast<int64_t>(b) * p.Hq + h) * D + c16 * EPL), wv);
     }
   }
 }
@@ -1888,7 +1901,7 @@ constexpr int kMfmaHeads = 16;
 
 bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int dtype) {
   if (dtype != QD_DTYPE_F16 && dtype != QD_DTYPE_BF16) return false;
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return false;
+  if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256) return false;
   if (block_size % 16 != 0) return false;
   if (kv_heads <= 0 || q_heads % kv_heads != 0) return false;
   return q_heads / kv_heads <= kMfmaHeads;
@@ -1940,6 +1953,7 @@ template <int DT>
 KernelFn pick_mfma(int D) {
   switch (D) {
     case 64: return decode_mfma_kernel<64, DT, kPrefetch>;
+    case 96: return decode_mfma_kernel<96, DT, kPrefetch>;
     case 128: return decode_mfma_kernel<128, DT, kPrefetch>;
     default: return decode_mfma_kernel<256, DT, 2>;
   }
@@ -1971,6 +1985,7 @@ KernelFn pick_mfma_sk(int D, int nkv, bool wide) {
   }
   switch (D) {
     case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch, 1, 0, FUSED, HOLD>;
+    case 96: return decode_mfma_sk_kernel<96, DT, kPrefetch, 1, 0, FUSED, HOLD>;
     case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch, 1, 0, FUSED, HOLD>;
     default: return decode_mfma_sk_kernel<256, DT, 2, 1, 0, FUSED, HOLD>;
   }
@@ -2013,6 +2028,7 @@ template <int DT, int KB, int RG>
 KernelFn pick_merge_sk(int D) {
   switch (D) {
     case 64: return merge_sk_kernel<64, DT, KB, RG>;
+    case 96: return merge_sk_kernel<96, DT, KB, RG>;
     case 128: return merge_sk_kernel<128, DT, KB, RG>;
     default: return merge_sk_kernel<256, DT, KB, RG>;
   }
@@ -2183,7 +2199,7 @@ constexpr int64_t kSkDualTokensPerWg = 2048;
 
 bool sk_dual_applies(int batch, int kv_heads, int head_dim, int block_size, int max_pages,
                      int resident_wgs) {
-  if (head_dim > 128 || kv_heads % 2 != 0 || kv_heads < 8) return false;
+  if ((head_dim != 64 && head_dim != 128) || kv_heads % 2 != 0 || kv_heads < 8) return false;
   const int64_t cap = static_cast<int64_t>(batch) * max_pages * block_size;
   return cap >= kSkDualTokensPerWg * resident_wgs;
 }

@@ -276,6 +276,9 @@ __device__ __forceinline__ u32x4 stream_load16(const char* ptr) {
 __device__ __forceinline__ u32x2 stream_load8(const char* ptr) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(ptr));
 }
+__device__ __forceinline__ uint32_t stream_load4(const char* ptr) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(ptr));
+}
 
 // Streaming (nontemporal) load when NT, else a plain cached load: data that
 // other workgroups of the same XCD read soon after should stay in L2.

@@ -145,7 +145,7 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  * one split) and the split heuristic of attention/core.py:80-96.  The
  * partition is chosen from static shapes and the device (CU count and
  * kernel occupancy), never from context_lens on the host:
- *   - 16-bit caches with head_dim 64/128/256, block_size a multiple of 16,
+ *   - 16-bit caches with head_dim 64/96/128/256, block_size a multiple of 16,
  *     group size <= 128 (a group above 16 is served as ceil(g/16) chunks of
  *     at most 16 q-heads, each like a kv-head of its own) and batch <= 4096:
  *     the (sequence, 16-token group)

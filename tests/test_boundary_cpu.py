@@ -219,6 +219,17 @@ def test_auto_large_groups():
     assert cabi.auto_info(32, 48, 1, 128, 16, 128, f32)[0] == 0
 
 
+def test_head_dim_96_takes_the_mfma_kernels():
+    """head_dim 96 (K loaded in the MFMA A layout, 12-byte V rows) runs the
+    MFMA kernels on both paths; 80 and other head dims the generic one."""
+    bf16 = cabi.DTYPE[torch.bfloat16]
+    assert cabi.auto_info(32, 32, 32, 96, 16, 128, bf16)[0] == 1
+    assert cabi.auto_info(32, 32, 8, 96, 32, 64, bf16)[0] == 1
+    assert cabi.lib().qd_gqa_decode_kernel_kind(32, 8, 96, 16, bf16, 0) == 1
+    assert cabi.auto_info(32, 32, 32, 80, 16, 128, bf16)[0] == 0
+    assert cabi.lib().qd_gqa_decode_kernel_kind(32, 8, 80, 16, bf16, 0) == 0
+
+
 def test_auto_plan_uses_the_merge_kernel():
     """The automatic plan merges split sequences with the separate merge
     kernel (kind 1) for every benchmark shape; the fused merge is a

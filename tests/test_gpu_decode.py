@@ -129,6 +129,8 @@ SHAPES = [
     (torch.float16, 12, 4, 17, 5, [3, 19, 64]),
     (torch.bfloat16, 4, 4, 1, 1, [1, 2, 9]),
     (torch.float16, 64, 8, 128, 16, [2000, 1]),
+    (torch.bfloat16, 32, 32, 96, 16, [1, 300, 2049]),    # head_dim 96 (K in the A layout, 12-byte V rows)
+    (torch.float16, 32, 8, 96, 32, [17, 1000, 0, 33]),
 ]
 
 
@@ -894,6 +896,8 @@ HELD_LAYOUTS = [
     (28, 4, 128, torch.bfloat16, 4, _fused_lengths(300, 1, 400, 95)),
     # two kv-heads per wave: a wide table (one long sequence) among short ones
     (32, 8, 128, torch.float16, 4, [3500] + _fused_lengths(299, 1, 100, 96)),
+    # head_dim 96: 8 single-kv-head waves, 12-byte output pieces
+    (32, 8, 96, torch.bfloat16, 8, _fused_lengths(300, 1, 200, 135)),
 ]
 
 
@@ -907,6 +911,7 @@ LARGE_GROUP_SHAPES = [
     (torch.float16, 128, 1, 128, 16, [40, 3000]),                           # 8 x 16, 8 waves
     (torch.bfloat16, 64, 1, 64, 16, [17, 1500, 3000]),                      # 4 x 16, D 64
     (torch.bfloat16, 64, 1, 128, 16, [700, 1, 3000]),                       # 4 x 16: one wave per SIMD
+    (torch.bfloat16, 48, 1, 96, 16, [1, 700, 2500]),                        # 3 x 16 at head_dim 96
     (torch.float16, 96, 2, 256, 16, [900, 31, 2000]),                       # D 256, 3 x 16
     (torch.bfloat16, 384, 8, 128, 16, [300, 1200]),                         # 24 virtual kv-heads, 6 waves
     (torch.bfloat16, 48, 1, 128, 16, _fused_lengths(300, 1, 200, 131)),     # held result rows
