@@ -426,7 +426,7 @@ __device__ __forceinline__ void store_words(char* dst, const uint32_t* wv) {
 template <int D, int NKV>
 struct GroupBuf {
   static constexpr int KC = D / 32;
-  u32x4 k[NKV][KC];   // K, coalesced: 16 bytes of row KTile<D>::row(c, lane)
+  u32x4 k[NKV][KC];   // K, coalesced: piece KTile<D>::col_bytes(c, lane) of row KTile<D>::row(c, lane)
   VRow<D> v[NKV][4];  // V rows 4*(lane/16)+i, elements (D/16)*(lane%16) ..
   int tg;             // first token of the group
 };
@@ -434,22 +434,30 @@ struct GroupBuf {
 // K of one 16-token group moves HBM -> VGPR -> LDS -> VGPR.  The global
 // loads are coalesced (each instruction reads whole 2*D-byte row segments,
 // 1 KB per instruction), which streams measurably faster than loading the
-// MFMA operand layout directly (16 rows x 64 bytes per instruction).  The
-// LDS tile re-reads it in the MFMA A layout.  Rows are padded by 32 bytes:
-// measured free of LDS bank conflicts for D = 128 (16 bytes left 20% of the
-// LDS cycles in conflicts, none left 64%).
+// MFMA operand layout directly (16 rows x 64 bytes per instruction; 5-8%
+// slower at head_dim 96, about 10% at 128).  The LDS tile re-reads it in the
+// MFMA A layout.  Rows are padded by 32 bytes: measured free of LDS bank
+// conflicts for D = 128 (16 bytes left 20% of the LDS cycles in conflicts,
+// none left 64%).
+//
+// Load c, lane l reads the 16-byte piece 64c + l of the group's 16 rows in
+// row order: row (64c + l) / kLanesPerRow, piece (64c + l) % kLanesPerRow.
+// At head_dim 96 (12 pieces per row) a load ends inside a row.
 template <int D>
 struct KTile {
   static constexpr int kRowBytes = 2 * D;
   static constexpr int kStride = kRowBytes + 32;
-  static constexpr int kLanesPerRow = kRowBytes / 16;  // 8, 16, 32 (12 at head_dim 96)
-  // Rows that do not tile a 1 KB load (head_dim 96): K is loaded straight in
-  // the MFMA A layout instead (16 rows x 64 bytes per instruction), no LDS.
-  static constexpr bool kDirect = 64 % kLanesPerRow != 0;
-  static constexpr int kRowsPerLoad = 64 / kLanesPerRow;
+  static constexpr int kLanesPerRow = kRowBytes / 16;  // 8, 12, 16, 32
+  static constexpr bool kWholeRows = 64 % kLanesPerRow == 0;
   static constexpr int kBytes = 16 * kStride;
-  __device__ static int row(int c, int lane) { return c * kRowsPerLoad + lane / kLanesPerRow; }
-  __device__ static int col_bytes(int lane) { return 16 * (lane % kLanesPerRow); }
+  __device__ static int row(int c, int lane) {
+    if constexpr (kWholeRows) return c * (64 / kLanesPerRow) + lane / kLanesPerRow;
+    return (64 * c + lane) / kLanesPerRow;
+  }
+  __device__ static int col_bytes(int c, int lane) {
+    if constexpr (kWholeRows) return 16 * (lane % kLanesPerRow);
+    return 16 * ((64 * c + lane) % kLanesPerRow);
+  }
 };
 
 // First q-head and q-head count of (virtual) kv-head v.
@@ -555,18 +563,12 @@ struct MfmaWave {
     const char* vp = vbase + off;
     const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
     const int last = len - 1 - tg;  // rows > last are past the end: reuse row `last`
-    const uint32_t kcol = static_cast<uint32_t>(KTile<D>::col_bytes(lane));
 #pragma unroll
     for (int j = 0; j < NKV; ++j) {
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
-        if constexpr (KTile<D>::kDirect) {  // the A layout: row r16, bytes 64c + 16q4
-          const uint32_t rk = static_cast<uint32_t>(min(r16, last));
-          buf.k[j][c] = stream_load16(kp + j * 2 * D + rk * rb32 + 64 * c + 16 * q4);
-        } else {
-          const uint32_t rk = static_cast<uint32_t>(min(KTile<D>::row(c, lane), last));
-          buf.k[j][c] = stream_load16(kp + j * 2 * D + rk * rb32 + kcol);
-        }
+        const uint32_t rk = static_cast<uint32_t>(min(KTile<D>::row(c, lane), last));
+        buf.k[j][c] = stream_load16(kp + j * 2 * D + rk * rb32 + KTile<D>::col_bytes(c, lane));
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -584,20 +586,15 @@ struct MfmaWave {
 #pragma unroll
     for (int j = 0; j < NKV; ++j) {
       // Transpose K through LDS into the A layout: lane (r16, q4), chunk c
-      // holds row r16, bytes [64c + 16q4, +16) (loaded that way when kDirect).
+      // holds row r16, bytes [64c + 16q4, +16).
       u32x4 ka[KC];
-      if constexpr (KTile<D>::kDirect) {
 #pragma unroll
-        for (int c = 0; c < KC; ++c) ka[c] = buf.k[j][c];
-      } else {
+      for (int c = 0; c < KC; ++c)
+        *reinterpret_cast<u32x4*>(ktile + KTile<D>::row(c, lane) * KTile<D>::kStride +
+                                  KTile<D>::col_bytes(c, lane)) = buf.k[j][c];
 #pragma unroll
-        for (int c = 0; c < KC; ++c)
-          *reinterpret_cast<u32x4*>(ktile + KTile<D>::row(c, lane) * KTile<D>::kStride +
-                                    KTile<D>::col_bytes(lane)) = buf.k[j][c];
-#pragma unroll
-        for (int c = 0; c < KC; ++c)
-          ka[c] = *reinterpret_cast<const u32x4*>(ktile + r16 * KTile<D>::kStride + 64 * c + 16 * q4);
-      }
+      for (int c = 0; c < KC; ++c)
+        ka[c] = *reinterpret_cast<const u32x4*>(ktile + r16 * KTile<D>::kStride + 64 * c + 16 * q4);
       f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < KC; ++c) s = Ops::qk(ka[c], qv[j][c], s);
@@ -1263,8 +1260,8 @@ struct MergeRows {
 constexpr int kMaxWgWaves = 8;
 
 // Waves per stream-K workgroup at most: 8 serving one kv-head each, or 4
-// (one per SIMD, so each may use 512 registers) serving two each or with
-// head_dim 256.
+// (one per SIMD, so each may use 512 registers) serving two each, with
+// head_dim 256, or with 3 groups in flight above head_dim 64.
 #ifndef QD_VALU_WAVES
 #define QD_VALU_WAVES 8
 #endif
@@ -1283,7 +1280,7 @@ constexpr int kValuPrefetch = QD_VALU_PF;
 template <int D, int NKV, int GV = 0, int PF = 2>
 constexpr int sk_max_waves() {
   if (GV > 0) return kValuMaxWaves;
-  return (NKV == 1 && D <= 128 && PF <= 2) ? kMaxWgWaves : kMaxWgWaves / 2;
+  return (NKV == 1 && D <= 128 && (PF <= 2 || D <= 64)) ? kMaxWgWaves : kMaxWgWaves / 2;
 }
 
 #ifndef QD_SK_SEQ_COST
@@ -1914,6 +1911,11 @@ bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int d
 // kv-head per wave on the stream-K path (cfg3's kernel 79.4 -> 78.7 us
 // against 3; 4 spills).
 constexpr int kPrefetch = QD_PREFETCH;
+// At head_dim 64 a group is half the bytes: 3 in flight (178-199 VGPRs,
+// still two waves per SIMD) took the stream-K kernel 7-9% faster on group
+// sizes 4-8 (graph replays, B8-B128, 1-8K tokens); 4 was slower than 3.  At
+// head_dim 96 a third group measured no faster.
+constexpr int kPrefetch64 = 3;
 
 // Stream-K path limits: each wave scans all lengths, so the batch is capped.
 constexpr int kSkMaxBatch = 4096;
@@ -1984,7 +1986,7 @@ KernelFn pick_mfma_sk(int D, int nkv, bool wide) {
     }
   }
   switch (D) {
-    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch, 1, 0, FUSED, HOLD>;
+    case 64: return decode_mfma_sk_kernel<64, DT, kPrefetch64, 1, 0, FUSED, HOLD>;
     case 96: return decode_mfma_sk_kernel<96, DT, kPrefetch, 1, 0, FUSED, HOLD>;
     case 128: return decode_mfma_sk_kernel<128, DT, kPrefetch, 1, 0, FUSED, HOLD>;
     default: return decode_mfma_sk_kernel<256, DT, 2, 1, 0, FUSED, HOLD>;
