@@ -68,11 +68,13 @@ def parse():
                     help="--mode read: sets of waves taking alternate groups (2: twice the waves per CU)")
     ap.add_argument("--probe-work", type=int, default=0,
                     help="--mode read: dependent multiply-adds per group standing in for the decode math")
-    ap.add_argument("--op", choices=["decode", "kv_append", "mla", "sweep", "splits"], default="decode",
+    ap.add_argument("--op", choices=["decode", "kv_append", "mla", "sweep", "splits", "models"], default="decode",
                     help="kv_append: time the paged cache append on the config's shapes instead; "
                          "mla: time paged MLA decode (attention_amd.mla_decode) on --mla-config; "
                          "sweep: the reference's decode sweep (benchmarks/measure_decode.py:43-57); "
-                         "splits: the split layout by split count on the sweep's fp32 shapes")
+                         "splits: the split layout by split count on the sweep's fp32 shapes; "
+                         "models: the automatic path on common model shapes (MODEL_SHAPES)")
+    ap.add_argument("--model", default="", help="--op models: one shape of MODEL_SHAPES, in this process")
     ap.add_argument("--mla-config", default="mla-h128")
     ap.add_argument("--mla-kernel", choices=["auto", "wave", "staged"], default="auto",
                     help="--op mla: attention kernel of the timed attention stage (comparison)")
@@ -704,6 +706,89 @@ def sweep_mode(args) -> None:
           flush=True)
 
 
+# Decode shapes of common model families (q_heads, kv_heads, head_dim), bf16,
+# 16-token pages: the Hq/Hkv/D of each model's attention (the tensor-parallel
+# share where named), and the batch x context points they are timed at.
+MODEL_SHAPES = {
+    "llama3.2-1b": (32, 8, 64),
+    "qwen2.5-0.5b": (14, 2, 64),
+    "tinyllama-1.1b": (32, 4, 64),
+    "qwen2.5-7b": (28, 4, 128),
+    "mistral-7b": (32, 8, 128),
+    "llama2-7b": (32, 32, 128),
+    "llama3-70b-tp8": (8, 1, 128),
+    "gemma2-9b": (16, 8, 256),
+    "gemma2-2b": (8, 4, 256),
+    "phi3-mini": (32, 32, 96),
+    "qwen3-30b-a3b": (32, 4, 128),
+}
+MODEL_POINTS = ((32, 4096), (128, 1024), (8, 8192))
+
+
+def models_mode(args) -> None:
+    """The automatic path on the shapes of MODEL_SHAPES at MODEL_POINTS
+    (make_decode_case, bf16, P16, equal lengths): GPU time per call from graph
+    replays of the C entry point (graph_replay_us; 10 calls captured over K/V
+    pools rotated above 768 MB, so the Infinity Cache does not serve them),
+    algorithmic GB/s and the share of 8 TB/s.  Without --model, each shape
+    runs in a child process of its own (this process never touches the GPU):
+    in one process, a shape allocated after a larger one was freed measured
+    up to 25% slower.  One JSON line per point."""
+    if not args.model:
+        import subprocess
+        for name in MODEL_SHAPES:
+            res = subprocess.run([sys.executable, os.path.abspath(__file__), "--op", "models", "--model", name],
+                                 stdout=subprocess.PIPE, text=True, timeout=300)
+            sys.stdout.write(res.stdout)
+            sys.stdout.flush()
+            if res.returncode != 0:
+                raise SystemExit(f"--op models --model {name} failed ({res.returncode})")
+        return
+    from attention_amd import cabi
+    from attention_amd.cases import algorithmic_bytes, make_decode_case
+
+    if args.model not in MODEL_SHAPES:
+        raise SystemExit(f"--model: one of {', '.join(MODEL_SHAPES)}")
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    hq, hkv, d = MODEL_SHAPES[args.model]
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    dt = torch.bfloat16
+    for batch, length in MODEL_POINTS:
+        q, k, v, table, lens = make_decode_case(lengths=[length] * batch, q_heads=hq, kv_heads=hkv, head_dim=d,
+                                                block_size=16, dtype=dt, device=dev)
+        kv_bytes = 2 * k.numel() * k.element_size()
+        pools = max(1, math.ceil(768e6 / kv_bytes))
+        ks, vs = [k], [v]
+        for i in range(1, pools):
+            ks.append(k.roll(i, dims=0).contiguous())
+            vs.append(v.roll(i, dims=0).contiguous())
+        maxp = table.shape[1]
+        kind, waves, _, _ = cabi.auto_info(batch, hq, hkv, d, 16, maxp, cabi.DTYPE[dt])
+        ws = cabi.auto_workspace(batch, hq, hkv, d, 16, maxp, cabi.DTYPE[dt], dev)
+        out = torch.empty_like(q)
+        turn = [0]
+
+        def enqueue():
+            i = turn[0] % pools
+            turn[0] += 1
+            rc = cabi.auto_launch(q, ks[i], vs[i], table, lens, out, scale=1 / math.sqrt(d), workspace=ws,
+                                  stream=torch.cuda.current_stream(dev).cuda_stream)
+            if rc:
+                raise RuntimeError(cabi.error_string(rc))
+
+        us = graph_replay_us(enqueue, stream)
+        nb = algorithmic_bytes([length] * batch, batch, hq, hkv, d, 16, 2)
+        print(json.dumps({"model": args.model, "q_heads": hq, "kv_heads": hkv, "head_dim": d, "batch": batch,
+                          "len": length, "path": "balanced MFMA + merge" if kind >= 1 else "split layout",
+                          "waves": waves if kind >= 1 else None, "pools": pools, "gpu_us": round(us, 2),
+                          "gbs": round(nb / us / 1e3, 1), "pct_of_8tbs": round(nb / us / 8e4, 1),
+                          "mb": round(nb / 1e6, 1)}), flush=True)
+        del q, k, v, table, lens, ks, vs, ws, out
+        torch.cuda.empty_cache()
+
+
 def splits_mode(args) -> None:
     """The split layout (decode_generic_kernel + the split merge) by split
     count, on fp32 shapes of the reference's sweep (Hq32/Hkv8/D128/P16,
@@ -903,6 +988,9 @@ def main() -> None:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the decode path is "
               "measured on one MI355X and multi-GPU sharding is design-only.", file=sys.stderr)
         sys.exit(2)
+    if args.op == "models":
+        models_mode(args)  # the parent starts one child per shape and never touches the GPU
+        return
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
