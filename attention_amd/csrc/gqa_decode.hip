@@ -443,11 +443,11 @@ struct GroupBuf {
 // Load c, lane l reads the 16-byte piece 64c + l of the group's 16 rows in
 // row order: row (64c + l) / kLanesPerRow, piece (64c + l) % kLanesPerRow.
 // At head_dim 96 (12 pieces per row) a load ends inside a row.
-template <int D>
+template <int D, int ES = 2>
 struct KTile {
-  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kRowBytes = ES * D;  // ES: bytes per element (4 for fp32 caches)
   static constexpr int kStride = kRowBytes + 32;
-  static constexpr int kLanesPerRow = kRowBytes / 16;  // 8, 12, 16, 32
+  static constexpr int kLanesPerRow = kRowBytes / 16;  // 8, 12, 16, 32 (16-bit), 16, 32 (fp32)
   static constexpr bool kWholeRows = 64 % kLanesPerRow == 0;
   static constexpr int kBytes = 16 * kStride;
   __device__ static int row(int c, int lane) {
@@ -888,6 +888,204 @@ struct MfmaWave {
   }
 };
 
+// One wave's decode state for one kv-head of an fp32 cache, on the matrix
+// cores in fp32 (v_mfma_f32_16x16x4_f32: fp32 products and sums, the
+// reference's arithmetic).  Lane l, r16 = l % 16, q4 = l / 16:
+//   QK  MFMA (c, e), c < D/16, e < 4, over dims 16c + 4*q4 + e:
+//       A = K      lane holds K[token r16][16c + 4*q4 + e] (16 bytes of row
+//                  r16 of the LDS tile per c: coalesced loads, transposed
+//                  through LDS as in MfmaWave)
+//       B = Q^T    lane holds Q[head r16][16c + 4*q4 + e]
+//       C = S^T    lane holds S[token 4*q4+i][head r16], i = 0..3 (the C
+//                  layout of every 16x16 MFMA, as in MfmaWave)
+//   PV  MFMA (d, c), d < D/16, c < 4: lane group q4's k index is token
+//       4*q4 + c, so
+//       B = P^T    is the lane's own weight of token 4*q4 + c (QK's C)
+//       A = V^T    lane holds V[token 4*q4+c][DV*r16 + d]: DV contiguous
+//                  floats of that row, 16 lanes reading the row whole
+//       C = O^T    lane holds O[head r16][DV*(4*q4+i) + d], MfmaWave's
+//                  accumulator layout, so its partial-row and staging
+//                  stores serve this wave unchanged.
+// The softmax is MfmaWave's (exact running max, base 2, scale folded in);
+// the weights enter the PV product unrounded.
+template <int D, int PF>
+struct MfmaWaveF32 : MfmaWave<D, QD_DTYPE_F32, PF, 1> {
+  static_assert(D == 64 || D == 128, "fp32 MFMA decode serves head_dim 64 and 128");
+  using Base = MfmaWave<D, QD_DTYPE_F32, PF, 1>;
+  using Tile = KTile<D, 4>;
+  static constexpr int KQ = D / 16;  // 16-byte pieces of K (per group) and of the query, per lane
+  static constexpr int DV = D / 16;
+  struct Buf {
+    u32x4 k[KQ];
+    VRow<2 * D> v[4];  // DV floats of rows 4*q4 + c
+    int tg;
+  };
+  u32x4 qf[KQ];
+
+  __device__ void begin_item(const DecodeParams& p, int b, int kvh0, int valid_tokens, int g_first) {
+    this->hcount = vhead_count(p, kvh0);
+    const bool head_ok = this->r16 < this->hcount;
+    this->trow = p.table + static_cast<int64_t>(b) * p.maxP;
+    this->wbase = g_first / (p.P >> 4);
+    this->tblv = (this->lane < p.maxP - this->wbase) ? this->trow[this->wbase + this->lane] : 0;
+    const char* qp = static_cast<const char*>(p.q) +
+                     (static_cast<int64_t>(b) * p.Hq + vhead_base(p, kvh0) + (head_ok ? this->r16 : 0)) * D * 4;
+#pragma unroll
+    for (int c = 0; c < KQ; ++c) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(qp + 64 * c + 16 * this->q4);
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      qf[c] = head_ok ? x : zero;
+    }
+    this->m_run[0] = -INFINITY;
+    this->l_run[0] = 0.f;
+#pragma unroll
+    for (int d = 0; d < DV; ++d) this->acc[0][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int64_t col = p.kv_split > 1 ? kvh0 / p.kv_split : kvh0;
+    this->kbase = static_cast<const char*>(p.k) + col * D * 4;
+    this->vbase = static_cast<const char*>(p.v) + col * D * 4;
+    this->len = valid_tokens;
+  }
+
+  // Issues the K/V loads of group gi, as MfmaWave::issue.
+  __device__ void issue(const DecodeParams& p, Buf& buf, int gi) {
+    const int gpp = p.P >> 4;
+    const int tg = 16 * gi;
+    buf.tg = tg;
+    const int pl = gi / gpp;
+    const int row0 = 16 * (gi - pl * gpp);
+    const int phys = clamp_page(__builtin_amdgcn_readlane(this->tblv, pl - this->wbase), p.num_blocks);
+    const int64_t row_bytes = static_cast<int64_t>(p.kv_rows) * D * 4;
+    const int64_t off = (static_cast<int64_t>(phys) * p.P + row0) * row_bytes;
+    const char* kp = this->kbase + off;
+    const char* vp = this->vbase + off;
+    const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
+    const int last = this->len - 1 - tg;
+#pragma unroll
+    for (int c = 0; c < KQ; ++c) {
+      const uint32_t rk = static_cast<uint32_t>(min(Tile::row(c, this->lane), last));
+      buf.k[c] = stream_load16(kp + rk * rb32 + Tile::col_bytes(c, this->lane));
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t rv = static_cast<uint32_t>(min(4 * this->q4 + c, last));
+      buf.v[c] = load_vrow<2 * D>(vp + rv * rb32 + 4 * DV * this->r16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  __device__ void compute(const DecodeParams& p, const Buf& buf, char* ktile) {
+    const int last = this->len - 1 - buf.tg;
+#pragma unroll
+    for (int c = 0; c < KQ; ++c)
+      *reinterpret_cast<u32x4*>(ktile + Tile::row(c, this->lane) * Tile::kStride + Tile::col_bytes(c, this->lane)) =
+          buf.k[c];
+    u32x4 ka[KQ];
+#pragma unroll
+    for (int c = 0; c < KQ; ++c)
+      ka[c] = *reinterpret_cast<const u32x4*>(ktile + this->r16 * Tile::kStride + 64 * c + 16 * this->q4);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KQ; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        s = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(ka[c][e]), __uint_as_float(qf[c][e]), s, 0, 0, 0);
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (4 * this->q4 + i <= last) ? s[i] : -INFINITY;
+    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(this->m_run[0], mx * p.sl2);
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = fast_exp2(this->m_run[0] - mref);
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(fmaf(x[i], p.sl2, -mref));
+    this->l_run[0] = fmaf(this->l_run[0], alpha, (pr[0] + pr[1]) + (pr[2] + pr[3]));
+    this->m_run[0] = mn;
+    if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int d = 0; d < DV; ++d) this->acc[0][d] *= alpha;
+    }
+#pragma unroll
+    for (int d = 0; d < DV; ++d)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        this->acc[0][d] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(buf.v[c].w[d]), pr[c],
+                                                               this->acc[0][d], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // MfmaWave::run with this wave's issue and compute.
+  __device__ void run(const DecodeParams& p, int ga, int gb, char* ktile, bool lockstep = false) {
+    const int gpp = p.P >> 4;
+    for (int g_lo = ga; g_lo < gb;) {
+      if (g_lo != ga) {
+        this->wbase = g_lo / gpp;
+        this->tblv = (this->lane < p.maxP - this->wbase) ? this->trow[this->wbase + this->lane] : 0;
+      }
+      const int g_hi = min(gb, (this->wbase + 64) * gpp);
+      const int n = g_hi - g_lo;
+      Buf buf[PF];
+      int i = 0;
+      if (n >= 2 * PF - 1) {
+#pragma unroll
+        for (int u = 0; u < PF - 1; ++u) issue(p, buf[u], g_lo + u);
+        for (; i + 2 * PF - 2 < n; i += PF) {
+          if (lockstep) __builtin_amdgcn_s_barrier();
+#pragma unroll
+          for (int u = 0; u < PF; ++u) {
+            issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
+            compute(p, buf[u], ktile);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < PF - 1; ++u)
+          if (u < n) issue(p, buf[u], g_lo + u);
+      }
+      for (; i < n; i += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+          if (i + u + PF - 1 < n) issue(p, buf[(u + PF - 1) % PF], g_lo + i + u + PF - 1);
+          if (i + u < n) compute(p, buf[u], ktile);
+        }
+      }
+      g_lo = g_hi;
+    }
+  }
+
+  // Output rows in fp32: DV contiguous floats per (lane, i).
+  __device__ void store_direct(const DecodeParams& p, int b, int kvh0, int, float l_tot) {
+    if (this->r16 >= this->hcount) return;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    float* o = static_cast<float*>(p.out) + (static_cast<int64_t>(b) * p.Hq + vhead_base(p, kvh0) + this->r16) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float* dst = o + DV * (4 * this->q4 + i);
+#pragma unroll
+      for (int d = 0; d < DV; d += 4) {
+        f32x4 v;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = l_tot > 0.f ? this->acc[0][d + t][i] * inv : 0.f;
+        *reinterpret_cast<f32x4*>(dst + d) = v;
+      }
+    }
+  }
+
+  __device__ void stage_direct(const DecodeParams& p, char* area, int, float l_tot) {
+    if (this->r16 >= this->hcount) return;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    float* o = reinterpret_cast<float*>(area) + this->r16 * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float* dst = o + DV * (4 * this->q4 + i);
+#pragma unroll
+      for (int d = 0; d < DV; ++d) dst[d] = l_tot > 0.f ? this->acc[0][d][i] * inv : 0.f;
+    }
+  }
+};
+
 // VALU compute of the same per-wave pipeline, for comparison with the MFMA
 // one (head_dim 128, one kv-head per wave, at most GV heads per group).
 // Same loads, table windows and partition as MfmaWave; only the math
@@ -1277,9 +1475,10 @@ constexpr int kMaxWgWaves = 8;
 constexpr int kValuMaxWaves = QD_VALU_WAVES;
 constexpr int kValuPrefetch = QD_VALU_PF;
 
-template <int D, int NKV, int GV = 0, int PF = 2>
+template <int D, int NKV, int GV = 0, int PF = 2, int DT = QD_DTYPE_BF16>
 constexpr int sk_max_waves() {
   if (GV > 0) return kValuMaxWaves;
+  if (DT == QD_DTYPE_F32) return D <= 64 ? kMaxWgWaves : kMaxWgWaves / 2;  // fp32 head_dim 128: 512 registers
   return (NKV == 1 && D <= 128 && (PF <= 2 || D <= 64)) ? kMaxWgWaves : kMaxWgWaves / 2;
 }
 
@@ -1414,7 +1613,7 @@ __device__ __forceinline__ uint32_t arrive(const DecodeParams& p, int b, int kvh
 // nwg slots and resets the counter to zero.  No wave ever waits for
 // another, and the counters are left as they were found (zero).
 template <int D, int DT, int PF, int NKV, int GV = 0, bool FUSED = false, bool HOLD = false>
-__global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_mfma_sk_kernel(DecodeParams p) {
+__global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF, DT>())) void decode_mfma_sk_kernel(DecodeParams p) {
   static_assert(!(HOLD && (FUSED || GV > 0)), "results are held only by the MFMA kernel with the merge kernel");
   using S = typename Elem<DT>::S;
   const int lane = threadIdx.x & 63;
@@ -1423,7 +1622,8 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
   const int w = blockIdx.x;
   const int W = p.splits;
   const int B = p.B;
-  __shared__ __align__(16) char ktile[sk_max_waves<D, NKV, GV, PF>()][KTile<D>::kBytes];
+  static_assert(DT != QD_DTYPE_F32 || (NKV == 1 && GV == 0 && !FUSED), "fp32 caches: one kv-head per wave, merge kernel");
+  __shared__ __align__(16) char ktile[sk_max_waves<D, NKV, GV, PF, DT>()][KTile<D, DT == QD_DTYPE_F32 ? 4 : 2>::kBytes];
   QD_STAMP(p, 0, stamp_now());
   QD_STAMP(p, 8, stamp_clock());
   QD_STAMP(p, 6, stamp_xcc());
@@ -1534,7 +1734,10 @@ __global__ __launch_bounds__((64 * sk_max_waves<D, NKV, GV, PF>())) void decode_
   };
 
   // GV > 0: the VALU comparison variant (ValuWave, GV heads per group).
-  using Wave = std::conditional_t<GV == 0, MfmaWave<D, DT, PF, NKV>, ValuWave<D, DT, PF, (GV > 0 ? GV : 4)>>;
+  using Wave = std::conditional_t<
+      GV == 0,
+      std::conditional_t<DT == QD_DTYPE_F32, MfmaWaveF32<D, PF>, MfmaWave<D, DT, PF, NKV>>,
+      ValuWave<D, DT, PF, (GV > 0 ? GV : 4)>>;
   Wave wv;
   wv.init_lane();
   const int64_t slot_floats = static_cast<int64_t>(p.Hq) * (D + 2);
@@ -1896,6 +2099,26 @@ bool same_sizes(const qd_tensor_desc* a, const qd_tensor_desc* b) {
 
 constexpr int kMfmaHeads = 16;
 
+// fp32 caches on the balanced path (MfmaWaveF32): head_dim 64 or 128, whole
+// 16-token groups per page, at most 16 q-heads per kv-head, and a batch whose
+// static capacity (batch * max_pages * block_size) is at least
+// kF32SkTokens.  Graph replays on the reference's fp32 sweep shape (Hq32/Hkv8)
+// against the split layout: head_dim 64 B16/L4096 78.1 -> 49.7 us, head_dim
+// 128 B16/L4096 98.6 -> 93.5 and B32/L4096 184.4 -> 167.7 us; below that
+// capacity the split layout's single launch was faster (head_dim 128 B1/L128
+// 10.9 against 15.6 us, B4/L4096 34.2 against 38.7, B16/L1024 34.1 against
+// 39.3; head_dim 64 B4/L1024 12.5 against 14.1).  At head_dim 128 a wave
+// holds 32 KB of K/V per group in flight and runs one per SIMD; one group in
+// flight at two waves per SIMD, or K loaded straight in the MFMA layout,
+// measured slower.
+constexpr int64_t kF32SkTokens = 65536;
+
+bool f32_sk_applies(int batch, int q_heads, int kv_heads, int head_dim, int block_size, int max_pages, int dtype) {
+  if (dtype != QD_DTYPE_F32 || (head_dim != 64 && head_dim != 128) || block_size % 16 != 0) return false;
+  if (static_cast<int64_t>(batch) * max_pages * block_size < kF32SkTokens) return false;
+  return kv_heads > 0 && q_heads % kv_heads == 0 && q_heads / kv_heads <= kMfmaHeads;
+}
+
 bool mfma_applies(int q_heads, int kv_heads, int head_dim, int block_size, int dtype) {
   if (dtype != QD_DTYPE_F16 && dtype != QD_DTYPE_BF16) return false;
   if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256) return false;
@@ -1997,6 +2220,13 @@ KernelFn pick_mfma_sk(int D, int nkv, bool wide) {
 // in LDS until its range ends (never both).
 KernelFn pick_mfma_sk_dt(int dtype, int D, int nkv, bool wide = false, bool fused = false, bool hold = false) {
   const bool f16 = dtype == QD_DTYPE_F16;
+  if (dtype == QD_DTYPE_F32) {  // f32_sk_applies: head_dim 64 or 128, one kv-head per wave, never fused
+    if (D == 64)
+      return hold ? decode_mfma_sk_kernel<64, QD_DTYPE_F32, kPrefetch, 1, 0, false, true>
+                  : decode_mfma_sk_kernel<64, QD_DTYPE_F32, kPrefetch, 1, 0, false, false>;
+    return hold ? decode_mfma_sk_kernel<128, QD_DTYPE_F32, kPrefetch, 1, 0, false, true>
+                : decode_mfma_sk_kernel<128, QD_DTYPE_F32, kPrefetch, 1, 0, false, false>;
+  }
   if (fused)
     return f16 ? pick_mfma_sk<QD_DTYPE_F16, true, false>(D, nkv, wide)
                : pick_mfma_sk<QD_DTYPE_BF16, true, false>(D, nkv, wide);
@@ -2047,6 +2277,11 @@ bool merge_one_head_per_wave(int batch, int q_heads) {
 }
 
 KernelFn pick_merge_sk_dt(int dtype, int D, bool one_head) {
+  if (dtype == QD_DTYPE_F32) {
+    if (one_head)
+      return D == 64 ? merge_sk_kernel<64, QD_DTYPE_F32, 16, 4> : merge_sk_kernel<128, QD_DTYPE_F32, 16, 4>;
+    return D == 64 ? merge_sk_kernel<64, QD_DTYPE_F32, 8, 1> : merge_sk_kernel<128, QD_DTYPE_F32, 8, 1>;
+  }
   if (one_head)
     return dtype == QD_DTYPE_F16 ? pick_merge_sk<QD_DTYPE_F16, 16, 4>(D)
                                  : pick_merge_sk<QD_DTYPE_BF16, 16, 4>(D);
@@ -2310,11 +2545,16 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
   const int split = kv_split_for(q_heads, kv_heads);
   const int vkv = kv_heads * (split > 0 ? split : 1);  // kv-heads as the stream-K kernel serves them
   const int gv = split > 0 ? kv_chunk_heads(q_heads, kv_heads, split) : 0;  // q-heads per one of them, at most
-  if (aligned && split > 0 && (split == 1 || !valu) && mfma_applies(vkv * gv, vkv, head_dim, block_size, dtype) &&
+  const bool f32 = dtype == QD_DTYPE_F32;
+  if (aligned && split > 0 && (split == 1 || !valu) &&
+      (f32 ? !valu && f32_sk_applies(batch, q_heads, kv_heads, head_dim, block_size, max_pages, dtype)
+           : mfma_applies(vkv * gv, vkv, head_dim, block_size, dtype)) &&
       batch <= kSkMaxBatch) {
     int nkv = 1;
-    const bool wide = !valu && sk_wide_applies(vkv, head_dim);
-    int nw = sk_wg_waves(vkv, nkv, head_dim, valu, wide);
+    const bool wide = !valu && !f32 && sk_wide_applies(vkv, head_dim);
+    // fp32 at head_dim 128 holds 64 KB of K/V per group in flight: one wave
+    // per SIMD (the 4-wave cap of the wide layout).
+    int nw = sk_wg_waves(vkv, nkv, head_dim, valu, wide || (f32 && head_dim > 64));
     // The chunks of one kv-head in one pass of the workgroup's waves.
     for (int n = nw; split > 1 && n >= split; --n) {
       if (vkv % n == 0 && n % split == 0) {
@@ -2325,7 +2565,7 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     const int g = gv;
     KernelFn fn = valu ? pick_valu_sk_dt(dtype, g) : pick_mfma_sk_dt(dtype, head_dim, nkv, wide);
     int resident = resident_blocks(fn, 64 * nw);
-    if (!valu && split == 1 && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
+    if (!valu && !f32 && split == 1 && sk_dual_applies(batch, kv_heads, head_dim, block_size, max_pages, resident)) {
       nkv = 2;
       nw = sk_wg_waves(kv_heads, nkv, head_dim);
       fn = pick_mfma_sk_dt(dtype, head_dim, nkv);
@@ -2738,10 +2978,10 @@ int qd_gqa_decode_auto_stages(const void* q, const void* k_cache, const void* v_
   bool fused = ap.fused;
   if (unfused) fused = false;
   if (force_fused) {
-    if (valu || ap.kv_split > 1 || !fused_fits(batch, q_heads, kv_heads, head_dim, ap.wgs) ||
+    if (valu || dtype == QD_DTYPE_F32 || ap.kv_split > 1 || !fused_fits(batch, q_heads, kv_heads, head_dim, ap.wgs) ||
         ap.stash_bytes > kFusedMaxStash ||
         !allow_dyn_lds(pick_mfma_sk_dt(dtype, head_dim, ap.kv_per_wave, ap.wide, true)))
-      return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_FUSED needs MFMA math, at most 16 q-heads per kv-head, "
+      return fail(QD_ERR_INVALID_VALUE, "QD_STAGE_FUSED needs 16-bit MFMA math, at most 16 q-heads per kv-head, "
                                         "batch * kv_heads <= 65536 and partial slots below 2 GiB");
     fused = true;
   }

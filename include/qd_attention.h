@@ -147,7 +147,10 @@ int qd_gqa_decode_kernel_kind(int q_heads, int kv_heads, int head_dim, int block
  * kernel occupancy), never from context_lens on the host:
  *   - 16-bit caches with head_dim 64/96/128/256, block_size a multiple of 16,
  *     group size <= 128 (a group above 16 is served as ceil(g/16) chunks of
- *     at most 16 q-heads, each like a kv-head of its own) and batch <= 4096:
+ *     at most 16 q-heads, each like a kv-head of its own) and batch <= 4096,
+ *     and fp32 caches with head_dim 64/128, block_size a multiple of 16,
+ *     group size <= 16 and batch * max_pages * block_size >= 65536 (fp32
+ *     matrix-core products):
  *     the (sequence, 16-token group)
  *     space is cut into cost-balanced ranges, one per resident workgroup;
  *     a sequence split across workgroups leaves one partial per workgroup,

@@ -324,10 +324,29 @@ def test_auto_plan_for_configs(name):
 
 
 def test_auto_plan_falls_back_to_splits():
-    # fp32 caches take the split layout with the split plan.
-    kind, waves, splits, chunk = cabi.auto_info(32, 32, 8, 128, 16, 256, F32)
-    assert (kind, waves) == (0, 0) and (splits, chunk) == cabi.plan(32, 32, 8, 128, 16, 256)
+    # fp32 caches at head dims other than 64 and 128, or with pages that do
+    # not hold whole 16-token groups, take the split layout with the split plan.
+    for d, p in [(100, 16), (256, 16), (128, 8)]:
+        kind, waves, splits, chunk = cabi.auto_info(32, 32, 8, d, p, 1024, F32)
+        assert (kind, waves) == (0, 0) and (splits, chunk) == cabi.plan(32, 32, 8, d, p, 1024), (d, p)
+    assert cabi.auto_info(32, 48, 2, 128, 16, 256, F32)[0] == 0   # more than 16 q-heads per kv-head
     assert cabi.auto_info(4, 8, 3, 64, 16, 4, F16)[0] == -1   # Hq % Hkv != 0
+
+
+def test_auto_plan_f32_balanced_path():
+    # fp32 caches at head_dim 64 and 128 take the balanced kernel on the fp32
+    # matrix cores once the batch's static capacity (B * max_pages * P) is
+    # 65536 tokens: 8-wave workgroups at 64, 4-wave ones (one wave per SIMD)
+    # at 128, so the wave count is a multiple of the workgroup's.
+    k64 = cabi.auto_info(32, 32, 8, 64, 16, 256, F32)
+    k128 = cabi.auto_info(32, 32, 8, 128, 16, 256, F32)
+    assert k64[0] == 1 and k64[1] % 8 == 0 and k64[1] > 0
+    assert k128[0] == 1 and k128[1] % 4 == 0 and k128[1] > 0
+    assert cabi.auto_info(4, 8, 2, 128, 32, 512, F32)[0] == 1    # 32-token pages
+    assert cabi.auto_info(4, 16, 1, 128, 16, 1024, F32)[0] == 1  # 16 q-heads per kv-head
+    # One token short of the capacity: the split layout.
+    assert cabi.auto_info(4, 16, 1, 128, 16, 1023, F32)[0] == 0
+    assert cabi.auto_info(16, 32, 8, 128, 16, 64, F32)[0] == 0
 
 
 def test_auto_waves_per_workgroup_divide_kv_heads():

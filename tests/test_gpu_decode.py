@@ -129,8 +129,12 @@ SHAPES = [
     (torch.float16, 12, 4, 17, 5, [3, 19, 64]),
     (torch.bfloat16, 4, 4, 1, 1, [1, 2, 9]),
     (torch.float16, 64, 8, 128, 16, [2000, 1]),
-    (torch.bfloat16, 32, 32, 96, 16, [1, 300, 2049]),    # head_dim 96 (K in the A layout, 12-byte V rows)
+    (torch.bfloat16, 32, 32, 96, 16, [1, 300, 2049]),    # head_dim 96 (loads ending inside a K row, 12-byte V rows)
     (torch.float16, 32, 8, 96, 32, [17, 1000, 0, 33]),
+    # fp32 on the balanced path (fp32 MFMA; B * max_pages * P >= 65536): head_dim 64
+    # on 32-token pages, a group of 16
+    (torch.float32, 16, 4, 64, 32, [17, 1000, 0, 16400]),
+    (torch.float32, 16, 1, 128, 16, [1, 700, 33, 16384]),
 ]
 
 
@@ -525,6 +529,9 @@ def test_shapes_auto_cabi(gpu, shape):
     kind, waves, splits, chunk = cabi.auto_info(len(lengths), hq, hkv, d, p,
                                                 max(1, -(-max(lengths) // p)), cabi.DTYPE[dtype])
     say(f"auto shape {shape[1:5]} {DT_NAME[dtype]} kind={kind} waves={waves} splits={splits}")
+    if dtype == torch.float32 and d in (64, 128) and p % 16 == 0 and hq // hkv <= 16:
+        # fp32 takes the balanced (fp32 MFMA) path exactly when the capacity reaches 65536 tokens
+        assert (kind == 1) == (len(lengths) * -(-max(lengths) // p) * p >= 65536), kind
     case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d,
                                    block_size=p, dtype=dtype, seed=8), gpu)
     q, k, v, table, lens = case
@@ -612,12 +619,16 @@ def test_auto_tiny_items(gpu, lengths):
     # four heads per wave (B*Hq > 2048); about 28 workgroups per sequence,
     # more than one 8-row round trip per head
     (torch.float16, 256, 16, 64, 16, [3000, 2900, 3100, 2999, 3001, 17, 2800, 3050, 2950]),
-], ids=["one-head-many-rows", "four-heads-many-rows"])
+    # fp32 output rows from both merge layouts
+    (torch.float32, 8, 2, 128, 16, [65600]),
+    (torch.float32, 256, 16, 64, 16, [8000, 1100, 1000, 17, 800, 950, 1, 1020, 990]),
+], ids=["one-head-many-rows", "four-heads-many-rows", "f32-one-head", "f32-four-heads"])
 def test_auto_merge_layouts(gpu, shape):
     dt, hq, hkv, d, p, lengths = shape
     say(f"merge layouts: {DT_NAME[dt]} Hq{hq} Hkv{hkv} D{d} lengths {lengths[:3]}... (B={len(lengths)})")
     case = to_dev(make_decode_case(lengths=lengths, q_heads=hq, kv_heads=hkv, head_dim=d, block_size=p,
                                    dtype=dt, seed=23, exact_pool=True), gpu)
+    assert cabi.auto_info(len(lengths), hq, hkv, d, p, case[3].shape[1], cabi.DTYPE[dt])[0] == 1
     ref, rows = oracle_rows(case)
     out = attention_amd.gqa_decode(*case)
     torch.cuda.synchronize()
@@ -898,6 +909,9 @@ HELD_LAYOUTS = [
     (32, 8, 128, torch.float16, 4, [3500] + _fused_lengths(299, 1, 100, 96)),
     # head_dim 96: 8 single-kv-head waves, 12-byte output pieces
     (32, 8, 96, torch.bfloat16, 8, _fused_lengths(300, 1, 200, 135)),
+    # fp32 caches: head_dim 128 with 4 waves (one per SIMD), head_dim 64 with 4 of up to 8
+    (32, 8, 128, torch.float32, 4, [240] + _fused_lengths(299, 1, 200, 136)),
+    (16, 4, 64, torch.float32, 4, _fused_lengths(600, 1, 300, 137)),
 ]
 
 
