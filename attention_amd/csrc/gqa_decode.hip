@@ -2585,8 +2585,14 @@ int auto_plan(int batch, int q_heads, int kv_heads, int head_dim, int block_size
     };
     int64_t w = grid(resident);
     // Result rows held in LDS until the range ends: the kernel's occupancy
-    // with that LDS sets the grid.
-    if (!valu && hold_results(batch, w)) {
+    // with that LDS sets the grid.  Not where each wave runs alone on its
+    // SIMD and serves a single kv-head per sequence (4 kv-heads at head_dim
+    // 128, head_dim 256 or fp32 head_dim 128 with at most 4 kv-heads): there
+    // the stores after each item measured faster (graph replays, B128/L1024:
+    // Qwen2.5-7B's shape 51.5 -> 47.2 us, Gemma-2-2B's 96.2 -> 87.4 us),
+    // while with two kv-heads per wave (Gemma-2-9B's shape) holding was level.
+    const bool one_per_simd = nkv == 1 && (wide || head_dim > 128 || (f32 && head_dim > 64));
+    if (!valu && !(one_per_simd && nw == vkv) && hold_results(batch, w)) {
       const KernelFn hfn = pick_mfma_sk_dt(dtype, head_dim, nkv, wide && nkv == 1, false, true);
       ap->stage_bytes = stage_lds_bytes(g, head_dim, nkv, nw);
       if (!allow_dyn_lds(hfn)) return fail(QD_ERR_INVALID_VALUE, "dynamic LDS limit not raised");

@@ -901,10 +901,9 @@ def test_held_results_flush_when_full(gpu, dtype):
 HELD_LAYOUTS = [
     # head_dim 64, 2 kv-heads: 2 single-kv-head waves per workgroup, several workgroups per CU
     (16, 2, 64, torch.float16, 2, _fused_lengths(1200, 1, 300, 93)),
-    # head_dim 256: 4 waves, one per SIMD
-    (16, 4, 256, torch.bfloat16, 4, _fused_lengths(300, 1, 200, 94)),
-    # 4 kv-heads at head_dim 128: one wave per SIMD, 3 groups in flight
-    (28, 4, 128, torch.bfloat16, 4, _fused_lengths(300, 1, 400, 95)),
+    # head_dim 256: 4 waves, one per SIMD, two kv-heads of a sequence per wave (with one
+    # kv-head per wave, as for 4 kv-heads at head_dim 128, the rows are stored after each item)
+    (16, 8, 256, torch.bfloat16, 4, _fused_lengths(300, 1, 200, 94)),
     # two kv-heads per wave: a wide table (one long sequence) among short ones
     (32, 8, 128, torch.float16, 4, [3500] + _fused_lengths(299, 1, 100, 96)),
     # head_dim 96: 8 single-kv-head waves, 12-byte output pieces
