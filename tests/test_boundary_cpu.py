@@ -379,6 +379,17 @@ def test_auto_argument_errors(over, msg):
     assert cabi.error_string(rc) == msg
 
 
+def test_auto_fused_stage_refused_for_f32():
+    # An fp32 plan on the balanced path (aligned pointers, capacity >= 65536
+    # tokens) refuses QD_STAGE_FUSED before anything is launched.
+    args = _auto_args(q=16, k=16, v=16, table=16, lens=16, out=16, ws=16, ws_bytes=1 << 30, B=16, Hq=32,
+                      Hkv=8, D=128, P=16, maxP=256, N=4096, dtype=F32, stages=cabi.QD_STAGE_ALL | cabi.QD_STAGE_FUSED)
+    assert cabi.auto_info(16, 32, 8, 128, 16, 256, F32)[0] == 1
+    rc = cabi.lib().qd_gqa_decode_auto_stages(*args)
+    assert rc == 1
+    assert cabi.error_string(rc).startswith("QD_STAGE_FUSED needs 16-bit MFMA math")
+
+
 def test_auto_batch_zero_is_a_no_op():
     assert cabi.lib().qd_gqa_decode_auto_stages(*_auto_args(B=0, q=None)) == 0
 
